@@ -1,0 +1,504 @@
+// capi.cpp -- the extern "C" entry points of libacfun_amd.so (include/acfun/acfun.h).
+//
+// Host-pointer entry points keep the reference's synchronous contract: host
+// operands are staged to pooled HBM buffers, the kernels run on the library
+// stream, results are copied back and the stream is synchronized before the
+// call returns.  Operands that already are device pointers are used in place.
+// Shape checks mirror the reference's silent early returns.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <unistd.h>
+
+#include "../../include/acfun/acfun.h"
+#include "rt.hpp"
+
+using namespace acfun;
+
+namespace acfun {
+
+// conv2d_impl of the reference (src/layers.cpp:106-195), route for route.
+bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float* w,
+                      const float* bias, int KH, int KW, int Cout, int stride, int pad, int groups,
+                      float* out, int act, hipStream_t s) {
+    if (groups > 1) {
+        if (groups == Cin && groups == Cout)  // :112-116
+            return dwconv_f32(in, N, H, W, Cin, w, bias, KH, KW, stride, pad, out, act, s);
+        int Cin_per = Cin / groups, Cout_per = Cout / groups;
+        int OH = (H + 2 * pad - KH) / stride + 1;
+        int OW = (W + 2 * pad - KW) / stride + 1;
+        if (OH <= 0 || OW <= 0) return true;
+        if (Cin_per <= 64 && Cout_per <= 128)  // :126-130
+            return gconv_f32(in, N, H, W, Cin, w, bias, KH, KW, Cout, stride, pad, groups, out, act, s);
+        // :134-153 -- each group through the dense routes on contiguous copies.
+        long long pin = (long long)N * H * W, pout = (long long)N * OH * OW;
+        Scratch ig((size_t)pin * Cin_per * sizeof(float), s);
+        Scratch og((size_t)pout * Cout_per * sizeof(float), s);
+        if (!ig.p || !og.p) return false;
+        for (int g = 0; g < groups; ++g) {
+            if (!group_split_copy(in, (int)pin, Cin, g * Cin_per, Cin_per, ig.as<float>(), Cin_per, 0, s))
+                return false;
+            if (!conv2d_route_f32(ig.as<float>(), N, H, W, Cin_per,
+                                  w + (size_t)g * Cout_per * KH * KW * Cin_per,
+                                  bias ? bias + g * Cout_per : nullptr, KH, KW, Cout_per, stride,
+                                  pad, 1, og.as<float>(), act, s))
+                return false;
+            if (!group_split_copy(og.as<float>(), (int)pout, Cout_per, 0, Cout_per, out, Cout,
+                                  g * Cout_per, s))
+                return false;
+        }
+        return true;
+    }
+    if (KH == 1 && KW == 1) {  // :157-160, conv1x1_impl (:66-101)
+        int OH = (H + 2 * pad - 1) / stride + 1;
+        int OW = (W + 2 * pad - 1) / stride + 1;
+        if (OH <= 0 || OW <= 0) return true;
+        ConvShape g{N, H, W, Cin, 1, 1, stride, pad, OH, OW};
+        return conv_igemm_f32(g, in, w, bias, Cout, out, act, s);
+    }
+    if (KH == 3 && KW == 3 && stride == 1 && pad == 1 && H >= 3 && W >= 3 && Cin >= 4 &&
+        Cout >= 4) {  // :169-176
+        int tile = (H >= 112 && W >= 112 && Cin >= 64 && Cout >= 64) ? 4 : 2;
+        return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    }
+    int OH = (H + 2 * pad - KH) / stride + 1;  // :178-194
+    int OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH <= 0 || OW <= 0) return true;
+    ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
+    return conv_igemm_f32(g, in, w, bias, Cout, out, act, s);
+}
+
+}  // namespace acfun
+
+namespace {
+
+int g_host_threads = 0;
+int g_rt_threads = 1;
+
+inline size_t F(long long n) { return (size_t)(n > 0 ? n : 0) * sizeof(float); }
+
+// Runs `body` with staged operands; returns after synchronizing.
+template <class Body>
+void host_call(Body body) {
+    if (!ensure_device()) return;
+    HostCall hc(lib_stream());
+    if (!body(hc)) {
+        hipStreamSynchronize(hc.stream());
+        return;
+    }
+    hc.finish();
+}
+
+int conv_out(int H, int K, int stride, int pad) { return (H + 2 * pad - K) / stride + 1; }
+
+}  // namespace
+
+extern "C" {
+
+// ------------------------------------------------------------------ runtime
+void acfun_set_threads(int n) { g_host_threads = n > 0 ? n : 0; }
+
+int acfun_backend(void) { return ensure_device() ? 4 : 0; }
+
+const char* acfun_backend_name(void) { return ensure_device() ? "MI355X-gfx950" : "none"; }
+
+void acfun_autotune(void) {
+    if (ensure_device()) autotune_run();
+}
+
+const char* acfun_tune_status(void) { return tune_status(); }
+
+const char* acfun_last_error(void) { return last_error(); }
+
+int acfun_sync(void) {
+    if (!ensure_device()) return -1;
+    return check(hipStreamSynchronize(lib_stream()), "acfun_sync") ? 0 : -1;
+}
+
+void acfun_set_num_threads_runtime(int n) { g_rt_threads = n > 0 ? n : 1; }
+int acfun_get_num_threads_runtime(void) { return g_rt_threads; }
+
+int acfun_effective_cores(void) {
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    int eff = n > 0 ? (int)n : 1;
+    FILE* f = fopen("/sys/fs/cgroup/cpu.max", "r");
+    if (f) {
+        char buf[64];
+        if (fgets(buf, sizeof(buf), f) && strncmp(buf, "max", 3) != 0) {
+            long long q = 0, p = 0;
+            if (sscanf(buf, "%lld %lld", &q, &p) == 2 && p > 0) {
+                long long c = (q + p - 1) / p;
+                if (c > 0 && c < eff) eff = (int)c;
+            }
+        }
+        fclose(f);
+    }
+    if (g_host_threads > 0 && g_host_threads < eff) eff = g_host_threads;
+    return eff;
+}
+
+// ------------------------------------------------------------------ GEMM
+void acfun_gemm_epi(int M, int N, int K, const float* A, const float* B, float* C,
+                    const float* bias, int act) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    host_call([&](HostCall& hc) {
+        auto dA = (const float*)hc.in(A, F((long long)M * K));
+        auto dB = (const float*)hc.in(B, F((long long)K * N));
+        auto db = (const float*)hc.in(bias, F(N));
+        auto dC = (float*)hc.out(C, F((long long)M * N));
+        if (hc.failed()) return false;
+        return gemm_f32(M, N, K, dA, K, dB, N, dC, N, db, act, hc.stream());
+    });
+}
+
+void acfun_gemm(int M, int N, int K, const float* A, const float* B, float* C) {
+    acfun_gemm_epi(M, N, K, A, B, C, nullptr, 0);
+}
+
+void acfun_gemm_bf16(int M, int N, int K, const float* A, const float* B, float* C) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    host_call([&](HostCall& hc) {
+        auto dA = (const float*)hc.in(A, F((long long)M * K));
+        auto dB = (const float*)hc.in(B, F((long long)K * N));
+        auto dC = (float*)hc.out(C, F((long long)M * N));
+        if (hc.failed()) return false;
+        Scratch a16(F((long long)M * K), hc.stream()), b16(F((long long)K * N), hc.stream());
+        if ((M * (long long)K && !a16.p) || (K * (long long)N && !b16.p)) return false;
+        return round_bf16(dA, a16.as<float>(), (size_t)M * K, hc.stream()) &&
+               round_bf16(dB, b16.as<float>(), (size_t)K * N, hc.stream()) &&
+               gemm_f32(M, N, K, a16.as<float>(), K, b16.as<float>(), N, dC, N, nullptr, 0,
+                        hc.stream());
+    });
+}
+
+// ------------------------------------------------------------------ conv
+static void conv_host(const float* input, int N, int H, int W, int Cin, const float* weight,
+                      const float* bias, int KH, int KW, int Cout, int stride, int pad, int groups,
+                      float* output, int act) {
+    if (N <= 0 || stride <= 0 || groups <= 0) return;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return;
+    long long wn = (long long)KH * KW * Cin * Cout / groups;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * Cin));
+        auto dw = (const float*)hc.in(weight, F(wn));
+        auto db = (const float*)hc.in(bias, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * Cout));
+        if (hc.failed()) return false;
+        return conv2d_route_f32(dx, N, H, W, Cin, dw, db, KH, KW, Cout, stride, pad, groups, dy,
+                                act, hc.stream());
+    });
+}
+
+void acfun_conv2d(const float* input, int N, int H, int W, int Cin, const float* weight,
+                  const float* bias, int KH, int KW, int Cout, int stride, int pad, float* output) {
+    conv_host(input, N, H, W, Cin, weight, bias, KH, KW, Cout, stride, pad, 1, output, 0);
+}
+
+void acfun_conv2d_relu(const float* input, int N, int H, int W, int Cin, const float* weight,
+                       const float* bias, int KH, int KW, int Cout, int stride, int pad,
+                       float* output) {
+    conv_host(input, N, H, W, Cin, weight, bias, KH, KW, Cout, stride, pad, 1, output, 1);
+}
+
+void acfun_conv2d_g(const float* input, int N, int H, int W, int Cin, const float* weight,
+                    const float* bias, int KH, int KW, int Cout, int stride, int pad, int groups,
+                    float* output, int act) {
+    conv_host(input, N, H, W, Cin, weight, bias, KH, KW, Cout, stride, pad,
+              groups > 1 ? groups : 1, output, act);
+}
+
+void acfun_conv2d_dw(const float* input, int N, int H, int W, int C, const float* weight,
+                     const float* bias, int KH, int KW, int stride, int pad, float* output,
+                     int act) {
+    if (KH <= 0 || KW <= 0 || N <= 0 || stride <= 0) return;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * C));
+        auto dw = (const float*)hc.in(weight, F((long long)C * KH * KW));
+        auto db = (const float*)hc.in(bias, F(C));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * C));
+        if (hc.failed()) return false;
+        return dwconv_f32(dx, N, H, W, C, dw, db, KH, KW, stride, pad, dy, act, hc.stream());
+    });
+}
+
+void acfun_conv2d_grouped(const float* input, int N, int H, int W, int Cin, const float* weight,
+                          const float* bias, int KH, int KW, int Cout, int stride, int pad,
+                          int groups, float* output, int act) {
+    if (groups <= 1 || KH <= 0 || KW <= 0 || N <= 0 || stride <= 0) return;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return;
+    long long wn = (long long)KH * KW * Cin * Cout / groups;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * Cin));
+        auto dw = (const float*)hc.in(weight, F(wn));
+        auto db = (const float*)hc.in(bias, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * Cout));
+        if (hc.failed()) return false;
+        return gconv_f32(dx, N, H, W, Cin, dw, db, KH, KW, Cout, stride, pad, groups, dy, act,
+                         hc.stream());
+    });
+}
+
+static void wino_host(int tile, const float* input, int N, int H, int W, int Cin,
+                      const float* weight, const float* bias, int Cout, float* output, int act) {
+    if (N <= 0 || H <= 0 || W <= 0 || Cin <= 0 || Cout <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * Cin));
+        auto dw = (const float*)hc.in(weight, F(9LL * Cin * Cout));
+        auto db = (const float*)hc.in(bias, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * H * W * Cout));
+        if (hc.failed()) return false;
+        return winograd_f32(tile, dx, N, H, W, Cin, dw, db, Cout, dy, act, hc.stream());
+    });
+}
+
+void acfun_winograd_conv3x3(const float* input, int N, int H, int W, int Cin, const float* weight,
+                            const float* bias, int Cout, float* output, int act) {
+    wino_host(2, input, N, H, W, Cin, weight, bias, Cout, output, act);
+}
+
+void acfun_winograd43_conv3x3(const float* input, int N, int H, int W, int Cin,
+                              const float* weight, const float* bias, int Cout, float* output,
+                              int act) {
+    wino_host(4, input, N, H, W, Cin, weight, bias, Cout, output, act);
+}
+
+// ------------------------------------------------------------------ FC
+void acfun_fc(const float* input, int N, int Cin, const float* weight, const float* bias, int Cout,
+              float* output) {
+    acfun_gemm_epi(N, Cout, Cin, input, weight, output, bias, 0);
+}
+
+void acfun_fc_relu(const float* input, int N, int Cin, const float* weight, const float* bias,
+                   int Cout, float* output) {
+    acfun_gemm_epi(N, Cout, Cin, input, weight, output, bias, 1);
+}
+
+// ------------------------------------------------------------------ elementwise
+void acfun_relu(float* data, size_t len) {
+    if (!len) return;
+    host_call([&](HostCall& hc) {
+        auto d = (float*)hc.inout(data, len * sizeof(float));
+        if (hc.failed()) return false;
+        return relu_f32(d, len, 0, hc.stream());
+    });
+}
+
+void acfun_relu6(float* data, size_t len) {
+    if (!len) return;
+    host_call([&](HostCall& hc) {
+        auto d = (float*)hc.inout(data, len * sizeof(float));
+        if (hc.failed()) return false;
+        return relu_f32(d, len, 1, hc.stream());
+    });
+}
+
+static void maxpool_host(const float* input, int N, int H, int W, int C, int pool, int stride,
+                         int pad, float* output, int post_relu) {
+    if (N <= 0 || C <= 0 || stride <= 0) return;
+    int OH = conv_out(H, pool, stride, pad), OW = conv_out(W, pool, stride, pad);
+    if (OH <= 0 || OW <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * C));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * C));
+        if (hc.failed()) return false;
+        return maxpool_f32(dx, N, H, W, C, pool, stride, pad, dy, post_relu, hc.stream());
+    });
+}
+
+void acfun_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride, int pad,
+                   float* output) {
+    maxpool_host(input, N, H, W, C, pool, stride, pad, output, 0);
+}
+
+void acfun_maxpool_relu(const float* input, int N, int H, int W, int C, int pool, int stride,
+                        int pad, float* output) {
+    maxpool_host(input, N, H, W, C, pool, stride, pad, output, 1);
+}
+
+void acfun_softmax(const float* input, int rows, int cols, float* output) {
+    if (rows <= 0 || cols <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)rows * cols));
+        auto dy = (float*)hc.out(output, F((long long)rows * cols));
+        if (hc.failed()) return false;
+        return softmax_f32(dx, rows, cols, dy, hc.stream());
+    });
+}
+
+void acfun_batchnorm(float* data, int size, int channels, const float* mean, const float* var,
+                     const float* gamma, const float* beta, float eps) {
+    if (size <= 0 || channels <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto d = (float*)hc.inout(data, F((long long)(size / channels) * channels));
+        auto dm = (const float*)hc.in(mean, F(channels));
+        auto dv = (const float*)hc.in(var, F(channels));
+        auto dg = (const float*)hc.in(gamma, F(channels));
+        auto dbt = (const float*)hc.in(beta, F(channels));
+        if (hc.failed()) return false;
+        return batchnorm_f32(d, size, channels, dm, dv, dg, dbt, eps, hc.stream());
+    });
+}
+
+// ------------------------------------------------------------------ int8
+void acfun_quantize_weights(const float* w, int K, int N, float* scales, int8_t* wq) {
+    if (K <= 0 || N <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dw = (const float*)hc.in(w, F((long long)K * N));
+        auto ds = (float*)hc.out(scales, F(N));
+        auto dq = (int8_t*)hc.out(wq, (size_t)K * N);
+        if (hc.failed()) return false;
+        return quantize_weights_dev(dw, K, N, ds, dq, hc.stream());
+    });
+}
+
+void acfun_conv2d_int8(const float* input, int N, int H, int W, int Cin, const int8_t* wq,
+                       const float* wscale, const float* bias, int KH, int KW, int Cout,
+                       int stride, int pad, float s_in, float* output, int act) {
+    (void)s_in;  // ignored, as in src/conv_int8.cpp:63-81
+    if (N <= 0 || stride <= 0) return;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * Cin));
+        auto dq = (const int8_t*)hc.in(wq, (size_t)KH * KW * Cin * Cout);
+        auto ds = (const float*)hc.in(wscale, F(Cout));
+        auto db = (const float*)hc.in(bias, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * Cout));
+        if (hc.failed()) return false;
+        ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
+        return conv2d_int8_dev(dx, g, dq, ds, db, Cout, dy, act, hc.stream());
+    });
+}
+
+void acfun_gemm_int8(int M, int N, int K, const uint8_t* A, const int8_t* B, int32_t* C) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    host_call([&](HostCall& hc) {
+        auto dA = (const uint8_t*)hc.in(A, (size_t)M * K);
+        auto dB = (const int8_t*)hc.in(B, (size_t)K * N);
+        auto dC = (int32_t*)hc.out(C, (size_t)M * N * sizeof(int32_t));
+        if (hc.failed()) return false;
+        return gemm_int8_dev(M, N, K, dA, dB, dC, nullptr, nullptr, nullptr, 0, hc.stream());
+    });
+}
+
+void acfun_gemm_int8_epi(int M, int N, int K, const uint8_t* A, const int8_t* B, float* C,
+                         const float* alpha, const float* beta, int act) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    host_call([&](HostCall& hc) {
+        auto dA = (const uint8_t*)hc.in(A, (size_t)M * K);
+        auto dB = (const int8_t*)hc.in(B, (size_t)K * N);
+        auto da = (const float*)hc.in(alpha, F(N));
+        auto db = (const float*)hc.in(beta, F(N));
+        auto dC = (float*)hc.out(C, F((long long)M * N));
+        if (hc.failed()) return false;
+        return gemm_int8_dev(M, N, K, dA, dB, nullptr, da, db, dC, act, hc.stream());
+    });
+}
+
+void acfun_quantize_u8(const float* in, uint8_t* out, size_t n, float inv_s, int zp) {
+    if (!n) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(in, n * sizeof(float));
+        auto dy = (uint8_t*)hc.out(out, n);
+        if (hc.failed()) return false;
+        return quantize_u8_dev(dx, dy, n, inv_s, zp, hc.stream());
+    });
+}
+
+void acfun_conv2d_int8_direct(const uint8_t* inQ, int N, int H, int W, int Cin, const int8_t* wq,
+                              const float* alpha, const float* beta, int KH, int KW, int Cout,
+                              int stride, int pad, int OH, int OW, float* output, int act) {
+    if (N <= 0 || OH <= 0 || OW <= 0 || Cout <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const uint8_t*)hc.in(inQ, (size_t)N * H * W * Cin);
+        auto dq = (const int8_t*)hc.in(wq, (size_t)KH * KW * Cin * Cout);
+        auto da = (const float*)hc.in(alpha, F(Cout));
+        auto db = (const float*)hc.in(beta, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * OH * OW * Cout));
+        if (hc.failed()) return false;
+        ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
+        return conv_int8_direct_dev(dx, g, dq, da, db, Cout, dy, act, hc.stream());
+    });
+}
+
+void acfun_conv1x1_int8(const uint8_t* inQ, int M, int K, int Cout, const int8_t* wq,
+                        const float* alpha, const float* beta, float* output, int act) {
+    if (M <= 0 || Cout <= 0 || K < 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const uint8_t*)hc.in(inQ, (size_t)M * K);
+        auto dq = (const int8_t*)hc.in(wq, (size_t)K * Cout);
+        auto da = (const float*)hc.in(alpha, F(Cout));
+        auto db = (const float*)hc.in(beta, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)M * Cout));
+        if (hc.failed()) return false;
+        return conv1x1_int8_dev(dx, M, K, Cout, dq, da, db, dy, act, hc.stream());
+    });
+}
+
+void acfun_winograd_conv3x3_int8(const float* input, int N, int H, int W, int Cin,
+                                 const int8_t* wq, const float* wscale, const float* bias,
+                                 int Cout, float s_in, float inv_s, float* output, int act) {
+    if (N <= 0 || H <= 0 || W <= 0 || Cin <= 0 || Cout <= 0) return;
+    host_call([&](HostCall& hc) {
+        auto dx = (const float*)hc.in(input, F((long long)N * H * W * Cin));
+        auto dq = (const int8_t*)hc.in(wq, (size_t)9 * Cin * Cout);
+        auto ds = (const float*)hc.in(wscale, F(Cout));
+        auto db = (const float*)hc.in(bias, F(Cout));
+        auto dy = (float*)hc.out(output, F((long long)N * H * W * Cout));
+        if (hc.failed()) return false;
+        return winograd_int8_dev(dx, N, H, W, Cin, dq, ds, db, Cout, s_in, inv_s, dy, act,
+                                 hc.stream());
+    });
+}
+
+// ------------------------------------------------------------------ device variants
+int acfun_dev_gemm_epi(int M, int N, int K, const float* A, const float* B, float* C,
+                       const float* bias, int act, void* stream) {
+    if (!ensure_device()) return -1;
+    if (M <= 0 || N <= 0 || K < 0) return 0;
+    return gemm_f32(M, N, K, A, K, B, N, C, N, bias, act, resolve(stream)) ? 0 : -1;
+}
+
+int acfun_dev_conv2d(const float* input, int N, int H, int W, int Cin, const float* weight,
+                     const float* bias, int KH, int KW, int Cout, int stride, int pad, int groups,
+                     float* output, int act, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0) return 0;
+    return conv2d_route_f32(input, N, H, W, Cin, weight, bias, KH, KW, Cout, stride, pad,
+                            groups > 1 ? groups : 1, output, act, resolve(stream))
+               ? 0 : -1;
+}
+
+int acfun_dev_conv2d_int8(const float* input, int N, int H, int W, int Cin, const int8_t* wq,
+                          const float* wscale, const float* bias, int KH, int KW, int Cout,
+                          int stride, int pad, float* output, int act, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0) return 0;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return 0;
+    ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
+    return conv2d_int8_dev(input, g, wq, wscale, bias, Cout, output, act, resolve(stream)) ? 0 : -1;
+}
+
+int acfun_dev_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride, int pad,
+                      float* output, int post_relu, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0) return 0;
+    return maxpool_f32(input, N, H, W, C, pool, stride, pad, output, post_relu, resolve(stream)) ? 0 : -1;
+}
+
+int acfun_dev_fc(const float* input, int N, int Cin, const float* weight, const float* bias,
+                 int Cout, float* output, int act, void* stream) {
+    return acfun_dev_gemm_epi(N, Cout, Cin, input, weight, output, bias, act, stream);
+}
+
+int acfun_dev_softmax(const float* input, int rows, int cols, float* output, void* stream) {
+    if (!ensure_device()) return -1;
+    return softmax_f32(input, rows, cols, output, resolve(stream)) ? 0 : -1;
+}
+
+}  // extern "C"

@@ -1,0 +1,360 @@
+// k_light.hip -- bandwidth-bound kernels: depthwise conv, grouped conv,
+// MaxPool, ReLU/ReLU6, softmax, unfused BatchNorm and small copies.
+//
+// These move bytes, not FLOPs, so there is no MFMA here: every kernel maps one
+// lane to one output element with the channel index fastest, so a wavefront
+// reads and writes contiguous NHWC channel runs (coalesced HBM access).
+//
+// Rounding follows the reference's AVX-512 host paths operation for operation
+// (the library is built with -ffp-contract=off, fmaf is written where the
+// reference fuses), so results are bit-identical, not just close:
+//   depthwise  src/dw_avx512.cpp:20-69      bias, then fmaf per tap (kh,kw), OOB tap = 0
+//   grouped    src/group_conv.cpp:60-79     fmaf chain from bias over (kh,kw,ic) for the
+//                                           vector channels, mul+add for the scalar path
+//   maxpool    src/maxpool_avx512.cpp:15-62 max from -1e30 over in-range taps
+#include "rt.hpp"
+
+namespace acfun {
+namespace {
+
+__device__ __forceinline__ float vmax(float a, float b) { return a > b ? a : b; }  // max_ps
+
+// Depthwise conv: weights [C][KH][KW]; act==1 -> ReLU (max_ps semantics).
+__global__ void k_dwconv(const float* __restrict__ in, int N, int H, int W, int C,
+                         const float* __restrict__ w, const float* __restrict__ bias, int KH,
+                         int KW, int stride, int pad, int OH, int OW, float* __restrict__ out,
+                         int act) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)N * OH * OW * C;
+    if (idx >= total) return;
+    int c = (int)(idx % C);
+    long long p = idx / C;
+    int ow = (int)(p % OW);
+    p /= OW;
+    int oh = (int)(p % OH);
+    int n = (int)(p / OH);
+    const float* wc = w + (long long)c * KH * KW;
+    float acc = bias ? bias[c] : 0.0f;
+    const float* img = in + (long long)n * H * W * C + c;
+    for (int kh = 0; kh < KH; ++kh) {
+        int ih = oh * stride - pad + kh;
+        for (int kw = 0; kw < KW; ++kw) {
+            int iw = ow * stride - pad + kw;
+            float v = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? img[((long long)ih * W + iw) * C] : 0.0f;
+            acc = fmaf(v, wc[kh * KW + kw], acc);
+        }
+    }
+    if (act == 1) acc = vmax(acc, 0.0f);
+    out[idx] = acc;
+}
+
+// Depthwise 3x3 for C % 4 == 0: one lane computes 4 channels with float4
+// loads (same per-channel arithmetic as k_dwconv).
+__global__ void k_dwconv3_c4(const float4* __restrict__ in, int N, int H, int W, int C4,
+                             const float* __restrict__ w, const float* __restrict__ bias,
+                             int stride, int pad, int OH, int OW, float4* __restrict__ out,
+                             int act) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)N * OH * OW * C4;
+    if (idx >= total) return;
+    int c4 = (int)(idx % C4);
+    long long p = idx / C4;
+    int ow = (int)(p % OW);
+    p /= OW;
+    int oh = (int)(p % OH);
+    int n = (int)(p / OH);
+    int c = c4 * 4;
+    float4 acc = bias ? make_float4(bias[c], bias[c + 1], bias[c + 2], bias[c + 3])
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4* img = in + (long long)n * H * W * C4 + c4;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+        int ih = oh * stride - pad + kh;
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+            int iw = ow * stride - pad + kw;
+            float4 v = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? img[((long long)ih * W + iw) * C4]
+                                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+            int t = kh * 3 + kw;
+            acc.x = fmaf(v.x, w[(c + 0) * 9 + t], acc.x);
+            acc.y = fmaf(v.y, w[(c + 1) * 9 + t], acc.y);
+            acc.z = fmaf(v.z, w[(c + 2) * 9 + t], acc.z);
+            acc.w = fmaf(v.w, w[(c + 3) * 9 + t], acc.w);
+        }
+    }
+    if (act == 1) {
+        acc.x = vmax(acc.x, 0.f); acc.y = vmax(acc.y, 0.f);
+        acc.z = vmax(acc.z, 0.f); acc.w = vmax(acc.w, 0.f);
+    }
+    out[idx] = acc;
+}
+
+// Grouped direct conv, weights [g][KH*KW*Cin_p][Cout_p].  vec_end / fma_all
+// encode which channels the reference's dispatcher (src/group_conv.cpp:60-79)
+// runs through a fused-multiply-add vector kernel.
+__global__ void k_gconv(const float* __restrict__ in, int N, int H, int W, int Cin,
+                        const float* __restrict__ w, const float* __restrict__ bias, int KH,
+                        int KW, int Cout, int stride, int pad, int groups, int OH, int OW,
+                        float* __restrict__ out, int act, int vec_end, int fma_all) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)N * OH * OW * Cout;
+    if (idx >= total) return;
+    int co = (int)(idx % Cout);
+    long long p = idx / Cout;
+    int ow = (int)(p % OW);
+    p /= OW;
+    int oh = (int)(p % OH);
+    int n = (int)(p / OH);
+    int Cin_p = Cin / groups, Cout_p = Cout / groups;
+    int g = co / Cout_p, oc = co - g * Cout_p;
+    const float* wg = w + (long long)g * Cout_p * KH * KW * Cin_p;
+    float s = bias ? bias[co] : 0.0f;
+    bool use_fma = fma_all || oc < vec_end;
+    for (int kh = 0; kh < KH; ++kh) {
+        int ih = oh * stride - pad + kh;
+        if (ih < 0 || ih >= H) continue;
+        for (int kw = 0; kw < KW; ++kw) {
+            int iw = ow * stride - pad + kw;
+            if (iw < 0 || iw >= W) continue;
+            const float* px = in + (((long long)n * H + ih) * W + iw) * Cin + (long long)g * Cin_p;
+            const float* wp = wg + (long long)((kh * KW + kw) * Cin_p) * Cout_p + oc;
+            if (use_fma) {
+                for (int ic = 0; ic < Cin_p; ++ic) s = fmaf(px[ic], wp[(long long)ic * Cout_p], s);
+            } else {
+                for (int ic = 0; ic < Cin_p; ++ic) s = s + px[ic] * wp[(long long)ic * Cout_p];
+            }
+        }
+    }
+    if (act == 1) {
+        if (oc < vec_end) s = vmax(s, 0.0f);
+        else if (s < 0.0f) s = 0.0f;
+    }
+    out[idx] = s;
+}
+
+// MaxPool: channels below vec_end use max_ps semantics, the rest the scalar
+// compare of src/layers.cpp:221-246 (they differ only for NaN / signed zero).
+__global__ void k_maxpool(const float* __restrict__ in, int N, int H, int W, int C, int pool,
+                          int stride, int pad, int OH, int OW, float* __restrict__ out,
+                          int post_relu, int vec_end) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)N * OH * OW * C;
+    if (idx >= total) return;
+    int c = (int)(idx % C);
+    long long p = idx / C;
+    int ow = (int)(p % OW);
+    p /= OW;
+    int oh = (int)(p % OH);
+    int n = (int)(p / OH);
+    const float* img = in + (long long)n * H * W * C + c;
+    bool vec = c < vec_end;
+    float mx = -1e30f;
+    for (int ph = 0; ph < pool; ++ph) {
+        int ih = oh * stride - pad + ph;
+        if (ih < 0 || ih >= H) continue;
+        for (int pw = 0; pw < pool; ++pw) {
+            int iw = ow * stride - pad + pw;
+            if (iw < 0 || iw >= W) continue;
+            float v = img[((long long)ih * W + iw) * C];
+            if (vec) mx = vmax(mx, v);
+            else if (v > mx) mx = v;
+        }
+    }
+    if (post_relu) {
+        if (vec) mx = vmax(mx, 0.0f);
+        else if (mx < 0.0f) mx = 0.0f;
+    }
+    out[idx] = mx;
+}
+
+__global__ void k_relu(float* __restrict__ d, size_t n, int six) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = d[i];
+    if (v < 0.0f) v = 0.0f;
+    else if (six && v > 6.0f) v = 6.0f;
+    d[i] = v;
+}
+
+__global__ void k_fill(float* __restrict__ d, size_t n, float v) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = v;
+}
+
+// Row softmax: one 256-thread block per row (src/layers.cpp:272-283).
+__global__ void k_softmax(const float* __restrict__ in, int cols, float* __restrict__ out) {
+    __shared__ float red[256];
+    const float* ri = in + (long long)blockIdx.x * cols;
+    float* ro = out + (long long)blockIdx.x * cols;
+    float mx = ri[0];
+    for (int c = threadIdx.x; c < cols; c += 256) mx = ri[c] > mx ? ri[c] : mx;
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = vmax(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    mx = red[0];
+    __syncthreads();
+    float sum = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        float e = expf(ri[c] - mx);
+        ro[c] = e;
+        sum += e;
+    }
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+        __syncthreads();
+    }
+    float inv = 1.0f / red[0];
+    for (int c = threadIdx.x; c < cols; c += 256) ro[c] = ro[c] * inv;
+}
+
+// Unfused BN, two roundings per step like src/layers.cpp:285-296.
+__global__ void k_batchnorm(float* __restrict__ d, long long total, int channels,
+                            const float* __restrict__ mean, const float* __restrict__ var,
+                            const float* __restrict__ gamma, const float* __restrict__ beta,
+                            float eps) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    int c = (int)(i % channels);
+    float scale = gamma ? gamma[c] : 1.0f;
+    float shift = beta ? beta[c] : 0.0f;
+    float inv = scale / sqrtf(var[c] + eps);
+    float t = d[i] - mean[c];
+    t = t * inv;
+    d[i] = t + shift;
+}
+
+// dst[p*dstC + dstOff + i] = src[p*srcC + off + i], i < cnt (per-group copies).
+__global__ void k_chan_copy(const float* __restrict__ src, int pix, int srcC, int off, int cnt,
+                            float* __restrict__ dst, int dstC, int dstOff) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)pix * cnt) return;
+    long long p = i / cnt;
+    int c = (int)(i - p * cnt);
+    dst[p * dstC + dstOff + c] = src[p * srcC + off + c];
+}
+
+__global__ void k_add_relu(const float* __restrict__ a, const float* __restrict__ b,
+                           float* __restrict__ y, size_t n, int act) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = a[i] + b[i];
+    if (act && v < 0.0f) v = 0.0f;
+    y[i] = v;
+}
+
+__global__ void k_gap(const float* __restrict__ x, int N, int HW, int C, float* __restrict__ y) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)N * C) return;
+    int n = (int)(i / C), c = (int)(i - (long long)n * C);
+    const float* p = x + (long long)n * HW * C + c;
+    float s = 0.0f;
+    for (int k = 0; k < HW; ++k) s += p[(long long)k * C];
+    y[i] = s / (float)HW;
+}
+
+inline dim3 grid1d(long long n, int bs = 256) { return dim3((unsigned)((n + bs - 1) / bs)); }
+
+}  // namespace
+
+bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, const float* bias,
+                int KH, int KW, int stride, int pad, float* out, int act, hipStream_t s) {
+    int OH = (H + 2 * pad - KH) / stride + 1;
+    int OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH <= 0 || OW <= 0 || KH <= 0 || KW <= 0) return true;
+    bool al = (((uintptr_t)in | (uintptr_t)out) & 15u) == 0;
+    if (KH == 3 && KW == 3 && C % 4 == 0 && al) {
+        long long total = (long long)N * OH * OW * (C / 4);
+        hipLaunchKernelGGL(k_dwconv3_c4, grid1d(total), dim3(256), 0, s, (const float4*)in, N, H,
+                           W, C / 4, w, bias, stride, pad, OH, OW, (float4*)out, act);
+        return check_launch("k_dwconv3_c4");
+    }
+    long long total = (long long)N * OH * OW * C;
+    hipLaunchKernelGGL(k_dwconv, grid1d(total), dim3(256), 0, s, in, N, H, W, C, w, bias, KH, KW,
+                       stride, pad, OH, OW, out, act);
+    return check_launch("k_dwconv");
+}
+
+bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+               int KH, int KW, int Cout, int stride, int pad, int groups, float* out, int act,
+               hipStream_t s) {
+    if (groups <= 1 || KH <= 0 || KW <= 0) return true;
+    int OH = (H + 2 * pad - KH) / stride + 1;
+    int OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH <= 0 || OW <= 0) return true;
+    int Cout_p = Cout / groups;
+    // src/group_conv.cpp:60-79 on an AVX-512 host: >=16 -> all-FMA kernel,
+    // >=8 -> AVX2 kernel (vector part + contracted scalar tail), else scalar.
+    int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
+    int fma_all = Cout_p >= 8 ? 1 : 0;
+    long long total = (long long)N * OH * OW * Cout;
+    hipLaunchKernelGGL(k_gconv, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH, KW,
+                       Cout, stride, pad, groups, OH, OW, out, act, vec_end, fma_all);
+    return check_launch("k_gconv");
+}
+
+bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stride, int pad,
+                 float* out, int post_relu, hipStream_t s) {
+    int OH = (H + 2 * pad - pool) / stride + 1;
+    int OW = (W + 2 * pad - pool) / stride + 1;
+    if (OH <= 0 || OW <= 0) return true;
+    int vec_end = C >= 16 ? (C & ~15) : (C >= 8 ? (C & ~7) : 0);
+    long long total = (long long)N * OH * OW * C;
+    hipLaunchKernelGGL(k_maxpool, grid1d(total), dim3(256), 0, s, in, N, H, W, C, pool, stride,
+                       pad, OH, OW, out, post_relu, vec_end);
+    return check_launch("k_maxpool");
+}
+
+bool relu_f32(float* d, size_t n, int six, hipStream_t s) {
+    if (!n) return true;
+    hipLaunchKernelGGL(k_relu, grid1d((long long)n), dim3(256), 0, s, d, n, six);
+    return check_launch("k_relu");
+}
+
+bool fill_f32(float* d, size_t n, float v, hipStream_t s) {
+    if (!n) return true;
+    hipLaunchKernelGGL(k_fill, grid1d((long long)n), dim3(256), 0, s, d, n, v);
+    return check_launch("k_fill");
+}
+
+bool add_relu_f32(const float* a, const float* b, float* y, size_t n, int act, hipStream_t s) {
+    if (!n) return true;
+    hipLaunchKernelGGL(k_add_relu, grid1d((long long)n), dim3(256), 0, s, a, b, y, n, act);
+    return check_launch("k_add_relu");
+}
+
+bool gap_f32(const float* x, int N, int HW, int C, float* y, hipStream_t s) {
+    if (N <= 0 || C <= 0 || HW <= 0) return true;
+    hipLaunchKernelGGL(k_gap, grid1d((long long)N * C), dim3(256), 0, s, x, N, HW, C, y);
+    return check_launch("k_gap");
+}
+
+bool softmax_f32(const float* in, int rows, int cols, float* out, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return true;
+    hipLaunchKernelGGL(k_softmax, dim3(rows), dim3(256), 0, s, in, cols, out);
+    return check_launch("k_softmax");
+}
+
+bool batchnorm_f32(float* d, int size, int channels, const float* mean, const float* var,
+                   const float* gamma, const float* beta, float eps, hipStream_t s) {
+    if (size <= 0 || channels <= 0) return true;
+    long long total = (long long)(size / channels) * channels;
+    hipLaunchKernelGGL(k_batchnorm, grid1d(total), dim3(256), 0, s, d, total, channels, mean, var,
+                       gamma, beta, eps);
+    return check_launch("k_batchnorm");
+}
+
+bool group_split_copy(const float* src, int pix, int srcC, int off, int cnt, float* dst, int dstC,
+                      int dstOff, hipStream_t s) {
+    long long total = (long long)pix * cnt;
+    if (!total) return true;
+    hipLaunchKernelGGL(k_chan_copy, grid1d(total), dim3(256), 0, s, src, pix, srcC, off, cnt, dst,
+                       dstC, dstOff);
+    return check_launch("k_chan_copy");
+}
+
+}  // namespace acfun

@@ -1,0 +1,525 @@
+// model.cpp -- ACFUN0 model loader and device executor.
+//
+// Format and load-time fusion follow the reference's src/model.cpp:
+//   header  "ACFUN0", u32 version, u32 inC, inH, inW, u32 num          (:3-16,117-122)
+//   records 1 Conv KH,KW,Cout,s,p,w,b | 2 FC Cout,inDim,w,b | 3 ReLU |
+//           4 MaxPool pool,s,p | 5 Softmax | 6 BN ch,mean,var,gamma,beta |
+//           7 ConvG KH,KW,Cout,s,p,groups,w,b                           (:130-196)
+//   fusion  Conv/FC/ConvG absorb a following ReLU and/or a following BN of
+//           matching width (folded by fold_bn_into, :69-95); a ReLU whose
+//           next layer is MaxPool is dropped; MaxPool absorbs a following
+//           ReLU (:199-247).
+// Differences, all stricter or additive:
+//   * truncated files and out-of-range records are rejected (nullptr);
+//   * version >= 2 files may also hold residual-network records (not in the
+//     reference; its loader rejects unknown types at :193):
+//       8  Add      u32 from, u32 act   cur = cur + out(from), ReLU if act
+//       9  GlobalAvgPool               [H,W,C] -> [1,1,C], sequential sum / (H*W)
+//       10 Input    u32 from            cur = out(from) (branch start)
+//     `from` is a raw record index whose output the executor keeps alive
+//     (0xFFFFFFFF = the model input); it must be the last record of its
+//     fused group;
+//   * inference runs batched on the device; folded weights live in HBM.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../include/acfun/acfun.h"
+#include "rt.hpp"
+
+using namespace acfun;
+
+namespace {
+
+struct Layer {
+    int type = 0;
+    int p[8] = {0};
+    int act = 0;
+    int post_relu = 0;
+    int raw_last = -1;  // last raw record this fused layer covers
+    int from = -2;      // Add/Input: fused index of the referenced tensor (-1 = input)
+    size_t wn = 0;      // weight element count
+    float* w = nullptr;  // device
+    float* b = nullptr;  // device
+    // BN (unfused) parameters live in w: mean|var|gamma|beta
+    // int8 variant of a conv: quantized weights and per-channel scales
+    int8_t* wq = nullptr;
+    float* ws = nullptr;
+};
+
+struct Raw {
+    int type = 0;
+    int p[8] = {0};
+    const float* w = nullptr;
+    const float* b = nullptr;
+    int prevC = 0;
+    size_t wn = 0;
+    int outC = 0;
+};
+
+unsigned rd32(const unsigned char* p) {
+    return (unsigned)p[0] | ((unsigned)p[1] << 8) | ((unsigned)p[2] << 16) | ((unsigned)p[3] << 24);
+}
+
+// fold_bn_into of src/model.cpp:69-95, same operation order (this file is
+// compiled with -ffp-contract=off, and x86 host code has no implicit FMA).
+void fold_bn(std::vector<float>& nw, std::vector<float>& nb, const float* w, const float* b,
+             const Raw& bn, int Cout, size_t wn, int groups) {
+    int ch = bn.p[0];
+    const float* mean = bn.w;
+    const float* var = bn.w + ch;
+    const float* gamma = bn.w + 2 * ch;
+    const float* beta = bn.w + 3 * ch;
+    int Cout_per = (groups > 1) ? Cout / groups : Cout;
+    size_t per_in = wn / (size_t)Cout;
+    nw.assign(w, w + wn);
+    nb.assign(Cout, 0.0f);
+    for (int c = 0; c < Cout; ++c) {
+        float scale = gamma[c] / sqrtf(var[c] + 1e-5f);
+        float shift = beta[c] - mean[c] * scale;
+        int gc = (groups > 1) ? c / Cout_per : 0;
+        int oc = (groups > 1) ? c % Cout_per : c;
+        for (size_t t = 0; t < per_in; ++t) {
+            size_t off = (size_t)gc * (size_t)Cout_per * per_in + t * (size_t)Cout_per + oc;
+            nw[off] *= scale;
+        }
+        nb[c] = (b ? b[c] : 0.0f) * scale + shift;
+    }
+}
+
+bool upload(const float* host, size_t n, float** dev) {
+    *dev = nullptr;
+    if (!n) return true;
+    if (!check(hipMalloc((void**)dev, n * sizeof(float)), "hipMalloc(model weights)")) return false;
+    return check(hipMemcpy(*dev, host, n * sizeof(float), hipMemcpyHostToDevice), "H2D weights");
+}
+
+// Per-column symmetric int8 quantization on the host, same rule as
+// acfun_quantize_weights (src/conv_int8.cpp:24-37).
+void quantize_cols(const std::vector<float>& w, int K, int N, std::vector<float>& sc,
+                   std::vector<int8_t>& q) {
+    sc.assign(N, 1.0f);
+    q.assign((size_t)K * N, 0);
+    for (int j = 0; j < N; ++j) {
+        float maxa = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            float a = std::fabs(w[(size_t)k * N + j]);
+            maxa = maxa < a ? a : maxa;
+        }
+        float s = maxa / 127.0f;
+        if (s <= 0.0f) s = 1.0f;
+        sc[j] = s;
+        for (int k = 0; k < K; ++k) {
+            long v = std::lroundf(w[(size_t)k * N + j] / s);
+            if (v > 127) v = 127;
+            else if (v < -128) v = -128;
+            q[(size_t)k * N + j] = (int8_t)v;
+        }
+    }
+}
+
+}  // namespace
+
+struct AcfunModel {
+    int inC = 0, inH = 0, inW = 0;
+    int version = 0;
+    int int8 = 0;
+    std::vector<Layer> layers;
+    int outSize = 0;
+};
+
+namespace {
+
+void free_layers(AcfunModel* m) {
+    for (auto& L : m->layers) {
+        if (L.w) hipFree(L.w);
+        if (L.b) hipFree(L.b);
+        if (L.wq) hipFree(L.wq);
+        if (L.ws) hipFree(L.ws);
+    }
+    m->layers.clear();
+}
+
+AcfunModel* load_impl(const char* path, int flags) {
+    if (!ensure_device()) return nullptr;
+    FILE* f = fopen(path, "rb");
+    if (!f) { set_error("acfun_model_load: cannot open %s", path); return nullptr; }
+    fseek(f, 0, SEEK_END);
+    long sz = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    std::vector<unsigned char> blob(sz > 0 ? (size_t)sz : 1);
+    if (sz < 0 || fread(blob.data(), 1, (size_t)sz, f) != (size_t)sz) { fclose(f); return nullptr; }
+    fclose(f);
+    if (sz < 6 + 4 * 5 || memcmp(blob.data(), "ACFUN0", 6) != 0) {
+        set_error("acfun_model_load: bad magic or short header");
+        return nullptr;
+    }
+    const unsigned char* B = blob.data();
+    size_t o = 6;
+    int version = (int)rd32(B + o); o += 4;
+    int inC = (int)rd32(B + o); o += 4;
+    int inH = (int)rd32(B + o); o += 4;
+    int inW = (int)rd32(B + o); o += 4;
+    int num = (int)rd32(B + o); o += 4;
+    if (num < 0 || inC <= 0 || inH <= 0 || inW <= 0) { set_error("acfun_model_load: bad header"); return nullptr; }
+
+    auto need = [&](size_t bytes) { return o + bytes <= (size_t)sz; };
+    std::vector<Raw> raw(num);
+    int prevC = inC;
+    for (int i = 0; i < num; ++i) {
+        Raw& L = raw[i];
+        if (!need(4)) { set_error("acfun_model_load: truncated at record %d", i); return nullptr; }
+        L.type = (int)rd32(B + o); o += 4;
+        auto u32s = [&](int n) -> bool {
+            if (!need(4 * (size_t)n)) return false;
+            for (int k = 0; k < n; ++k) { L.p[k] = (int)rd32(B + o); o += 4; }
+            return true;
+        };
+        auto floats = [&](size_t n, const float** dst) -> bool {
+            if (n > ((size_t)sz) / 4 || !need(4 * n)) return false;
+            *dst = (const float*)(B + o);
+            o += 4 * n;
+            return true;
+        };
+        bool ok = true;
+        switch (L.type) {
+            case 1:  // Conv
+                ok = u32s(5) && L.p[0] > 0 && L.p[1] > 0 && L.p[2] > 0 && L.p[3] > 0;
+                if (ok) {
+                    L.prevC = prevC;
+                    L.wn = (size_t)L.p[0] * L.p[1] * prevC * L.p[2];
+                    ok = floats(L.wn, &L.w) && floats(L.p[2], &L.b);
+                    prevC = L.p[2];
+                }
+                break;
+            case 2:  // FC
+                ok = u32s(2) && L.p[0] > 0 && L.p[1] > 0;
+                if (ok) {
+                    L.wn = (size_t)L.p[1] * L.p[0];
+                    ok = floats(L.wn, &L.w) && floats(L.p[0], &L.b);
+                    prevC = L.p[0];
+                }
+                break;
+            case 7:  // ConvGrouped
+                ok = u32s(6) && L.p[0] > 0 && L.p[1] > 0 && L.p[2] > 0 && L.p[3] > 0 && L.p[5] > 0;
+                if (ok) {
+                    L.prevC = prevC;
+                    L.wn = (size_t)L.p[0] * L.p[1] * prevC * L.p[2] / L.p[5];
+                    ok = floats(L.wn, &L.w) && floats(L.p[2], &L.b);
+                    prevC = L.p[2];
+                }
+                break;
+            case 3: case 5: break;
+            case 4: ok = u32s(3) && L.p[0] > 0 && L.p[1] > 0; break;
+            case 6:
+                ok = u32s(1) && L.p[0] > 0;
+                if (ok) { L.wn = (size_t)L.p[0] * 4; ok = floats(L.wn, &L.w); }
+                break;
+            case 8:
+                ok = version >= 2 && u32s(2);
+                break;
+            case 9:
+                ok = version >= 2;
+                break;
+            case 10:
+                ok = version >= 2 && u32s(1);
+                if (ok) {
+                    int from = L.p[0];
+                    if (from == -1) prevC = inC;
+                    else if (from >= 0 && from < i) prevC = raw[from].outC;
+                    else ok = false;
+                }
+                break;
+            default: ok = false;
+        }
+        if (!ok) { set_error("acfun_model_load: bad or truncated record %d (type %d)", i, L.type); return nullptr; }
+        L.outC = prevC;
+    }
+
+    AcfunModel* m = new AcfunModel();
+    m->inC = inC; m->inH = inH; m->inW = inW; m->version = version;
+    m->int8 = (flags & 1) ? 1 : 0;
+    std::vector<char> consumed(num, 0);
+    std::vector<int> raw2fused(num, -1);
+    bool fail = false;
+    for (int i = 0; i < num && !fail; ++i) {
+        if (consumed[i]) continue;
+        Raw& L = raw[i];
+        Layer F;
+        F.type = L.type;
+        memcpy(F.p, L.p, sizeof(L.p));
+        F.raw_last = i;
+        if (L.type == 1 || L.type == 2 || L.type == 7) {  // :204-228
+            int Cout = (L.type == 2) ? L.p[0] : L.p[2];
+            int groups = (L.type == 7) ? L.p[5] : 0;
+            std::vector<float> hw(L.w, L.w + L.wn), hb(L.b, L.b + Cout);
+            int j = i + 1, reluIdx = -1;
+            if (j < num && raw[j].type == 3) { reluIdx = j; j++; }
+            if (j < num && raw[j].type == 6 && raw[j].p[0] == Cout) {
+                fold_bn(hw, hb, L.w, L.b, raw[j], Cout, L.wn, groups);
+                consumed[j] = 1;
+                F.raw_last = j;
+            }
+            if (reluIdx >= 0) {
+                if (j < num && raw[j].type == 4) { consumed[reluIdx] = 1; F.act = 0; }
+                else { F.act = 1; consumed[reluIdx] = 1; }
+                if (reluIdx > F.raw_last) F.raw_last = reluIdx;
+            }
+            F.wn = L.wn;
+            if (!upload(hw.data(), hw.size(), &F.w) || !upload(hb.data(), hb.size(), &F.b)) fail = true;
+            if (!fail && m->int8 && L.type == 1) {
+                int K = (int)(L.wn / Cout);
+                std::vector<float> sc;
+                std::vector<int8_t> q;
+                quantize_cols(hw, K, Cout, sc, q);
+                if (!upload(sc.data(), sc.size(), &F.ws) ||
+                    !check(hipMalloc((void**)&F.wq, q.size()), "hipMalloc(wq)") ||
+                    !check(hipMemcpy(F.wq, q.data(), q.size(), hipMemcpyHostToDevice), "H2D wq"))
+                    fail = true;
+            }
+        } else if (L.type == 3) {  // :229-233
+            if (i + 1 < num && raw[i + 1].type == 4) { consumed[i] = 1; continue; }
+        } else if (L.type == 6) {  // :234-235
+            F.wn = L.wn;
+            if (!upload(L.w, L.wn, &F.w)) fail = true;
+        } else if (L.type == 4) {  // :236-242
+            if (i + 1 < num && raw[i + 1].type == 3) {
+                F.post_relu = 1;
+                consumed[i + 1] = 1;
+                F.raw_last = i + 1;
+            }
+        }
+        m->layers.push_back(F);
+        int fi = (int)m->layers.size() - 1;
+        for (int r = i; r <= F.raw_last; ++r) raw2fused[r] = fi;
+    }
+    // Resolve Add / Input references to fused layers.
+    for (auto& F : m->layers) {
+        if (F.type != 8 && F.type != 10) continue;
+        int from = F.p[0];
+        if (from == -1) { F.from = -1; continue; }
+        if (from < 0 || from >= num || raw2fused[from] < 0 ||
+            m->layers[raw2fused[from]].raw_last != from) {
+            set_error("acfun_model_load: record reference %d is not the end of a fused layer", from);
+            fail = true;
+            break;
+        }
+        F.from = raw2fused[from];
+    }
+    if (fail) {
+        free_layers(m);
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+struct Dims { int H, W, C; };
+
+// Runs the fused layers on N images resident in HBM.
+int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s) {
+    const int L = (int)m->layers.size();
+    // Shapes and last uses (liveness) of every fused output.
+    std::vector<Dims> out(L);
+    std::vector<int> last_use(L, -1);
+    Dims cur{m->inH, m->inW, m->inC};
+    int input_last = 0;
+    for (int i = 0; i < L; ++i) {
+        Layer& F = m->layers[i];
+        Dims in = cur;
+        if (F.type == 10) in = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from];
+        Dims o = in;
+        switch (F.type) {
+            case 1: case 7: {
+                int KH = F.p[0], KW = F.p[1], st = F.p[3], pd = F.p[4];
+                o = Dims{(in.H + 2 * pd - KH) / st + 1, (in.W + 2 * pd - KW) / st + 1, F.p[2]};
+                break;
+            }
+            case 2: o = Dims{1, 1, F.p[0]}; break;
+            case 4: o = Dims{(in.H + 2 * F.p[2] - F.p[0]) / F.p[1] + 1, (in.W + 2 * F.p[2] - F.p[0]) / F.p[1] + 1, in.C}; break;
+            case 9: o = Dims{1, 1, in.C}; break;
+            default: break;
+        }
+        if (o.H <= 0 || o.W <= 0 || o.C <= 0) { set_error("model: empty output at layer %d", i); return 0; }
+        if (F.type == 8) {
+            Dims r = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from];
+            if (r.H != in.H || r.W != in.W || r.C != in.C) { set_error("model: Add shape mismatch at layer %d", i); return 0; }
+        }
+        // consumers
+        if (F.type == 10 || F.type == 8) {
+            if (F.from < 0) input_last = i; else last_use[F.from] = i;
+        }
+        if (F.type != 10) {
+            if (i == 0) input_last = std::max(input_last, 0);
+            else last_use[i - 1] = std::max(last_use[i - 1], i);
+        }
+        out[i] = o;
+        cur = o;
+    }
+    if (L) last_use[L - 1] = L;  // the result stays until copied out
+    // Execute.
+    std::vector<float*> buf(L, nullptr);
+    std::vector<Scratch> hold(L);
+    auto tensor_of = [&](int idx) -> const float* { return idx < 0 ? din : buf[idx]; };
+    cur = Dims{m->inH, m->inW, m->inC};
+    const float* x = din;
+    int xi = -1;
+    for (int i = 0; i < L; ++i) {
+        Layer& F = m->layers[i];
+        Dims in = cur;
+        if (F.type == 10) { x = tensor_of(F.from); xi = F.from; in = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from]; }
+        Dims o = out[i];
+        size_t cap = (size_t)N * o.H * o.W * o.C;
+        bool inplace = (F.type == 3 || F.type == 5 || F.type == 6 || F.type == 10);
+        float* y;
+        if (inplace && F.type != 10 && xi >= 0 && last_use[xi] == i) {
+            // take over the input buffer
+            y = buf[xi];
+            hold[i] = std::move(hold[xi]);
+            buf[xi] = nullptr;
+        } else {
+            hold[i] = Scratch(cap * sizeof(float), s);
+            if (!hold[i].p) return 0;
+            y = hold[i].as<float>();
+            if (inplace && F.type != 10 &&
+                !check(hipMemcpyAsync(y, x, cap * sizeof(float), hipMemcpyDeviceToDevice, s), "D2D"))
+                return 0;
+        }
+        buf[i] = y;
+        bool ok = true;
+        switch (F.type) {
+            case 1: case 7: {
+                int groups = F.type == 7 ? F.p[5] : 1;
+                if (m->int8 && F.type == 1 && F.wq) {
+                    ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
+                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, F.act, s);
+                } else {
+                    ok = conv2d_route_f32(x, N, in.H, in.W, in.C, F.w, F.b, F.p[0], F.p[1], o.C,
+                                          F.p[3], F.p[4], groups > 1 ? groups : 1, y, F.act, s);
+                }
+                break;
+            }
+            case 2: {
+                int inDim = in.H * in.W * in.C;
+                if ((size_t)inDim * F.p[0] != F.wn) {
+                    set_error("model: FC input %d does not match weights", inDim);
+                    return 0;
+                }
+                ok = gemm_f32(N, o.C, inDim, x, inDim, F.w, o.C, y, o.C, F.b, F.act, s);
+                break;
+            }
+            case 3: ok = relu_f32(y, cap, 0, s); break;
+            case 4: ok = maxpool_f32(x, N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[2], y, F.post_relu, s); break;
+            case 5: ok = softmax_f32(y, N, (int)(cap / N), y, s); break;
+            case 6: {
+                int ch = F.p[0];
+                size_t per = cap / N;
+                const float* P = F.w;
+                if (per % ch == 0) ok = batchnorm_f32(y, (int)cap, ch, P, P + ch, P + 2 * ch, P + 3 * ch, 1e-5f, s);
+                else
+                    for (int n = 0; n < N && ok; ++n)
+                        ok = batchnorm_f32(y + n * per, (int)per, ch, P, P + ch, P + 2 * ch, P + 3 * ch, 1e-5f, s);
+                break;
+            }
+            case 8: ok = add_relu_f32(x, tensor_of(F.from), y, cap, F.p[1], s); break;
+            case 9: ok = gap_f32(x, N, in.H * in.W, in.C, y, s); break;
+            case 10: ok = check(hipMemcpyAsync(y, x, cap * sizeof(float), hipMemcpyDeviceToDevice, s), "D2D"); break;
+        }
+        if (!ok) return 0;
+        // release inputs whose last consumer was this layer
+        for (int j = 0; j < i; ++j)
+            if (buf[j] && last_use[j] == i) { hold[j] = Scratch(); buf[j] = nullptr; }
+        cur = o;
+        x = y;
+        xi = i;
+    }
+    size_t per = (size_t)cur.H * cur.W * cur.C;
+    if (L == 0) per = (size_t)m->inH * m->inW * m->inC;
+    if (!check(hipMemcpyAsync(dout, x, (size_t)N * per * sizeof(float), hipMemcpyDeviceToDevice, s), "D2D out"))
+        return 0;
+    m->outSize = (int)per;
+    return (int)per;
+}
+
+}  // namespace
+
+extern "C" {
+
+AcfunModel* acfun_model_load(const char* path) { return load_impl(path, 0); }
+
+AcfunModel* acfun_model_load_ex(const char* path, int flags) { return load_impl(path, flags); }
+
+void acfun_model_destroy(AcfunModel* m) {
+    if (!m) return;
+    free_layers(m);
+    delete m;
+}
+
+int acfun_model_output_size(AcfunModel* m) { return m ? m->outSize : 0; }
+
+void acfun_model_input_dims(AcfunModel* m, int* Cin, int* Hin, int* Win) {
+    if (!m) return;
+    if (Cin) *Cin = m->inC;
+    if (Hin) *Hin = m->inH;
+    if (Win) *Win = m->inW;
+}
+
+int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float* output,
+                                void* stream) {
+    if (!m || N <= 0 || !ensure_device()) return 0;
+    return run_model(m, N, input, output, resolve(stream));
+}
+
+int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* output) {
+    if (!m || N <= 0 || !ensure_device()) return 0;
+    hipStream_t s = lib_stream();
+    // The output size is known only after shape inference; run shape-only
+    // pass through run_model on the device result buffer sized generously.
+    size_t in_n = (size_t)N * m->inC * m->inH * m->inW;
+    HostCall hc(s);
+    const float* din = (const float*)hc.in(input, in_n * sizeof(float));
+    if (hc.failed()) return 0;
+    // Upper bound of the per-image output: the largest tensor in the graph.
+    size_t maxper = (size_t)m->inC * m->inH * m->inW;
+    {
+        int H = m->inH, W = m->inW, C = m->inC;
+        std::vector<Dims> outs;
+        for (auto& F : m->layers) {
+            if (F.type == 10) {
+                Dims d = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : outs[F.from];
+                H = d.H; W = d.W; C = d.C;
+            }
+            switch (F.type) {
+                case 1: case 7: H = (H + 2 * F.p[4] - F.p[0]) / F.p[3] + 1; W = (W + 2 * F.p[4] - F.p[1]) / F.p[3] + 1; C = F.p[2]; break;
+                case 2: H = W = 1; C = F.p[0]; break;
+                case 4: H = (H + 2 * F.p[2] - F.p[0]) / F.p[1] + 1; W = (W + 2 * F.p[2] - F.p[0]) / F.p[1] + 1; break;
+                case 9: H = W = 1; break;
+                default: break;
+            }
+            outs.push_back(Dims{H, W, C});
+            if (H > 0 && W > 0 && C > 0 && (size_t)H * W * C > maxper) maxper = (size_t)H * W * C;
+        }
+    }
+    Scratch dres((size_t)N * maxper * sizeof(float), s);
+    if (!dres.p) return 0;
+    int per = run_model(m, N, din, dres.as<float>(), s);
+    if (per > 0) {
+        void* dst = output;
+        if (is_device_ptr(output)) {
+            if (!check(hipMemcpyAsync(dst, dres.p, (size_t)N * per * sizeof(float), hipMemcpyDeviceToDevice, s), "D2D")) per = 0;
+        } else if (!check(hipMemcpyAsync(dst, dres.p, (size_t)N * per * sizeof(float), hipMemcpyDeviceToHost, s), "D2H")) {
+            per = 0;
+        }
+    }
+    if (!check(hipStreamSynchronize(s), "sync")) return 0;
+    return per;
+}
+
+int acfun_model_infer(AcfunModel* m, const float* input, float* output) {
+    return acfun_model_infer_batch(m, 1, input, output);
+}
+
+}  // extern "C"

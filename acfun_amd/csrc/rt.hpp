@@ -1,0 +1,162 @@
+// rt.hpp -- runtime shared by the HIP kernels and the C-ABI layer of
+// libacfun_amd.so: device state, the library stream, a stream-ordered caching
+// memory pool, host<->device staging for the synchronous reference API, and
+// the launchers each kernel file exports.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace acfun {
+
+// ----------------------------------------------------------------- errors
+void set_error(const char* fmt, ...);
+const char* last_error();
+// Records `what` + the HIP error string and returns false when e != success.
+bool check(hipError_t e, const char* what);
+// Checks the launch status of the last kernel.
+bool check_launch(const char* kernel);
+
+// ----------------------------------------------------------------- device
+// Initializes the current device once (verifies it is gfx950, creates the
+// library stream).  Returns false (and sets the error) when no usable GPU.
+bool ensure_device();
+hipStream_t lib_stream();
+int num_cus();
+// Resolves a user stream argument: NULL -> library stream.
+inline hipStream_t resolve(void* s) { return s ? (hipStream_t)s : lib_stream(); }
+
+// ----------------------------------------------------------------- memory
+// Stream-ordered caching pool: a block returned with pool_free(p, s) is only
+// handed out again for work queued on the same stream s, so reuse is ordered
+// after every kernel that used it.
+void* pool_alloc(size_t bytes, hipStream_t s);
+void pool_free(void* p, hipStream_t s);
+
+// RAII scratch buffer from the pool.
+struct Scratch {
+    void* p = nullptr;
+    hipStream_t s = nullptr;
+    Scratch() = default;
+    Scratch(size_t bytes, hipStream_t st) : s(st) { p = bytes ? pool_alloc(bytes, st) : nullptr; }
+    ~Scratch() { if (p) pool_free(p, s); }
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
+    Scratch(Scratch&& o) noexcept : p(o.p), s(o.s) { o.p = nullptr; }
+    Scratch& operator=(Scratch&& o) noexcept {
+        if (this != &o) {
+            if (p) pool_free(p, s);
+            p = o.p;
+            s = o.s;
+            o.p = nullptr;
+        }
+        return *this;
+    }
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+bool is_device_ptr(const void* p);
+
+// Staging for the synchronous host-pointer API (the reference's contract):
+// inputs that are host memory are copied to pooled device buffers, outputs
+// are allocated on the device and copied back by finish(), which then
+// synchronizes the stream.  Device pointers pass through untouched.
+class HostCall {
+  public:
+    explicit HostCall(hipStream_t s) : s_(s) {}
+    ~HostCall();
+    const void* in(const void* host, size_t bytes);   // read-only operand
+    void* out(void* host, size_t bytes);              // write-only result
+    void* inout(void* host, size_t bytes);            // read-modify-write
+    bool finish();                                    // D2H + sync
+    hipStream_t stream() const { return s_; }
+    bool failed() const { return failed_; }
+
+  private:
+    struct Back { void* host; void* dev; size_t bytes; };
+    hipStream_t s_;
+    std::vector<void*> owned_;
+    std::vector<Back> back_;
+    bool failed_ = false;
+};
+
+// ----------------------------------------------------------------- launchers
+// All launchers take device pointers and a stream and return false on error.
+
+// fp32 implicit GEMM on MFMA: C = A*B (+bias, ReLU).  For conv, A is the
+// im2col view of an NHWC tensor, never materialized.
+struct ConvShape {
+    int N, H, W, Cin, KH, KW, stride, pad, OH, OW;
+};
+bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+              int ldc, const float* bias, int act, hipStream_t s);
+bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const float* bias,
+                    int Cout, float* out, int act, hipStream_t s);
+// Batched GEMM (batch = gridDim.z) with fixed strides, no epilogue.
+bool gemm_f32_batched(int batch, int M, int N, int K, const float* A, long long sA, int lda,
+                      const float* B, long long sB, int ldb, float* C, long long sC, int ldc,
+                      hipStream_t s);
+bool round_bf16(const float* in, float* out, size_t n, hipStream_t s);
+
+// Winograd 3x3/s1/p1 (tile = 2 for F(2,3), 4 for F(4,3)).
+bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
+                  const float* bias, int Cout, float* out, int act, hipStream_t s);
+
+// Bandwidth kernels.
+bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, const float* bias,
+                int KH, int KW, int stride, int pad, float* out, int act, hipStream_t s);
+bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+               int KH, int KW, int Cout, int stride, int pad, int groups, float* out, int act,
+               hipStream_t s);
+bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stride, int pad,
+                 float* out, int post_relu, hipStream_t s);
+bool relu_f32(float* d, size_t n, int six, hipStream_t s);
+bool softmax_f32(const float* in, int rows, int cols, float* out, hipStream_t s);
+bool batchnorm_f32(float* d, int size, int channels, const float* mean, const float* var,
+                   const float* gamma, const float* beta, float eps, hipStream_t s);
+bool fill_f32(float* d, size_t n, float v, hipStream_t s);
+// y = a + b (ReLU if act): the residual Add record of version-2 models.
+bool add_relu_f32(const float* a, const float* b, float* y, size_t n, int act, hipStream_t s);
+// Global average pool [N][HW][C] -> [N][C]: sequential sum over HW, then / HW.
+bool gap_f32(const float* x, int N, int HW, int C, float* y, hipStream_t s);
+bool group_split_copy(const float* src, int pix, int srcC, int off, int cnt, float* dst,
+                      int dstC, int dstOff, hipStream_t s);
+
+// int8 family.
+enum class RoundMode : int { RNE = 0, LROUND = 1, WINO = 2 };
+bool quantize_weights_dev(const float* w, int K, int N, float* scales, int8_t* wq, hipStream_t s);
+bool quantize_u8_dev(const float* in, uint8_t* out, size_t n, float inv_s, int zp, hipStream_t s);
+bool gemm_int8_dev(int M, int N, int K, const uint8_t* A, const int8_t* B, int32_t* C,
+                   const float* alpha, const float* beta, float* Cf, int act, hipStream_t s);
+bool conv1x1_int8_dev(const uint8_t* inQ, int M, int K, int Cout, const int8_t* wq,
+                      const float* alpha, const float* beta, float* out, int act, hipStream_t s);
+bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* wq,
+                          const float* alpha, const float* beta, int Cout, float* out, int act,
+                          hipStream_t s);
+// acfun_conv2d_int8 end to end on device (absmax, params, quantize, conv).
+bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
+                     const float* bias, int Cout, float* out, int act, hipStream_t s);
+// The int8 Winograd-route entry with caller-supplied scales.
+bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,
+                       const float* ws, const float* bias, int Cout, float s_in, float inv_s,
+                       float* out, int act, hipStream_t s);
+
+// fp32 convolution routing exactly as the reference's conv2d_impl
+// (src/layers.cpp:106-195).
+bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float* w,
+                      const float* bias, int KH, int KW, int Cout, int stride, int pad,
+                      int groups, float* out, int act, hipStream_t s);
+
+// Tile-config table (autotune).
+struct TileCfg { int bm, bn, split; };
+TileCfg default_f32_tile(int M, int N, int K);
+TileCfg tuned_f32_tile(int M, int N, int K);
+// Runs one fp32 GEMM with an explicit tile config (used by the tile search).
+bool gemm_f32_cfg(int M, int N, int K, const float* A, const float* B, float* C,
+                  const TileCfg& cfg, hipStream_t s);
+void autotune_run();
+const char* tune_status();
+
+}  // namespace acfun

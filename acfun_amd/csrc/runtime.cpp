@@ -1,0 +1,221 @@
+// runtime.cpp -- device bring-up, library stream, caching pool, staging of
+// host buffers for the synchronous API, and the error string.
+#include "rt.hpp"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+namespace acfun {
+
+// ------------------------------------------------------------------ errors
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+const char* last_error() { return g_err; }
+
+bool check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool check_launch(const char* kernel) { return check(hipGetLastError(), kernel); }
+
+// ------------------------------------------------------------------ device
+namespace {
+constexpr int kMaxDev = 16;
+struct DevState {
+    bool init = false;
+    bool usable = false;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+};
+DevState g_dev[kMaxDev];
+std::mutex g_dev_mu;
+
+int current_device() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) return -1;
+    return d;
+}
+}  // namespace
+
+bool ensure_device() {
+    int d = current_device();
+    if (d < 0 || d >= kMaxDev) {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        set_error("no usable HIP device (hipGetDeviceCount: %s, count %d)",
+                  hipGetErrorString(e), n);
+        return false;
+    }
+    DevState& st = g_dev[d];
+    if (st.init) {
+        if (!st.usable) set_error("device %d is not a gfx950 GPU", d);
+        return st.usable;
+    }
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (!st.init) {
+        hipDeviceProp_t prop;
+        if (!check(hipGetDeviceProperties(&prop, d), "hipGetDeviceProperties")) return false;
+        st.usable = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+        st.cus = prop.multiProcessorCount;
+        if (st.usable) {
+            // Default priority, non-blocking with respect to the null stream.
+            if (!check(hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking),
+                       "hipStreamCreate")) {
+                st.usable = false;
+            }
+        } else {
+            set_error("device %d is %s, this library is built for gfx950 only", d,
+                      prop.gcnArchName);
+        }
+        st.init = true;
+    }
+    return st.usable;
+}
+
+hipStream_t lib_stream() {
+    int d = current_device();
+    return (d >= 0 && d < kMaxDev) ? g_dev[d].stream : nullptr;
+}
+
+int num_cus() {
+    int d = current_device();
+    return (d >= 0 && d < kMaxDev && g_dev[d].cus > 0) ? g_dev[d].cus : 256;
+}
+
+// ------------------------------------------------------------------ memory
+namespace {
+// Blocks are rounded up so that similar sizes share a free list.
+size_t round_size(size_t b) {
+    if (b <= 4096) return 4096;
+    if (b <= (1u << 20)) return (b + 65535) & ~size_t(65535);
+    return (b + (1u << 20) - 1) & ~size_t((1u << 20) - 1);
+}
+struct PoolKey {
+    int dev;
+    hipStream_t s;
+    size_t bytes;
+    bool operator<(const PoolKey& o) const {
+        if (dev != o.dev) return dev < o.dev;
+        if (s != o.s) return s < o.s;
+        return bytes < o.bytes;
+    }
+};
+std::mutex g_pool_mu;
+std::multimap<PoolKey, void*> g_free;
+std::map<void*, size_t> g_size;
+}  // namespace
+
+void* pool_alloc(size_t bytes, hipStream_t s) {
+    size_t rb = round_size(bytes);
+    int d = current_device();
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        auto it = g_free.find(PoolKey{d, s, rb});
+        if (it != g_free.end()) {
+            void* p = it->second;
+            g_free.erase(it);
+            return p;
+        }
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, rb) != hipSuccess) {
+        // Release cached blocks of this device and retry once.
+        std::vector<void*> drop;
+        {
+            std::lock_guard<std::mutex> lk(g_pool_mu);
+            for (auto it = g_free.begin(); it != g_free.end();) {
+                if (it->first.dev == d) { drop.push_back(it->second); it = g_free.erase(it); }
+                else ++it;
+            }
+            for (void* q : drop) g_size.erase(q);
+        }
+        hipDeviceSynchronize();
+        for (void* q : drop) hipFree(q);
+        if (!check(hipMalloc(&p, rb), "hipMalloc")) return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    g_size[p] = rb;
+    return p;
+}
+
+void pool_free(void* p, hipStream_t s) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    auto it = g_size.find(p);
+    if (it == g_size.end()) return;
+    g_free.emplace(PoolKey{current_device(), s, it->second}, p);
+}
+
+bool is_device_ptr(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // unregistered host memory: clear the sticky status
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+// ------------------------------------------------------------------ staging
+HostCall::~HostCall() {
+    for (void* p : owned_) pool_free(p, s_);
+}
+
+const void* HostCall::in(const void* host, size_t bytes) {
+    if (!host || bytes == 0 || failed_) return host;
+    if (is_device_ptr(host)) return host;
+    void* d = pool_alloc(bytes, s_);
+    if (!d) { failed_ = true; return nullptr; }
+    owned_.push_back(d);
+    if (!check(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, s_), "H2D copy")) {
+        failed_ = true;
+        return nullptr;
+    }
+    return d;
+}
+
+void* HostCall::out(void* host, size_t bytes) {
+    if (!host || bytes == 0 || failed_) return host;
+    if (is_device_ptr(host)) return host;
+    void* d = pool_alloc(bytes, s_);
+    if (!d) { failed_ = true; return nullptr; }
+    owned_.push_back(d);
+    back_.push_back({host, d, bytes});
+    return d;
+}
+
+void* HostCall::inout(void* host, size_t bytes) {
+    if (!host || bytes == 0 || failed_) return host;
+    if (is_device_ptr(host)) return host;
+    void* d = const_cast<void*>(in(host, bytes));
+    if (d) back_.push_back({host, d, bytes});
+    return d;
+}
+
+bool HostCall::finish() {
+    bool ok = !failed_;
+    if (ok) {
+        for (auto& b : back_) {
+            if (!check(hipMemcpyAsync(b.host, b.dev, b.bytes, hipMemcpyDeviceToHost, s_),
+                       "D2H copy")) { ok = false; break; }
+        }
+    }
+    if (!check(hipStreamSynchronize(s_), "hipStreamSynchronize")) ok = false;
+    return ok;
+}
+
+}  // namespace acfun

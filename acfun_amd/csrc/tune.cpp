@@ -1,0 +1,174 @@
+// tune.cpp -- MFMA tile-shape search, replacing the reference's cache-blocking
+// autotune (src/autotune.cpp:29-30,148-302,336-388).
+//
+// The reference searches (KC, NC) cache blocks for its CPU micro-kernel and
+// caches the winner per machine.  On the GPU the free parameters are the
+// workgroup tile (BM x BN of the MFMA kernel) and the split-K factor, which
+// trade occupancy of the 256 CUs against operand reuse.  acfun_autotune()
+// times every candidate on every GEMM shape this process has run (plus the
+// shapes named in ACFUN_TUNE_SHAPES="MxNxK,..."), keeps the fastest per
+// shape, and writes them to $HOME/.cache/acfun_amd/tune_gfx950.txt, which
+// later processes read at first use.  ACFUN_AUTOTUNE=1 runs the search at the
+// first GEMM of a process.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <set>
+#include <string>
+#include <tuple>
+
+#include "rt.hpp"
+
+namespace acfun {
+namespace {
+
+using Key = std::tuple<int, int, int>;
+std::mutex g_mu;
+std::map<Key, TileCfg> g_table;
+std::set<Key> g_seen;
+bool g_loaded = false;
+bool g_busy = false;
+std::string g_status = "default heuristic (no tile search run)";
+
+std::string cache_path() {
+    const char* h = std::getenv("HOME");
+    return std::string(h ? h : "/tmp") + "/.cache/acfun_amd/tune_gfx950.txt";
+}
+
+void load_cache_locked() {
+    if (g_loaded) return;
+    g_loaded = true;
+    FILE* f = fopen(cache_path().c_str(), "r");
+    if (!f) return;
+    int M, N, K, bm, bn, sp, n = 0;
+    while (fscanf(f, "TILE %d %d %d %d %d %d\n", &M, &N, &K, &bm, &bn, &sp) == 6) {
+        g_table[Key{M, N, K}] = TileCfg{bm, bn, sp};
+        ++n;
+    }
+    fclose(f);
+    if (n) g_status = "tile table from cache " + cache_path() + " (" + std::to_string(n) + " shapes)";
+}
+
+void save_cache_locked() {
+    std::string p = cache_path();
+    std::string dir = p.substr(0, p.rfind('/'));
+    std::string mk = "mkdir -p '" + dir + "'";
+    if (std::system(mk.c_str()) != 0) return;
+    FILE* f = fopen(p.c_str(), "w");
+    if (!f) return;
+    for (auto& kv : g_table)
+        fprintf(f, "TILE %d %d %d %d %d %d\n", std::get<0>(kv.first), std::get<1>(kv.first),
+                std::get<2>(kv.first), kv.second.bm, kv.second.bn, kv.second.split);
+    fclose(f);
+}
+
+float time_cfg(int M, int N, int K, const float* A, const float* B, float* C, const TileCfg& c,
+               hipStream_t s) {
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    if (!gemm_f32_cfg(M, N, K, A, B, C, c, s)) return 1e30f;  // warm
+    float best = 1e30f;
+    for (int r = 0; r < 3; ++r) {
+        hipEventRecord(e0, s);
+        for (int i = 0; i < 5; ++i) gemm_f32_cfg(M, N, K, A, B, C, c, s);
+        hipEventRecord(e1, s);
+        hipEventSynchronize(e1);
+        float ms = 0;
+        hipEventElapsedTime(&ms, e0, e1);
+        best = std::min(best, ms / 5);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return best;
+}
+
+}  // namespace
+
+TileCfg tuned_f32_tile(int M, int N, int K) {
+    bool run_now = false;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        load_cache_locked();
+        if (!g_busy) g_seen.insert(Key{M, N, K});
+        auto it = g_table.find(Key{M, N, K});
+        if (it != g_table.end()) return it->second;
+        static bool env_checked = false;
+        if (!env_checked && !g_busy) {
+            env_checked = true;
+            const char* e = std::getenv("ACFUN_AUTOTUNE");
+            run_now = e && std::atoi(e) > 0;
+        }
+    }
+    if (run_now) {
+        autotune_run();
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_table.find(Key{M, N, K});
+        if (it != g_table.end()) return it->second;
+    }
+    return default_f32_tile(M, N, K);
+}
+
+void autotune_run() {
+    std::set<Key> shapes;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        load_cache_locked();
+        if (g_busy) return;
+        g_busy = true;
+        shapes = g_seen;
+    }
+    if (const char* e = std::getenv("ACFUN_TUNE_SHAPES")) {
+        std::string s(e);
+        size_t pos = 0;
+        while (pos < s.size()) {
+            size_t nx = s.find(',', pos);
+            std::string t = s.substr(pos, nx == std::string::npos ? std::string::npos : nx - pos);
+            int M, N, K;
+            if (sscanf(t.c_str(), "%dx%dx%d", &M, &N, &K) == 3) shapes.insert(Key{M, N, K});
+            if (nx == std::string::npos) break;
+            pos = nx + 1;
+        }
+    }
+    if (shapes.empty()) shapes.insert(Key{1024, 1024, 1024});
+    hipStream_t s = lib_stream();
+    const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+    int tuned = 0;
+    for (const Key& k : shapes) {
+        int M = std::get<0>(k), N = std::get<1>(k), K = std::get<2>(k);
+        size_t bytes = sizeof(float) * ((size_t)M * K + (size_t)K * N + (size_t)M * N);
+        if (bytes > (size_t)4 << 30) continue;
+        Scratch a(sizeof(float) * (size_t)M * K, s), b(sizeof(float) * (size_t)K * N, s),
+            c(sizeof(float) * (size_t)M * N, s);
+        if (!a.p || !b.p || !c.p) continue;
+        hipMemsetAsync(a.p, 0, sizeof(float) * (size_t)M * K, s);
+        hipMemsetAsync(b.p, 0, sizeof(float) * (size_t)K * N, s);
+        TileCfg best = default_f32_tile(M, N, K);
+        float best_ms = time_cfg(M, N, K, a.as<float>(), b.as<float>(), c.as<float>(), best, s);
+        for (auto& cc : cand)
+            for (int sp : {1, 2, 4, 8}) {
+                if (sp > 1 && K < 256 * sp) continue;
+                TileCfg t{cc[0], cc[1], sp};
+                float ms = time_cfg(M, N, K, a.as<float>(), b.as<float>(), c.as<float>(), t, s);
+                if (ms < best_ms) { best_ms = ms; best = t; }
+            }
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_table[k] = best;
+        ++tuned;
+    }
+    hipStreamSynchronize(s);
+    std::lock_guard<std::mutex> lk(g_mu);
+    save_cache_locked();
+    g_busy = false;
+    g_status = "tile search: " + std::to_string(tuned) + " shapes tuned, cached at " + cache_path();
+}
+
+const char* tune_status() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    load_cache_locked();
+    return g_status.c_str();
+}
+
+}  // namespace acfun

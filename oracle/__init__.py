@@ -1,0 +1,204 @@
+"""CPU oracle for the acfun convolution/GEMM path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this package, and only as the checker or the CPU baseline; the product package
+(acfun_amd) never imports it.
+
+Two libraries live here:
+  * build/libacfun_oracle.so -- acfun_oracle.c, a plain-C restatement of the
+    reference arithmetic (each function cites the reference file:line);
+  * _ref/libacfun_ref.so     -- the reference compiled from its own sources by
+    ref.mk (present wherever it was built; it is the "reference" CPU baseline).
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(_HERE, "build", "libacfun_oracle.so")
+REF_SO = os.path.join(_HERE, "_ref", "libacfun_ref.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i, _f, _sz, _vp = C.c_int, C.c_float, C.c_size_t, C.c_void_p
+
+_lib = None
+_ref = None
+
+
+def lib():
+    """The C restatement (raises if it was not built: run `make -C oracle`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise FileNotFoundError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        L = C.CDLL(ORACLE_SO)
+        sig = {
+            "oracle_gemm": [_i, _i, _i, _f32p, _f32p, _f32p],
+            "oracle_gemm_epi": [_i, _i, _i, _f32p, _f32p, _f32p, _vp, _i],
+            "oracle_gemm_f64": [_i, _i, _i, _f32p, _f32p, _f64p],
+            "oracle_conv2d_route": [_i] * 10,
+            "oracle_conv2d_f64": [_f32p, _i, _i, _i, _i, _f32p, _vp, _i, _i, _i, _i, _i, _i, _f64p, _i],
+            "oracle_conv2d_dw": [_f32p, _i, _i, _i, _i, _f32p, _vp, _i, _i, _i, _i, _f32p, _i],
+            "oracle_conv2d_grouped": [_f32p, _i, _i, _i, _i, _f32p, _vp, _i, _i, _i, _i, _i, _i, _f32p, _i],
+            "oracle_maxpool": [_f32p, _i, _i, _i, _i, _i, _i, _i, _f32p, _i],
+            "oracle_relu": [_f32p, _sz],
+            "oracle_relu6": [_f32p, _sz],
+            "oracle_softmax": [_f32p, _i, _i, _f32p],
+            "oracle_batchnorm": [_f32p, _i, _i, _f32p, _f32p, _vp, _vp, _f],
+            "oracle_fold_bn": [_f32p, _f32p, _i, _i, _sz, _i, _f32p, _f32p, _f32p, _f32p],
+            "oracle_quantize_weights": [_f32p, _i, _i, _f32p, _i8p],
+            "oracle_absmax": [_f32p, _sz],
+            "oracle_quantize_u8": [_f32p, _u8p, _sz, _f, _i, _i],
+            "oracle_gemm_int8": [_i, _i, _i, _u8p, _i8p, _i32p],
+            "oracle_gemm_int8_epi": [_i, _i, _i, _u8p, _i8p, _f32p, _f32p, _f32p, _i],
+            "oracle_conv1x1_int8": [_u8p, _i, _i, _i, _i8p, _f32p, _f32p, _f32p, _i],
+            "oracle_conv2d_int8_direct": [_u8p, _i, _i, _i, _i, _i8p, _f32p, _f32p,
+                                          _i, _i, _i, _i, _i, _i, _i, _f32p, _i],
+            "oracle_winograd_conv3x3_int8": [_f32p, _i, _i, _i, _i, _i8p, _f32p, _vp, _i,
+                                             _f, _f, _f32p, _i],
+            "oracle_conv_int8_centered_acc": [_u8p, _i, _i, _i, _i, _i8p, _i, _i, _i, _i, _i,
+                                              _i, _i, _i32p],
+            "oracle_conv2d_int8_route": [_i] * 8,
+            "oracle_conv2d_int8": [_f32p, _i, _i, _i, _i, _i8p, _f32p, _vp, _i, _i, _i, _i, _i,
+                                   _f, _f32p, _i],
+            "oracle_requantize_s8": [_f32p, _sz, _i8p],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        L.oracle_conv2d_route.restype = _i
+        L.oracle_conv2d_int8_route.restype = _i
+        L.oracle_absmax.restype = _f
+        L.oracle_requantize_s8.restype = _f
+        _lib = L
+    return _lib
+
+
+def ref():
+    """The compiled reference library, or None where it was not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        _ref = C.CDLL(REF_SO)
+    return _ref
+
+
+def ptr(a):
+    """ctypes void* of a numpy array, or None for None (a NULL bias)."""
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def out_hw(H, W, KH, KW, stride, pad):
+    return (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+
+
+# ---- numpy-level wrappers (shapes as the reference API takes them) ----------
+
+def gemm(A, B):
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float32)
+    lib().oracle_gemm(M, N, K, A, B, Cm)
+    return Cm
+
+
+def gemm_f64(A, B):
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float64)
+    lib().oracle_gemm_f64(M, N, K, A, B, Cm)
+    return Cm
+
+
+def conv2d_f64(x, w, b, KH, KW, Cout, stride, pad, groups=1, act=0):
+    N, H, W, Cin = x.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    out = np.zeros((N, max(OH, 0), max(OW, 0), Cout), np.float64)
+    lib().oracle_conv2d_f64(x, N, H, W, Cin, w, ptr(b), KH, KW, Cout, stride, pad, groups, out, act)
+    return out
+
+
+def conv2d_dw(x, w, b, KH, KW, stride, pad, act):
+    N, H, W, Cc = x.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    out = np.zeros((N, OH, OW, Cc), np.float32)
+    lib().oracle_conv2d_dw(x, N, H, W, Cc, w, ptr(b), KH, KW, stride, pad, out, act)
+    return out
+
+
+def conv2d_grouped(x, w, b, KH, KW, Cout, stride, pad, groups, act):
+    N, H, W, Cin = x.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    out = np.zeros((N, OH, OW, Cout), np.float32)
+    lib().oracle_conv2d_grouped(x, N, H, W, Cin, w, ptr(b), KH, KW, Cout, stride, pad, groups, out, act)
+    return out
+
+
+def maxpool(x, pool, stride, pad, post_relu=0):
+    N, H, W, Cc = x.shape
+    OH, OW = out_hw(H, W, pool, pool, stride, pad)
+    out = np.zeros((N, OH, OW, Cc), np.float32)
+    lib().oracle_maxpool(x, N, H, W, Cc, pool, stride, pad, out, post_relu)
+    return out
+
+
+def quantize_weights(w2d):
+    K, N = w2d.shape
+    s = np.empty(N, np.float32)
+    q = np.empty((K, N), np.int8)
+    lib().oracle_quantize_weights(np.ascontiguousarray(w2d, np.float32), K, N, s, q)
+    return s, q
+
+
+def quantize_u8(x, inv_s, zp=128, mode=0):
+    xf = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(xf.size, np.uint8)
+    lib().oracle_quantize_u8(xf, out, xf.size, inv_s, zp, mode)
+    return out.reshape(np.shape(x))
+
+
+def gemm_int8(A, B):
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.int32)
+    lib().oracle_gemm_int8(M, N, K, A, B, Cm)
+    return Cm
+
+
+def gemm_int8_epi(A, B, alpha, beta, act):
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float32)
+    lib().oracle_gemm_int8_epi(M, N, K, A, B, Cm, alpha, beta, act)
+    return Cm
+
+
+def conv2d_int8(x, wq, ws, b, KH, KW, Cout, stride, pad, act, s_in=0.0):
+    N, H, W, Cin = x.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    out = np.zeros((N, max(OH, 0), max(OW, 0), Cout), np.float32)
+    lib().oracle_conv2d_int8(x, N, H, W, Cin, wq, ws, ptr(b), KH, KW, Cout, stride, pad,
+                             s_in, out, act)
+    return out
+
+
+def conv2d_int8_route(H, W, Cin, KH, KW, Cout, stride, pad):
+    return lib().oracle_conv2d_int8_route(H, W, Cin, KH, KW, Cout, stride, pad)
+
+
+def conv2d_route(N, H, W, Cin, KH, KW, Cout, stride, pad, groups):
+    return lib().oracle_conv2d_route(N, H, W, Cin, KH, KW, Cout, stride, pad, groups)
+
+
+def fold_bn(w, b, Cout, groups, mean, var, gamma, beta):
+    """Returns folded copies (w', b') per fold_bn_into (src/model.cpp:69-95)."""
+    w2 = np.array(w, np.float32, copy=True).ravel()
+    has_b = b is not None
+    b2 = np.array(b if has_b else np.zeros(Cout), np.float32, copy=True)
+    lib().oracle_fold_bn(w2, b2, int(has_b), Cout, w2.size, groups, mean, var, gamma, beta)
+    return w2, b2

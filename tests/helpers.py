@@ -1,0 +1,54 @@
+"""Shared test helpers: pointers, seeded inputs, comparisons."""
+import ctypes as C
+
+import numpy as np
+
+
+def P(a):
+    """void* of a numpy array (None passes through as NULL)."""
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def u8(rng, shape):
+    return rng.integers(0, 256, size=shape, dtype=np.uint8)
+
+
+def s8(rng, shape, lo=-128, hi=127):
+    return rng.integers(lo, hi + 1, size=shape).astype(np.int8)
+
+
+def rel_err(got, want):
+    """Normwise relative error max|got-want| / max|want| (the fp32 tolerance measure)."""
+    want = np.asarray(want, np.float64)
+    d = np.max(np.abs(np.asarray(got, np.float64) - want)) if want.size else 0.0
+    den = np.max(np.abs(want)) if want.size else 1.0
+    return d / (den if den > 0 else 1.0)
+
+
+def assert_bitexact(got, want, what=""):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    if got.dtype.kind == "f":
+        same = (got == want) | (np.isnan(got) & np.isnan(want))
+    else:
+        same = got == want
+    if not np.all(same):
+        idx = np.argwhere(~same)[:5]
+        raise AssertionError(f"{what}: {np.count_nonzero(~same)} of {got.size} differ; first at "
+                             f"{idx.tolist()}: got {got[tuple(idx[0])]!r} want {want[tuple(idx[0])]!r}")
+
+
+def int8_conv_inputs(rng, N, H, W, Cin, KH, KW, Cout, bias=True):
+    """Config-3 style inputs: x = q_a * s_a with q_a ~ U{-127..127}, wq ~ U{-127..127},
+    ws ~ U[0.005, 0.05], b ~ N(0, 0.01)."""
+    sa = np.float32(rng.uniform(0.005, 0.05))
+    x = (rng.integers(-127, 128, size=(N, H, W, Cin)).astype(np.float32) * sa).astype(np.float32)
+    wq = rng.integers(-127, 128, size=(KH * KW * Cin, Cout)).astype(np.int8)
+    ws = rng.uniform(0.005, 0.05, Cout).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32) if bias else None
+    return x, wq, ws, b
