@@ -95,9 +95,20 @@ _lib = None
 
 
 def lib():
-    """The product library (raises when it has not been built)."""
+    """The product library (raises when it has not been built).
+
+    torch is imported first when it is installed: it bundles its own HIP
+    runtime under the same soname (libamdhip64.so.7) as the ROCm one this
+    library links, and the first one loaded serves the whole process.  Loading
+    torch's first keeps one runtime in the process, so torch tensors and this
+    library share devices, streams and allocations.
+    """
     global _lib
     if _lib is None:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"{LIB_PATH} is missing: build it with "
                               "`python -c 'import __graft_entry__ as g; g.build()'`")

@@ -339,7 +339,7 @@ bool aligned16(const void* q) { return ((uintptr_t)q & 15u) == 0; }
 template <bool CONV>
 bool run(GemmP p, int batch, bool va, bool vb, hipStream_t s, const TileCfg* force = nullptr) {
     if (p.M <= 0 || p.N <= 0) return true;
-    TileCfg c = force ? *force : tuned_f32_tile(p.M, p.N, p.K);
+    TileCfg c = force ? *force : tuned_f32_tile(p.M, p.N, p.K, batch);
     if (batch > 1) c.split = 1;
     int splits = c.split < 1 ? 1 : c.split;
     int kchunk = (p.K + splits - 1) / splits;
@@ -374,13 +374,16 @@ bool run(GemmP p, int batch, bool va, bool vb, hipStream_t s, const TileCfg* for
 
 }  // namespace
 
-TileCfg default_f32_tile(int M, int N, int K) {
+TileCfg default_f32_tile(int M, int N, int K, int batch) {
     const int cus = num_cus();
     const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
     for (auto& c : cand) {
-        long long tiles = (long long)((M + c[0] - 1) / c[0]) * ((N + c[1] - 1) / c[1]);
+        if (c[1] > 64 && N <= 64) continue;   // half of every tile would be padding
+        if (c[0] > 64 && M <= 64) continue;
+        long long tiles = (long long)((M + c[0] - 1) / c[0]) * ((N + c[1] - 1) / c[1]) * batch;
         if (tiles >= cus) return TileCfg{c[0], c[1], 1};
     }
+    if (batch > 1) return TileCfg{64, 64, 1};
     long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
     int split = 1;
     if (tiles * 2 <= cus && K >= 512) {

@@ -7,11 +7,10 @@
 // (src/winograd.cpp:9-17, src/winograd43.cpp:33-54):
 //   d_hat = BT d BT^T (input tile), g_hat = G g G^T (filter), Y = AT M AT^T.
 //
-// Pipeline on the device (T = tiles, A = 16 or 36 transform points):
-//   1. filter transform  U[a][Cin][Cout]   (per call, like the reference)
-//   2. input transform   V[a][T][Cin]      one lane per (tile, channel)
-//   3. A independent GEMMs M[a] = V[a] * U[a] on fp32 MFMA (batched launch)
-//   4. output transform  Y = AT M AT^T + bias (+ReLU) written straight to NHWC
+// Two kernels per call: the filter transform U = G g G^T (per call, like the
+// reference, :195-206) and one fused kernel doing input transform, the P =
+// 16 (36) transform-point GEMMs on fp32 MFMA and the output transform with
+// bias and ReLU, so the input is read once and the output written once.
 #include "rt.hpp"
 
 namespace acfun {
@@ -154,119 +153,526 @@ template <> struct Wino<4> {
     }
 };
 
-// U[a][c][o], weight[(k*Cin + c)*Cout + o] with k = kh*3 + kw.
+// Filter transform into the fused kernel's layout U[a][Cout][Cinp]: for each
+// transform point a and output channel o, the Cinp (= Cin rounded up to 16)
+// input channels are contiguous and zero-padded, so one lane fetches four
+// k-steps of an MFMA B operand with a single 16-byte load.
 template <int TILE>
-__global__ void k_wino_filter(const float* __restrict__ w, int Cin, int Cout, float* __restrict__ U) {
+__global__ void k_wino_filter_t(const float* __restrict__ w, int Cin, int Cinp, int Cout,
+                                float* __restrict__ U) {
     constexpr int A = Wino<TILE>::A;
     int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= Cin * Cout) return;
-    int c = idx / Cout, o = idx - c * Cout;
-    float g[3][3];
-#pragma unroll
-    for (int kh = 0; kh < 3; ++kh)
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw) g[kh][kw] = w[((long long)(kh * 3 + kw) * Cin + c) * Cout + o];
+    if (idx >= Cinp * Cout) return;
+    int o = idx / Cinp, c = idx - o * Cinp;
     float gh[A][A];
-    Wino<TILE>::f_tf(g, gh);
-    long long plane = (long long)Cin * Cout;
+    if (c < Cin) {
+        float g[3][3];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) g[kh][kw] = w[((long long)(kh * 3 + kw) * Cin + c) * Cout + o];
+        Wino<TILE>::f_tf(g, gh);
+    } else {
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) gh[i][j] = 0.f;
+    }
+    long long plane = (long long)Cout * Cinp;
 #pragma unroll
     for (int i = 0; i < A; ++i)
 #pragma unroll
         for (int j = 0; j < A; ++j) U[(i * A + j) * plane + idx] = gh[i][j];
 }
 
-// V[a][t][c]: tile t = (n, ty, tx), origin (TILE*ty - 1, TILE*tx - 1).
-template <int TILE>
-__global__ void k_wino_input(const float* __restrict__ in, int N, int H, int W, int Cin, int tH,
-                             int tW, float* __restrict__ V) {
-    constexpr int A = Wino<TILE>::A;
-    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    long long T = (long long)N * tH * tW;
-    if (idx >= T * Cin) return;
-    int c = (int)(idx % Cin);
-    long long t = idx / Cin;
-    int tx = (int)(t % tW);
-    long long r = t / tW;
-    int ty = (int)(r % tH);
-    int n = (int)(r / tH);
-    const float* img = in + (long long)n * H * W * Cin + c;
-    float d[A][A];
-    int ih0 = ty * TILE - 1, iw0 = tx * TILE - 1;
-#pragma unroll
-    for (int i = 0; i < A; ++i)
-#pragma unroll
-        for (int j = 0; j < A; ++j) {
-            int ih = ih0 + i, iw = iw0 + j;
-            d[i][j] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? img[((long long)ih * W + iw) * Cin] : 0.f;
-        }
-    float dh[A][A];
-    Wino<TILE>::in_tf(d, dh);
-    long long plane = T * Cin;
-#pragma unroll
-    for (int i = 0; i < A; ++i)
-#pragma unroll
-        for (int j = 0; j < A; ++j) V[(i * A + j) * plane + idx] = dh[i][j];
-}
+typedef float f4 __attribute__((ext_vector_type(4)));
 
-template <int TILE>
-__global__ void k_wino_output(const float* __restrict__ Mm, int N, int OH, int OW, int Cout,
-                              int tH, int tW, const float* __restrict__ bias,
-                              float* __restrict__ out, int act) {
+// Fused Winograd: one workgroup = TB consecutive tiles (flattened n,ty,tx
+// order) x CB = 16*NW output channels; wave w owns output channels
+// 16w..16w+15 of the block and every tile of it, so for each transform point
+// a its accumulators hold M[a][tile][o] with lane l, register r <-> tile
+// 4*(l/16)+r, channel l%16 (the 16x16 MFMA D layout).  Input channels are
+// consumed in chunks of KC, software-pipelined:
+//   while the MFMAs of chunk k read d_hat (sV) and the filter chunk (sU) from
+//   LDS, the raw input patches and the filter slice of chunk k+1 are already
+//   in flight into registers; then the patches are transformed into sV and
+//   the filter slice stored into sU for the next round.
+// LDS rows hold KC channels plus 4 floats of padding, so the 16 rows touched
+// by one ds_read_b128 land in distinct banks; one b128 read gives a lane four
+// MFMA k-steps (channel 4*(l/16)+s of the chunk, s = 0..3, for both operands).
+// After the last chunk the output transform, bias and ReLU run in registers.
+template <int TILE, int TB, int NW, int KC>
+__global__ __launch_bounds__(64 * NW) void k_wino_fused(
+    const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
+    float* __restrict__ out, int N, int H, int W, int Cin, int Cinp, int Cout, int tH, int tW,
+    int act) {
     constexpr int A = Wino<TILE>::A;
-    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    long long T = (long long)N * tH * tW;
-    if (idx >= T * Cout) return;
-    int o = (int)(idx % Cout);
-    long long t = idx / Cout;
-    int tx = (int)(t % tW);
-    long long r = t / tW;
-    int ty = (int)(r % tH);
-    int n = (int)(r / tH);
-    long long plane = T * Cout;
-    float m[A][A];
+    constexpr int P = A * A;
+    constexpr int FB = TB / 16;
+    constexpr int NT = 64 * NW;
+    constexpr int CB = 16 * NW;
+    constexpr int LDV = KC + 4;
+    constexpr int KQ = KC / 4;                        // float4 per (a, channel-row) of a chunk
+    constexpr int VEC = KC / 4;                       // k-steps per LDS read (4: b128, 2: b64)
+    constexpr int UV = (P * CB * KQ + NT - 1) / NT;   // filter float4 per thread per chunk
+    constexpr int XV = (TB * KC + NT - 1) / NT;       // (tile, channel) patches per thread
+    static_assert(KC == 8 || KC == 16, "one LDS read covers the chunk's 4 lane groups");
+    __shared__ __attribute__((aligned(16))) float sV[P * TB * LDV];
+    __shared__ __attribute__((aligned(16))) float sU[P * CB * LDV];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long long T = (long long)N * tH * tW;
+    const long long tile0 = (long long)blockIdx.x * TB;
+    const int cob = blockIdx.y * CB;
+    const long long uplane = (long long)Cout * Cinp;
+
+    // ---- per-thread patch bookkeeping (fixed over chunks)
+    const float* xbase[XV];
+    int xih0[XV], xiw0[XV], xt[XV], xc[XV];
+    bool xok[XV];
 #pragma unroll
-    for (int i = 0; i < A; ++i)
+    for (int v = 0; v < XV; ++v) {
+        int idx = tid + v * NT;
+        int t = idx / KC, c = idx - (idx / KC) * KC;
+        xt[v] = t;
+        xc[v] = c;
+        long long tile = tile0 + t;
+        xok[v] = idx < TB * KC && tile < T;
+        long long tl = xok[v] ? tile : 0;
+        int tx = (int)(tl % tW);
+        long long r = tl / tW;
+        int ty = (int)(r % tH);
+        int n = (int)(r / tH);
+        xbase[v] = in + (long long)n * H * W * Cin + c;
+        xih0[v] = ty * TILE - 1;
+        xiw0[v] = tx * TILE - 1;
+    }
+    float xr[XV][A][A];
+    f4 ur[UV];
+
+    auto load_chunk = [&](int c0) {
 #pragma unroll
-        for (int j = 0; j < A; ++j) m[i][j] = Mm[(i * A + j) * plane + idx];
-    float y[TILE][TILE];
-    Wino<TILE>::out_tf(m, y);
-    float b = bias ? bias[o] : 0.f;
+        for (int v = 0; v < XV; ++v) {
+            bool ok = xok[v] && (c0 + xc[v]) < Cin;
 #pragma unroll
-    for (int i = 0; i < TILE; ++i)
+            for (int i = 0; i < A; ++i)
 #pragma unroll
-        for (int j = 0; j < TILE; ++j) {
-            int oh = ty * TILE + i, ow = tx * TILE + j;
-            if (oh < OH && ow < OW) {
-                float v = y[i][j] + b;
-                if (act == 1) v = v > 0.f ? v : 0.f;
-                out[(((long long)n * OH + oh) * OW + ow) * Cout + o] = v;
+                for (int j = 0; j < A; ++j) {
+                    int ih = xih0[v] + i, iw = xiw0[v] + j;
+                    xr[v][i][j] = (ok && ih >= 0 && ih < H && iw >= 0 && iw < W)
+                                      ? xbase[v][((long long)ih * W + iw) * Cin + c0] : 0.f;
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < UV; ++u) {
+            int idx = tid + u * NT;                    // (a, co, q) with q fastest
+            int q = idx % KQ;
+            int row = idx / KQ;                        // a*CB + co_local
+            int a = row / CB, col = row - a * CB;
+            f4 val = {0.f, 0.f, 0.f, 0.f};
+            if (idx < P * CB * KQ && cob + col < Cout)
+                val = *(const f4*)(U + a * uplane + (long long)(cob + col) * Cinp + c0 + q * 4);
+            ur[u] = val;
+        }
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int v = 0; v < XV; ++v) {
+            if (tid + v * NT >= TB * KC) continue;
+            float dh[A][A];
+            Wino<TILE>::in_tf(xr[v], dh);
+#pragma unroll
+            for (int i = 0; i < A; ++i)
+#pragma unroll
+                for (int j = 0; j < A; ++j) sV[((i * A + j) * TB + xt[v]) * LDV + xc[v]] = dh[i][j];
+        }
+#pragma unroll
+        for (int u = 0; u < UV; ++u) {
+            int idx = tid + u * NT;
+            if (idx >= P * CB * KQ) continue;
+            int q = idx % KQ;
+            int row = idx / KQ;
+            *(f4*)&sU[row * LDV + q * 4] = ur[u];
+        }
+    };
+
+    f4 acc[P][FB];
+#pragma unroll
+    for (int a = 0; a < P; ++a)
+#pragma unroll
+        for (int b = 0; b < FB; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int lr = lane & 15, lg = lane >> 4;
+    load_chunk(0);
+    for (int c0 = 0; c0 < Cinp; c0 += KC) {
+        __syncthreads();          // previous chunk's MFMAs are done with sV / sU
+        store_chunk();
+        if (c0 + KC < Cinp) load_chunk(c0 + KC);   // in flight during the MFMAs below
+        __syncthreads();
+        // lane group g = l/16 supplies channel VEC*g + s to MFMA step s
+#pragma unroll
+        for (int a = 0; a < P; ++a) {
+            typedef float fv __attribute__((ext_vector_type(VEC)));
+            fv bfr = *(const fv*)&sU[(a * CB + wave * 16 + lr) * LDV + lg * VEC];
+#pragma unroll
+            for (int b = 0; b < FB; ++b) {
+                fv afr = *(const fv*)&sV[(a * TB + b * 16 + lr) * LDV + lg * VEC];
+#pragma unroll
+                for (int s = 0; s < VEC; ++s)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(afr[s], bfr[s], acc[a][b], 0, 0, 0);
             }
         }
+    }
+
+    // ---- output transform + bias + ReLU in registers
+    const int co = cob + wave * 16 + lr;
+    if (co >= Cout) return;
+    const float bv = bias ? bias[co] : 0.f;
+#pragma unroll
+    for (int b = 0; b < FB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            long long tile = tile0 + b * 16 + (lane >> 4) * 4 + r;
+            if (tile >= T) continue;
+            int tx = (int)(tile % tW);
+            long long q = tile / tW;
+            int ty = (int)(q % tH);
+            int n = (int)(q / tH);
+            float m[A][A];
+#pragma unroll
+            for (int i = 0; i < A; ++i)
+#pragma unroll
+                for (int j = 0; j < A; ++j) m[i][j] = acc[i * A + j][b][r];
+            float y[TILE][TILE];
+            Wino<TILE>::out_tf(m, y);
+#pragma unroll
+            for (int i = 0; i < TILE; ++i)
+#pragma unroll
+                for (int j = 0; j < TILE; ++j) {
+                    int oh = ty * TILE + i, ow = tx * TILE + j;
+                    if (oh < H && ow < W) {
+                        float v = y[i][j] + bv;
+                        if (act == 1) v = v > 0.f ? v : 0.f;
+                        out[(((long long)n * H + oh) * W + ow) * Cout + co] = v;
+                    }
+                }
+        }
 }
 
-template <int TILE>
-bool run_wino(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
-              int Cout, float* out, int act, hipStream_t s) {
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 256 zero bytes in global memory: DMA source for padding pixels/channels.
+__device__ __attribute__((aligned(256))) float g_wino_zero[64];
+
+// F(2,3) on v_mfma_f32_32x32x2f32, input and filter staged by LDS DMA.
+//
+// Workgroup (512 threads) = one image's tile rows ty0..ty0+R-1 x tile
+// columns tx0..tx0+TC-1 (R*TC <= 128 tile slots) x 32 output channels.
+// Waves 2p and 2p+1 form pair p, owning tile slots 32p..32p+31; wave 2p+h
+// keeps the accumulators of the 8 transform points in rows i = 2h, 2h+1 of
+// the 4x4 transform grid (8 x 16 AGPRs), so two waves share each SIMD and one
+// wave's MFMAs overlap the other's LDS reads and transforms.
+//
+// Input channels are consumed in chunks of 16.  Per chunk the workgroup DMAs
+// (global_load_lds_dwordx4, no VGPRs) into one of two LDS buffers:
+//   X: the 2R+2 pixel rows x 2TC+2 columns the block's 4x4 patches touch,
+//      as [row][col%2][col/2][4 channel quads], quad q of pixel column index
+//      k stored at quad slot q ^ ((k>>2)&3);
+//   U: the filter chunk [16 points][32 channels][4 quads], quad q of channel
+//      row co stored at slot q ^ ((co>>2)&3).
+// The XOR swizzles keep DMA destinations contiguous while the 16 rows read
+// by a ds_read_b128 lane group fall on distinct banks.  Chunk k+1's DMAs are
+// issued between chunk k's MFMAs and fly while it is computed.  Per 8-channel
+// half, lane l reads the pixel rows of its tile's 4x4 patch that its
+// transform rows need (channel quad 4*(l/32)), applies BT per column, and
+// each row of d_hat feeds its 4 points x 4 k-steps (k-step s <-> channel
+// 4*(l/32)+s, as in the B operand).
+// Epilogue: the output transform is linear, so each wave forms the partial
+// 2x2 outputs of its 8 points into one of two LDS output tiles; all threads
+// then sum the tiles, add bias, apply ReLU and store 16-byte channel quads.
+__global__ __launch_bounds__(512) void k_wino23(
+    const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
+    float* __restrict__ out, int N, int H, int W, int Cin, int Cinp, int Cout, int tH, int tW,
+    int R, int TC, int act) {
+    constexpr int KC = 16;
+    constexpr int NT = 512;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
+    const int pair = wave >> 1, hr = wave & 1;
+    const int g = lane >> 5, li = lane & 31;
+    const int TCP = TC + 1;
+    const int nrow = 2 * R + 2;
+    // X region rounded up to whole 64-slot DMA blocks: the last block's lanes
+    // past the region land in this padding, never in the U region.
+    const int xfl = (nrow * 2 * TCP * 4 + 63) / 64 * 64 * 4;
+    const int bufsz = xfl + 16 * 32 * 16;                // X + U floats per buffer
+    const int rblocks = (tH + R - 1) / R;
+    const int n = blockIdx.y / rblocks;
+    const int ty0 = (blockIdx.y - n * rblocks) * R;
+    const int tx0 = blockIdx.x * TC;
+    const int cob = blockIdx.z * 32;
+    const long long uplane = (long long)Cout * Cinp;
+    const float* __restrict__ img = in + (long long)n * H * W * Cin;
+
+    f16v acc[8];                                         // points 8*hr .. 8*hr+7
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+
+    // ---- DMA descriptors.  Wave w issues X blocks w, w+8, ... (64 slots of
+    // 16 bytes each); lane l of block k covers slot 64k+l, i.e. pixel index
+    // pix0 + 128k with pix = (row*2 + plane)*TCP + kk.  kk and row*2+plane of
+    // block 0 are computed once; later blocks step them by 128 = dr*TCP + dk.
+    // Filter slots advance by 4 points (4 * Cout * Cinp floats) per block, so
+    // one offset serves all of them.
+    constexpr int KXM = 9;
+    const int xslots = nrow * 2 * TCP * 4;
+    const int pix0 = (wave * 64 + lane) >> 2;
+    const int kk0 = pix0 % TCP, rp0 = pix0 / TCP;
+    const int dk = 128 % TCP, dr = 128 / TCP;
+    const int sq = lane & 3;
+    const int ih0 = 2 * ty0 - 1, iw0 = 2 * tx0 - 1;
+    int ud;
+    {
+        int row = (wave * 64 + lane) >> 2;                // a*32 + co, a < 4
+        int co = row & 31;
+        int q = (lane & 3) ^ ((co >> 2) & 3);
+        ud = cob + co < Cout ? (int)((row >> 5) * uplane) + (cob + co) * Cinp + 4 * q : -1;
+    }
+    const long long ustep = 4 * uplane;
+    const int nxb = (xslots + 63) / 64;                   // X blocks per chunk
+    const float* zero = g_wino_zero;
+    // DMA item t of a chunk: t < KU are this wave's filter blocks (the 16 x
+    // 32 x 4 quads of a chunk are 32 blocks, KU = 4 per wave), t >= KU its X
+    // block t-KU (kk, rp carry the X walk from item to item).
+    constexpr int KU = 16 * 32 * 4 / NT;
+    constexpr int NITEM = KU + KXM;
+    static_assert(NITEM <= 16, "DMA items are issued after the 16 MFMA groups of a chunk");
+    auto dma_item = [&](int t, int c0, float* base, int& kk, int& rp) {
+        if (t < KU) {
+            const float* src = ud >= 0 ? U + ud + c0 + t * ustep : zero;
+            __builtin_amdgcn_global_load_lds((const void*)src,
+                                             (lds_void*)(base + xfl + (wave + 8 * t) * 256), 16, 0, 0);
+            return;
+        }
+        const int blk = wave + 8 * (t - KU);
+        if (blk < nxb) {
+            int q = sq ^ ((kk >> 2) & 3);
+            int ih = ih0 + (rp >> 1);
+            int iw = iw0 + 2 * kk + (rp & 1);
+            bool ok = rp < 2 * nrow && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W &&
+                      c0 + 4 * q < Cin;
+            const float* src = ok ? img + (ih * W + iw) * Cin + 4 * q + c0 : zero;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(base + blk * 256), 16, 0, 0);
+        }
+        kk += dk;
+        rp += dr;
+        if (kk >= TCP) { kk -= TCP; ++rp; }
+    };
+
+    // this lane's MFMA row (tile slot)
+    const int slot = pair * 32 + li;
+    const int sr = slot / TC, stx = slot - sr * TC;
+    const int srr = sr < R ? sr : 0;
+    const int usw = (li >> 2) & 3;                        // U swizzle of row li
+    const int rA = 2 * hr, rB = 2 - hr, rC = 1 + 2 * hr;
+    const int smask = hr << 31;                           // sign flip of dB for hr = 1
+
+    // Compute chunk buffer b; when c0n >= 0 also issue the DMA items of the
+    // next chunk (channels c0n.., buffer bn), one after each group of 4 MFMAs,
+    // so the address traffic is spread over the chunk instead of stalling all
+    // waves after the barrier.
+    auto compute = [&](int b, int c0n, int bn) {
+        const float* X = smem + b * bufsz;
+        float* nbase = smem + bn * bufsz;
+        int kk = kk0, rp = rp0;
+        const float* Ub = X + xfl;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int q = 2 * h + g;
+            f4 bf[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                bf[a] = *(const f4*)&Ub[(((8 * hr + a) * 32 + li) * 4 + (q ^ usw)) * 4];
+            // BT rows 2hr, 2hr+1 of the patch column: hr = 0 gives d0-d2 and
+            // d1+d2, hr = 1 gives d2-d1 and d3-d1, i.e. dA-dB and dC+(+-dB)
+            // with A = 2hr, B = 2-hr, C = 1+2hr (wave-uniform row choice, no
+            // branch between the reads).
+            f4 t[2][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = stx + (j >> 1);
+                const int qs = q ^ ((k >> 2) & 3);
+                auto px = [&](int i) {
+                    return *(const f4*)&X[((((2 * srr + i) * 2 + (j & 1)) * TCP + k) * 4 + qs) * 4];
+                };
+                f4 dA = px(rA), dB = px(rB), dC = px(rC);
+                f4 dBs;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    dBs[e] = __int_as_float(__float_as_int(dB[e]) ^ smask);
+                t[0][j] = dA - dB;
+                t[1][j] = dC + dBs;
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                f4 dh[4];
+                dh[0] = t[i][0] - t[i][2];
+                dh[1] = t[i][1] + t[i][2];
+                dh[2] = t[i][2] - t[i][1];
+                dh[3] = t[i][3] - t[i][1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int a = i * 4 + j;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(dh[j][s], bf[a][s], acc[a], 0, 0, 0);
+                    const int item = h * 8 + a;
+                    if (item < NITEM && c0n >= 0) dma_item(item, c0n, nbase, kk, rp);
+                }
+            }
+        }
+    };
+
+    const int nch = Cinp / KC;
+    {
+        int kk = kk0, rp = rp0;
+#pragma unroll
+        for (int t = 0; t < NITEM; ++t) dma_item(t, 0, smem, kk, rp);
+    }
+    for (int ch = 0; ch < nch; ++ch) {
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs for chunk ch have landed
+        __syncthreads();                 // ... and every other wave's; buffer ch+1 is free
+        compute(ch & 1, ch + 1 < nch ? (ch + 1) * KC : -1, (ch + 1) & 1);
+    }
+
+    // ---- epilogue.  Lane l, register r <-> MFMA row 8*(r/4)+4*(l/32)+r%4, channel l%32.
+    // S_i[c] = sum_j AT[c][j] M[i][j]; Y[0][c] = S0+S1+S2, Y[1][c] = S1-S2+S3.
+    // Wave 2p+h writes the partial 2x2 outputs of its transform rows into
+    // output tile h in LDS ([2R rows][2TC cols][32 channels] each); then every
+    // thread adds the two tiles, bias and ReLU and stores 16-byte quads
+    // (32 output channels = 128 contiguous bytes per pixel).  Divisions by
+    // the runtime TC use a float reciprocal: numerators stay below 2^9 and
+    // sit at least 1/256 from an integer quotient, far above float rounding.
+    __syncthreads();                     // staging buffers are free
+    const int OW2 = 2 * TC;
+    const int tile = 2 * R * OW2 * 32;   // floats per output tile
+    const float rtc = 1.0f / (float)TC, rw2 = 0.5f * rtc;
+    {
+        float* so = smem + hr * tile;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            int os = pair * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            int orr = (int)(((float)os + 0.5f) * rtc), otx = os - orr * TC;
+            if (orr >= R) continue;
+            float S[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float m0 = acc[i * 4 + 0][r], m1 = acc[i * 4 + 1][r];
+                float m2 = acc[i * 4 + 2][r], m3 = acc[i * 4 + 3][r];
+                S[i][0] = m0 + m1 + m2;
+                S[i][1] = m1 - m2 + m3;
+            }
+            float* p = so + ((2 * orr) * OW2 + 2 * otx) * 32 + li;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                // wave 2p holds S0,S1 (rows 0,1), wave 2p+1 holds S2,S3
+                p[c * 32] = hr == 0 ? S[0][c] + S[1][c] : S[0][c];
+                p[OW2 * 32 + c * 32] = hr == 0 ? S[1][c] : S[1][c] - S[0][c];
+            }
+        }
+    }
+    __syncthreads();
+    const int qd = tid & 7;              // channel quad: fixed, since NT % 8 == 0
+    const int c = cob + 4 * qd;
+    f4 bq = {0.f, 0.f, 0.f, 0.f};
+    if (bias) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bq[t] = c + t < Cout ? bias[c + t] : 0.f;
+    }
+    const int nq = 2 * R * OW2 * 8;      // float4 quads of the output tile
+    for (int e = tid; e < nq; e += NT) {
+        int pxl = e >> 3;
+        int py = (int)(((float)pxl + 0.5f) * rw2), pxx = pxl - py * OW2;
+        int oh = 2 * ty0 + py, ow = 2 * tx0 + pxx;
+        if (oh >= H || ow >= W || c >= Cout) continue;
+        f4 v = *(const f4*)&smem[pxl * 32 + 4 * qd] + *(const f4*)&smem[tile + pxl * 32 + 4 * qd] + bq;
+        if (act == 1) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = v[t] > 0.f ? v[t] : 0.f;
+        }
+        float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + c;
+        if (c + 4 <= Cout && (Cout & 3) == 0) {
+            *(f4*)dst = v;
+        } else {
+            for (int t = 0; t < 4 && c + t < Cout; ++t) dst[t] = v[t];
+        }
+    }
+}
+
+bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+                int Cout, float* out, int act, hipStream_t s) {
+    int tH = (H + 1) / 2, tW = (W + 1) / 2;
+    int Cinp = (Cin + 15) / 16 * 16;
+    // The DMA staging moves whole 4-channel quads from 16-byte aligned rows.
+    if (Cin % 4 != 0 || ((uintptr_t)in & 15u) != 0) {
+        ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
+        return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
+    }
+    Scratch U((size_t)16 * Cout * Cinp * sizeof(float), s);
+    if (!U.p) return false;
+    hipLaunchKernelGGL(k_wino_filter_t<2>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w, Cin,
+                       Cinp, Cout, U.as<float>());
+    if (!check_launch("k_wino_filter_t")) return false;
+    // Block: TC tile columns x R tile rows of one image, R*TC <= 128 slots and
+    // two LDS buffers (padded X region + 16*32*16 filter floats) within 160 KB.
+    auto buf_floats = [](int R, int TC) {
+        return (size_t)(((2 * R + 2) * 2 * (TC + 1) * 4 + 63) / 64 * 64 * 4 + 16 * 32 * 16);
+    };
+    int TC = tW < 64 ? tW : 64;
+    int R = 128 / TC;
+    if (R > tH) R = tH;
+    while (R > 1 && 2 * sizeof(float) * buf_floats(R, TC) > 160 * 1024) --R;
+    size_t lds = 2 * sizeof(float) * buf_floats(R, TC);
+    // Each wave issues at most 9 X blocks of 64 slots per chunk, and two
+    // 2R x 2TC x 32 output tiles are staged in LDS by the epilogue.
+    size_t xblocks = ((size_t)(2 * R + 2) * 2 * (TC + 1) * 4 + 63) / 64;
+    if (lds > 160 * 1024 || xblocks > 8 * 9 || (size_t)256 * R * TC * sizeof(float) > lds) {
+        ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
+        return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
+    }
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        hipFuncSetAttribute((const void*)k_wino23, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }
+    int rblocks = (tH + R - 1) / R;
+    dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
+    hipLaunchKernelGGL(k_wino23, grid, dim3(512), lds, s, in, U.as<float>(), bias, out, N, H, W,
+                       Cin, Cinp, Cout, tH, tW, R, TC, act);
+    return check_launch("k_wino23");
+}
+
+template <int TILE, int TB, int NW, int KC>
+bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+               int Cout, float* out, int act, hipStream_t s) {
     constexpr int A = Wino<TILE>::A;
     constexpr int P = A * A;
     int tH = (H + TILE - 1) / TILE, tW = (W + TILE - 1) / TILE;
     long long T = (long long)N * tH * tW;
-    Scratch U((size_t)P * Cin * Cout * sizeof(float), s);
-    Scratch V((size_t)P * T * Cin * sizeof(float), s);
-    Scratch Mm((size_t)P * T * Cout * sizeof(float), s);
-    if (!U.p || !V.p || !Mm.p) return false;
-    hipLaunchKernelGGL(k_wino_filter<TILE>, dim3((Cin * Cout + 255) / 256), dim3(256), 0, s, w,
-                       Cin, Cout, U.as<float>());
-    if (!check_launch("k_wino_filter")) return false;
-    hipLaunchKernelGGL(k_wino_input<TILE>, dim3((unsigned)((T * Cin + 255) / 256)), dim3(256), 0, s,
-                       in, N, H, W, Cin, tH, tW, V.as<float>());
-    if (!check_launch("k_wino_input")) return false;
-    if (!gemm_f32_batched(P, (int)T, Cout, Cin, V.as<float>(), T * Cin, Cin, U.as<float>(),
-                          (long long)Cin * Cout, Cout, Mm.as<float>(), T * Cout, Cout, s))
-        return false;
-    hipLaunchKernelGGL(k_wino_output<TILE>, dim3((unsigned)((T * Cout + 255) / 256)), dim3(256), 0,
-                       s, Mm.as<float>(), N, H, W, Cout, tH, tW, bias, out, act);
-    return check_launch("k_wino_output");
+    int Cinp = (Cin + KC - 1) / KC * KC;
+    Scratch U((size_t)P * Cout * Cinp * sizeof(float), s);
+    if (!U.p) return false;
+    hipLaunchKernelGGL(k_wino_filter_t<TILE>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w,
+                       Cin, Cinp, Cout, U.as<float>());
+    if (!check_launch("k_wino_filter_t")) return false;
+    dim3 grid((unsigned)((T + TB - 1) / TB), (Cout + 16 * NW - 1) / (16 * NW));
+    hipLaunchKernelGGL((k_wino_fused<TILE, TB, NW, KC>), grid, dim3(64 * NW), 0, s, in, U.as<float>(),
+                       bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act);
+    return check_launch("k_wino_fused");
 }
 
 }  // namespace
@@ -274,8 +680,8 @@ bool run_wino(const float* in, int N, int H, int W, int Cin, const float* w, con
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
                   const float* bias, int Cout, float* out, int act, hipStream_t s) {
     if (N <= 0 || H <= 0 || W <= 0) return true;
-    return tile == 4 ? run_wino<4>(in, N, H, W, Cin, w, bias, Cout, out, act, s)
-                     : run_wino<2>(in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    if (tile == 4) return run_fused<4, 16, 4, 8>(in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    return run_wino23(in, N, H, W, Cin, w, bias, Cout, out, act, s);
 }
 
 }  // namespace acfun

@@ -151,8 +151,8 @@ bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float
 
 // Tile-config table (autotune).
 struct TileCfg { int bm, bn, split; };
-TileCfg default_f32_tile(int M, int N, int K);
-TileCfg tuned_f32_tile(int M, int N, int K);
+TileCfg default_f32_tile(int M, int N, int K, int batch = 1);
+TileCfg tuned_f32_tile(int M, int N, int K, int batch = 1);
 // Runs one fp32 GEMM with an explicit tile config (used by the tile search).
 bool gemm_f32_cfg(int M, int N, int K, const float* A, const float* B, float* C,
                   const TileCfg& cfg, hipStream_t s);

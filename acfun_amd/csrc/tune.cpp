@@ -87,14 +87,14 @@ float time_cfg(int M, int N, int K, const float* A, const float* B, float* C, co
 
 }  // namespace
 
-TileCfg tuned_f32_tile(int M, int N, int K) {
+TileCfg tuned_f32_tile(int M, int N, int K, int batch) {
     bool run_now = false;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         load_cache_locked();
-        if (!g_busy) g_seen.insert(Key{M, N, K});
+        if (!g_busy && batch == 1) g_seen.insert(Key{M, N, K});
         auto it = g_table.find(Key{M, N, K});
-        if (it != g_table.end()) return it->second;
+        if (batch == 1 && it != g_table.end()) return it->second;
         static bool env_checked = false;
         if (!env_checked && !g_busy) {
             env_checked = true;
@@ -106,9 +106,9 @@ TileCfg tuned_f32_tile(int M, int N, int K) {
         autotune_run();
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_table.find(Key{M, N, K});
-        if (it != g_table.end()) return it->second;
+        if (batch == 1 && it != g_table.end()) return it->second;
     }
-    return default_f32_tile(M, N, K);
+    return default_f32_tile(M, N, K, batch);
 }
 
 void autotune_run() {

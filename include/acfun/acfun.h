@@ -189,6 +189,12 @@ int acfun_dev_fc(const float* input, int N, int Cin, const float* weight, const 
                  int Cout, float* output, int act, void* stream);
 int acfun_dev_softmax(const float* input, int rows, int cols, float* output, void* stream);
 
+/* acfun_model_load with options: flags & 1 quantizes every dense conv (type 1)
+ * to int8 at load (per-output-channel weights, acfun_quantize_weights rule) and
+ * runs it through the acfun_conv2d_int8 path with a per-batch dynamic
+ * activation scale; other layers stay fp32. */
+AcfunModel* acfun_model_load_ex(const char* path, int flags);
+
 /* Batched inference: input [N, inH, inW, inC], output [N, outSize].  Each image
  * gives the same result as acfun_model_infer on it alone.  Returns outSize
  * (per image), 0 on error. */
