@@ -362,9 +362,6 @@ __global__ __launch_bounds__(64 * NW) void k_wino_fused(
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 256 zero bytes in global memory: DMA source for padding pixels/channels.
-__device__ __attribute__((aligned(256))) float g_wino_zero[64];
-
 // F(2,3) on v_mfma_f32_32x32x2f32, input and filter staged by LDS DMA.
 //
 // Workgroup (512 threads) = one image's tile rows ty0..ty0+R-1 x tile
@@ -375,7 +372,7 @@ __device__ __attribute__((aligned(256))) float g_wino_zero[64];
 // wave's MFMAs overlap the other's LDS reads and transforms.
 //
 // Input channels are consumed in chunks of 16.  Per chunk the workgroup DMAs
-// (global_load_lds_dwordx4, no VGPRs) into one of two LDS buffers:
+// (buffer_load_dwordx4 ... lds, no data VGPRs) into one of two LDS buffers:
 //   X: the 2R+2 pixel rows x 2TC+2 columns the block's 4x4 patches touch,
 //      as [row][col%2][col/2][4 channel quads], quad q of pixel column index
 //      k stored at quad slot q ^ ((k>>2)&3);
@@ -422,64 +419,86 @@ __global__ __launch_bounds__(512) void k_wino23(
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
 
-    // ---- DMA descriptors.  Wave w issues X blocks w, w+8, ... (64 slots of
-    // 16 bytes each); lane l of block k covers slot 64k+l, i.e. pixel index
-    // pix0 + 128k with pix = (row*2 + plane)*TCP + kk.  kk and row*2+plane of
-    // block 0 are computed once; later blocks step them by 128 = dr*TCP + dk.
-    // Filter slots advance by 4 points (4 * Cout * Cinp floats) per block, so
-    // one offset serves all of them.
+    // ---- DMA descriptors.  Sources are read through buffer resources, so a
+    // byte offset past the resource's size (kOOB) reads zeros: padding pixels
+    // and missing output channels cost no branch or select, and the chunk's
+    // channel offset rides in the scalar offset.  Wave w issues X blocks w,
+    // w+8, ... (64 slots of 16 bytes); lane l of block k covers slot 64k+l,
+    // pixel index pix = (row*2 + plane)*TCP + kk = pix0 + 128k.  The byte
+    // offsets of this lane's KXM X slots are computed once; xq packs their
+    // channel quads (2 bits each) for a last chunk that ends inside a quad
+    // row (Cin % 16 != 0).  Filter block t of a wave sits 4t points (4 *
+    // Cout * Cinp floats) after block 0, a uniform step.
     constexpr int KXM = 9;
+    constexpr unsigned kOOB = 0x80000000u;
     const int xslots = nrow * 2 * TCP * 4;
-    const int pix0 = (wave * 64 + lane) >> 2;
-    const int kk0 = pix0 % TCP, rp0 = pix0 / TCP;
-    const int dk = 128 % TCP, dr = 128 / TCP;
-    const int sq = lane & 3;
-    const int ih0 = 2 * ty0 - 1, iw0 = 2 * tx0 - 1;
-    int ud;
+    const int nxb = (xslots + 63) / 64;                   // X blocks per chunk
+    unsigned xv[KXM];
+    unsigned xq = 0;
+    {
+        const int pix0 = (wave * 64 + lane) >> 2;         // < 128: float quotient is exact
+        int rp = (int)(((float)pix0 + 0.5f) / (float)TCP), kk = pix0 - rp * TCP;
+        const int dk = 128 % TCP, dr = 128 / TCP;
+        const int ih0 = 2 * ty0 - 1, iw0 = 2 * tx0 - 1;
+#pragma unroll
+        for (int k = 0; k < KXM; ++k) {
+            int q = (lane & 3) ^ ((kk >> 2) & 3);
+            int ih = ih0 + (rp >> 1);
+            int iw = iw0 + 2 * kk + (rp & 1);
+            bool ok = rp < 2 * nrow && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            xv[k] = ok ? (unsigned)((ih * W + iw) * Cin + 4 * q) * 4u : kOOB;
+            xq |= (unsigned)q << (2 * k);
+            kk += dk;
+            rp += dr;
+            if (kk >= TCP) { kk -= TCP; ++rp; }
+        }
+    }
+    unsigned uv;
     {
         int row = (wave * 64 + lane) >> 2;                // a*32 + co, a < 4
         int co = row & 31;
         int q = (lane & 3) ^ ((co >> 2) & 3);
-        ud = cob + co < Cout ? (int)((row >> 5) * uplane) + (cob + co) * Cinp + 4 * q : -1;
+        uv = cob + co < Cout ? (unsigned)((row >> 5) * Cout * Cinp + (cob + co) * Cinp + 4 * q) * 4u
+                             : kOOB;
     }
-    const long long ustep = 4 * uplane;
-    const int nxb = (xslots + 63) / 64;                   // X blocks per chunk
-    const float* zero = g_wino_zero;
+    const unsigned ustep = 16u * Cout * Cinp;             // bytes per 4 points
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, H * W * Cin * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ures =
+        __builtin_amdgcn_make_buffer_rsrc((void*)U, (short)0, (int)(16 * uplane * 4), 0x00020000);
+    const bool ragged = (Cin & 15) != 0;
     // DMA item t of a chunk: t < KU are this wave's filter blocks (the 16 x
     // 32 x 4 quads of a chunk are 32 blocks, KU = 4 per wave), t >= KU its X
-    // block t-KU (kk, rp carry the X walk from item to item).
+    // block t-KU.
     constexpr int KU = 16 * 32 * 4 / NT;
     constexpr int NITEM = KU + KXM;
     static_assert(NITEM <= 16, "DMA items are issued after the 16 MFMA groups of a chunk");
-    auto dma_item = [&](int t, int c0, float* base, int& kk, int& rp) {
+    auto dma_item = [&](int t, int c0, float* base) {
         if (t < KU) {
-            const float* src = ud >= 0 ? U + ud + c0 + t * ustep : zero;
-            __builtin_amdgcn_global_load_lds((const void*)src,
-                                             (lds_void*)(base + xfl + (wave + 8 * t) * 256), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ures, (lds_void*)(base + xfl + (wave + 8 * t) * 256),
+                                                     16, uv, c0 * 4 + t * ustep, 0, 0);
             return;
         }
-        const int blk = wave + 8 * (t - KU);
-        if (blk < nxb) {
-            int q = sq ^ ((kk >> 2) & 3);
-            int ih = ih0 + (rp >> 1);
-            int iw = iw0 + 2 * kk + (rp & 1);
-            bool ok = rp < 2 * nrow && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W &&
-                      c0 + 4 * q < Cin;
-            const float* src = ok ? img + (ih * W + iw) * Cin + 4 * q + c0 : zero;
-            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(base + blk * 256), 16, 0, 0);
-        }
-        kk += dk;
-        rp += dr;
-        if (kk >= TCP) { kk -= TCP; ++rp; }
+        const int k = t - KU;
+        const int blk = wave + 8 * k;
+        if (blk >= nxb) return;
+        unsigned v = xv[k];
+        if (ragged && c0 + 16 > Cin && c0 + 4 * (int)((xq >> (2 * k)) & 3) >= Cin) v = kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + blk * 256), 16, v, c0 * 4, 0, 0);
     };
 
-    // this lane's MFMA row (tile slot)
+    // first chunk's DMA goes out before the remaining setup
+#pragma unroll
+    for (int t = 0; t < NITEM; ++t) dma_item(t, 0, smem);
+
+    // this lane's MFMA row (tile slot); slot < 128, so the float quotient
+    // (slot + 0.5) / TC sits at least 1/128 from an integer
     const int slot = pair * 32 + li;
-    const int sr = slot / TC, stx = slot - sr * TC;
+    const int sr = (int)(((float)slot + 0.5f) / (float)TC), stx = slot - sr * TC;
     const int srr = sr < R ? sr : 0;
     const int usw = (li >> 2) & 3;                        // U swizzle of row li
     const int rA = 2 * hr, rB = 2 - hr, rC = 1 + 2 * hr;
-    const int smask = hr << 31;                           // sign flip of dB for hr = 1
+    const unsigned smask = (unsigned)hr << 31;            // sign flip of dB for hr = 1
 
     // Compute chunk buffer b; when c0n >= 0 also issue the DMA items of the
     // next chunk (channels c0n.., buffer bn), one after each group of 4 MFMAs,
@@ -488,7 +507,6 @@ __global__ __launch_bounds__(512) void k_wino23(
     auto compute = [&](int b, int c0n, int bn) {
         const float* X = smem + b * bufsz;
         float* nbase = smem + bn * bufsz;
-        int kk = kk0, rp = rp0;
         const float* Ub = X + xfl;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -497,10 +515,11 @@ __global__ __launch_bounds__(512) void k_wino23(
 #pragma unroll
             for (int a = 0; a < 8; ++a)
                 bf[a] = *(const f4*)&Ub[(((8 * hr + a) * 32 + li) * 4 + (q ^ usw)) * 4];
-            // BT rows 2hr, 2hr+1 of the patch column: hr = 0 gives d0-d2 and
+            // BT rows 2hr, 2hr+1 of each patch column: hr = 0 gives d0-d2 and
             // d1+d2, hr = 1 gives d2-d1 and d3-d1, i.e. dA-dB and dC+(+-dB)
-            // with A = 2hr, B = 2-hr, C = 1+2hr (wave-uniform row choice, no
-            // branch between the reads).
+            // with A = 2hr, B = 2-hr, C = 1+2hr: a wave-uniform row choice
+            // with no branch between the reads.  (Separate code per hr costs
+            // registers here and spills.)
             f4 t[2][4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -513,7 +532,7 @@ __global__ __launch_bounds__(512) void k_wino23(
                 f4 dBs;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    dBs[e] = __int_as_float(__float_as_int(dB[e]) ^ smask);
+                    dBs[e] = __uint_as_float(__float_as_uint(dB[e]) ^ smask);
                 t[0][j] = dA - dB;
                 t[1][j] = dC + dBs;
             }
@@ -531,18 +550,13 @@ __global__ __launch_bounds__(512) void k_wino23(
                     for (int s = 0; s < 4; ++s)
                         acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(dh[j][s], bf[a][s], acc[a], 0, 0, 0);
                     const int item = h * 8 + a;
-                    if (item < NITEM && c0n >= 0) dma_item(item, c0n, nbase, kk, rp);
+                    if (item < NITEM && c0n >= 0) dma_item(item, c0n, nbase);
                 }
             }
         }
     };
 
     const int nch = Cinp / KC;
-    {
-        int kk = kk0, rp = rp0;
-#pragma unroll
-        for (int t = 0; t < NITEM; ++t) dma_item(t, 0, smem, kk, rp);
-    }
     for (int ch = 0; ch < nch; ++ch) {
         __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs for chunk ch have landed
         __syncthreads();                 // ... and every other wave's; buffer ch+1 is free
@@ -552,36 +566,46 @@ __global__ __launch_bounds__(512) void k_wino23(
     // ---- epilogue.  Lane l, register r <-> MFMA row 8*(r/4)+4*(l/32)+r%4, channel l%32.
     // S_i[c] = sum_j AT[c][j] M[i][j]; Y[0][c] = S0+S1+S2, Y[1][c] = S1-S2+S3.
     // Wave 2p+h writes the partial 2x2 outputs of its transform rows into
-    // output tile h in LDS ([2R rows][2TC cols][32 channels] each); then every
-    // thread adds the two tiles, bias and ReLU and stores 16-byte quads
-    // (32 output channels = 128 contiguous bytes per pixel).  Divisions by
-    // the runtime TC use a float reciprocal: numerators stay below 2^9 and
-    // sit at least 1/256 from an integer quotient, far above float rounding.
+    // output tile h in LDS, slot-major ([128 slots][2x2 pixels][32 channels],
+    // so every write is a lane base plus an immediate); then every thread
+    // adds the two tiles, bias and ReLU and stores 16-byte channel quads (32
+    // output channels = 128 contiguous bytes per pixel).
     __syncthreads();                     // staging buffers are free
-    const int OW2 = 2 * TC;
-    const int tile = 2 * R * OW2 * 32;   // floats per output tile
-    const float rtc = 1.0f / (float)TC, rw2 = 0.5f * rtc;
+    // Slot stride 136 floats: the lane halves (4 slots apart) of a 64-lane
+    // write land 32 banks apart.
+    constexpr int SS = 136;
+    constexpr int TILE = 128 * SS;       // floats per output tile
     {
-        float* so = smem + hr * tile;
+        float* p = smem + hr * TILE + (pair * 32 + 4 * g) * SS + li;
+        if (hr == 0) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            int os = pair * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            int orr = (int)(((float)os + 0.5f) * rtc), otx = os - orr * TC;
-            if (orr >= R) continue;
-            float S[2][2];
+            for (int r = 0; r < 16; ++r) {
+                float* ps = p + (8 * (r >> 2) + (r & 3)) * SS;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                float m0 = acc[i * 4 + 0][r], m1 = acc[i * 4 + 1][r];
-                float m2 = acc[i * 4 + 2][r], m3 = acc[i * 4 + 3][r];
-                S[i][0] = m0 + m1 + m2;
-                S[i][1] = m1 - m2 + m3;
+                for (int c = 0; c < 2; ++c) {
+                    // rows 0, 1 of M: S0 and S1
+                    float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
+                    float n0 = acc[4][r], n1 = acc[5][r], n2 = acc[6][r], n3 = acc[7][r];
+                    float s0 = c == 0 ? m0 + m1 + m2 : m1 - m2 + m3;
+                    float s1 = c == 0 ? n0 + n1 + n2 : n1 - n2 + n3;
+                    ps[c * 32] = s0 + s1;          // Y[0][c] partial: S0 + S1
+                    ps[(2 + c) * 32] = s1;         // Y[1][c] partial: S1
+                }
             }
-            float* p = so + ((2 * orr) * OW2 + 2 * otx) * 32 + li;
+        } else {
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                // wave 2p holds S0,S1 (rows 0,1), wave 2p+1 holds S2,S3
-                p[c * 32] = hr == 0 ? S[0][c] + S[1][c] : S[0][c];
-                p[OW2 * 32 + c * 32] = hr == 0 ? S[1][c] : S[1][c] - S[0][c];
+            for (int r = 0; r < 16; ++r) {
+                float* ps = p + (8 * (r >> 2) + (r & 3)) * SS;
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    // rows 2, 3 of M: S2 and S3
+                    float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
+                    float n0 = acc[4][r], n1 = acc[5][r], n2 = acc[6][r], n3 = acc[7][r];
+                    float s2 = c == 0 ? m0 + m1 + m2 : m1 - m2 + m3;
+                    float s3 = c == 0 ? n0 + n1 + n2 : n1 - n2 + n3;
+                    ps[c * 32] = s2;               // Y[0][c] partial: S2
+                    ps[(2 + c) * 32] = s3 - s2;    // Y[1][c] partial: S3 - S2
+                }
             }
         }
     }
@@ -593,13 +617,23 @@ __global__ __launch_bounds__(512) void k_wino23(
 #pragma unroll
         for (int t = 0; t < 4; ++t) bq[t] = c + t < Cout ? bias[c + t] : 0.f;
     }
-    const int nq = 2 * R * OW2 * 8;      // float4 quads of the output tile
-    for (int e = tid; e < nq; e += NT) {
+    // Output pixel (py, px) of the block = slot (py/2)*TC + px/2, sub-pixel
+    // 2*(py&1) + (px&1).  py = pxl / (2TC) uses a float reciprocal: pxl < 2^9
+    // and the exact quotient sits at least 1/256 from an integer, far above
+    // the float rounding error.
+    const int OW2 = 2 * TC;
+    const float rw2 = 1.0f / (float)OW2;
+    const int nq = 2 * R * OW2 * 8;      // float4 quads of the output block (<= 8 * NT)
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int e = tid + it * NT;
+        if (e >= nq) break;
         int pxl = e >> 3;
         int py = (int)(((float)pxl + 0.5f) * rw2), pxx = pxl - py * OW2;
         int oh = 2 * ty0 + py, ow = 2 * tx0 + pxx;
         if (oh >= H || ow >= W || c >= Cout) continue;
-        f4 v = *(const f4*)&smem[pxl * 32 + 4 * qd] + *(const f4*)&smem[tile + pxl * 32 + 4 * qd] + bq;
+        int so = ((py >> 1) * TC + (pxx >> 1)) * SS + (2 * (py & 1) + (pxx & 1)) * 32 + 4 * qd;
+        f4 v = *(const f4*)&smem[so] + *(const f4*)&smem[TILE + so] + bq;
         if (act == 1) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[t] = v[t] > 0.f ? v[t] : 0.f;
@@ -637,10 +671,13 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     if (R > tH) R = tH;
     while (R > 1 && 2 * sizeof(float) * buf_floats(R, TC) > 160 * 1024) --R;
     size_t lds = 2 * sizeof(float) * buf_floats(R, TC);
-    // Each wave issues at most 9 X blocks of 64 slots per chunk, and two
-    // 2R x 2TC x 32 output tiles are staged in LDS by the epilogue.
+    // Each wave issues at most 9 X blocks of 64 slots per chunk; the epilogue
+    // stages two 128-slot output tiles (136 KB) in the same LDS; buffer
+    // resources address one image and the filter with 32-bit byte offsets.
     size_t xblocks = ((size_t)(2 * R + 2) * 2 * (TC + 1) * 4 + 63) / 64;
-    if (lds > 160 * 1024 || xblocks > 8 * 9 || (size_t)256 * R * TC * sizeof(float) > lds) {
+    if (lds < 2 * 128 * 136 * sizeof(float)) lds = 2 * 128 * 136 * sizeof(float);
+    if (lds > 160 * 1024 || xblocks > 8 * 9 || (long long)H * W * Cin * 4 >= (1ll << 31) ||
+        16ll * Cout * Cinp * 4 >= (1ll << 31)) {
         ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
         return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
     }
