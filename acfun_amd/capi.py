@@ -72,6 +72,8 @@ SIGNATURES = {
     "acfun_model_load_ex": (_p, [_s, _i]),
     "acfun_model_infer_batch": (_i, [_p, _i, _p, _p]),
     "acfun_dev_model_infer_batch": (_i, [_p, _i, _p, _p, _p]),
+    "acfun_prof_enable": (None, [_i]),
+    "acfun_prof_kernel_ms": (C.c_double, [_s, C.POINTER(_i)]),
 }
 
 

@@ -313,7 +313,10 @@ __global__ void k_round_bf16(const float* __restrict__ in, float* __restrict__ o
 template <int BM, int BN, bool CONV, bool VA, bool VB>
 bool launch_t(const GemmP& p, int batch, hipStream_t s) {
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, batch * p.splits);
-    hipLaunchKernelGGL((k_gemm_f32<BM, BN, CONV, VA, VB>), grid, dim3(256), 0, s, p);
+    {
+        KTimer kt("k_gemm_f32", s);
+        hipLaunchKernelGGL((k_gemm_f32<BM, BN, CONV, VA, VB>), grid, dim3(256), 0, s, p);
+    }
     return check_launch("k_gemm_f32");
 }
 

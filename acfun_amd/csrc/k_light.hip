@@ -269,11 +269,13 @@ bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, con
     bool al = (((uintptr_t)in | (uintptr_t)out) & 15u) == 0;
     if (KH == 3 && KW == 3 && C % 4 == 0 && al) {
         long long total = (long long)N * OH * OW * (C / 4);
+        KTimer kt("k_dwconv", s);
         hipLaunchKernelGGL(k_dwconv3_c4, grid1d(total), dim3(256), 0, s, (const float4*)in, N, H,
                            W, C / 4, w, bias, stride, pad, OH, OW, (float4*)out, act);
         return check_launch("k_dwconv3_c4");
     }
     long long total = (long long)N * OH * OW * C;
+    KTimer kt("k_dwconv", s);
     hipLaunchKernelGGL(k_dwconv, grid1d(total), dim3(256), 0, s, in, N, H, W, C, w, bias, KH, KW,
                        stride, pad, OH, OW, out, act);
     return check_launch("k_dwconv");
@@ -292,6 +294,7 @@ bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, co
     int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
     int fma_all = Cout_p >= 8 ? 1 : 0;
     long long total = (long long)N * OH * OW * Cout;
+    KTimer kt("k_gconv", s);
     hipLaunchKernelGGL(k_gconv, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH, KW,
                        Cout, stride, pad, groups, OH, OW, out, act, vec_end, fma_all);
     return check_launch("k_gconv");
@@ -304,6 +307,7 @@ bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stri
     if (OH <= 0 || OW <= 0) return true;
     int vec_end = C >= 16 ? (C & ~15) : (C >= 8 ? (C & ~7) : 0);
     long long total = (long long)N * OH * OW * C;
+    KTimer kt("k_maxpool", s);
     hipLaunchKernelGGL(k_maxpool, grid1d(total), dim3(256), 0, s, in, N, H, W, C, pool, stride,
                        pad, OH, OW, out, post_relu, vec_end);
     return check_launch("k_maxpool");

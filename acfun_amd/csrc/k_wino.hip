@@ -688,6 +688,7 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     }
     int rblocks = (tH + R - 1) / R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
+    KTimer kt("k_wino23", s);
     hipLaunchKernelGGL(k_wino23, grid, dim3(512), lds, s, in, U.as<float>(), bias, out, N, H, W,
                        Cin, Cinp, Cout, tH, tW, R, TC, act);
     return check_launch("k_wino23");
@@ -707,6 +708,7 @@ bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, co
                        Cin, Cinp, Cout, U.as<float>());
     if (!check_launch("k_wino_filter_t")) return false;
     dim3 grid((unsigned)((T + TB - 1) / TB), (Cout + 16 * NW - 1) / (16 * NW));
+    KTimer kt("k_wino_fused", s);
     hipLaunchKernelGGL((k_wino_fused<TILE, TB, NW, KC>), grid, dim3(64 * NW), 0, s, in, U.as<float>(),
                        bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act);
     return check_launch("k_wino_fused");

@@ -19,6 +19,19 @@ bool check(hipError_t e, const char* what);
 // Checks the launch status of the last kernel.
 bool check_launch(const char* kernel);
 
+// ----------------------------------------------------------------- timing
+// Kernel timing for measurement: while enabled (acfun_prof_enable), KTimer
+// records a HIP event pair around one launch on its stream; the pairs are
+// summed per kernel name by acfun_prof_kernel_ms.  Disabled: no events.
+void prof_begin(const char* kernel, hipStream_t s);
+void prof_end(const char* kernel, hipStream_t s);
+struct KTimer {
+    const char* k;
+    hipStream_t s;
+    KTimer(const char* kernel, hipStream_t st) : k(kernel), s(st) { prof_begin(k, s); }
+    ~KTimer() { prof_end(k, s); }
+};
+
 // ----------------------------------------------------------------- device
 // Initializes the current device once (verifies it is gfx950, creates the
 // library stream).  Returns false (and sets the error) when no usable GPU.

@@ -31,6 +31,41 @@ bool check(hipError_t e, const char* what) {
 
 bool check_launch(const char* kernel) { return check(hipGetLastError(), kernel); }
 
+// ------------------------------------------------------------------ timing
+namespace {
+struct ProfKernel {
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;   // created on demand, reused
+    size_t used = 0;
+    bool open = false;
+};
+bool g_prof_on = false;
+std::map<std::string, ProfKernel> g_prof;
+std::mutex g_prof_mu;
+}  // namespace
+
+void prof_begin(const char* kernel, hipStream_t s) {
+    if (!g_prof_on) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    ProfKernel& k = g_prof[kernel];
+    if (k.used == k.ev.size()) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return;
+        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return; }
+        k.ev.emplace_back(a, b);
+    }
+    if (hipEventRecord(k.ev[k.used].first, s) == hipSuccess) k.open = true;
+}
+
+void prof_end(const char* kernel, hipStream_t s) {
+    if (!g_prof_on) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    auto it = g_prof.find(kernel);
+    if (it == g_prof.end() || !it->second.open) return;
+    ProfKernel& k = it->second;
+    k.open = false;
+    if (hipEventRecord(k.ev[k.used].second, s) == hipSuccess) ++k.used;
+}
+
 // ------------------------------------------------------------------ device
 namespace {
 constexpr int kMaxDev = 16;
@@ -219,3 +254,34 @@ bool HostCall::finish() {
 }
 
 }  // namespace acfun
+
+// ------------------------------------------------------------------ C ABI: timing
+extern "C" void acfun_prof_enable(int on) {
+    std::lock_guard<std::mutex> lk(acfun::g_prof_mu);
+    if (on) {                            // a new measurement starts empty; off keeps the records
+        for (auto& kv : acfun::g_prof) {
+            kv.second.used = 0;
+            kv.second.open = false;
+        }
+    }
+    acfun::g_prof_on = on != 0;
+}
+
+extern "C" double acfun_prof_kernel_ms(const char* kernel, int* launches) {
+    if (launches) *launches = 0;
+    if (!kernel) return 0.0;
+    std::lock_guard<std::mutex> lk(acfun::g_prof_mu);
+    auto it = acfun::g_prof.find(kernel);
+    if (it == acfun::g_prof.end() || it->second.used == 0) return 0.0;
+    double total = 0.0;
+    for (size_t i = 0; i < it->second.used; ++i) {
+        auto& e = it->second.ev[i];
+        if (!acfun::check(hipEventSynchronize(e.second), "acfun_prof_kernel_ms")) return -1.0;
+        float ms = 0.f;
+        if (!acfun::check(hipEventElapsedTime(&ms, e.first, e.second), "acfun_prof_kernel_ms"))
+            return -1.0;
+        total += ms;
+    }
+    if (launches) *launches = (int)it->second.used;
+    return total / (double)it->second.used;
+}

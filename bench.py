@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
+    ap.add_argument("--traffic", action="store_true",
+                    help="for rocprofv3 --pmc runs: 5 headline steps, then 3 plain copies of "
+                         "256 MiB (the counter scale reference); prints no JSON line")
     return ap.parse_args()
 
 
@@ -62,6 +65,19 @@ class Timer:
         e1.record(self.stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps   # ms per step
+
+    def kernel_ms(self, lib, fn, steps, kernel):
+        """Mean duration (ms) of one library kernel over `steps` more steps: the
+        library brackets each launch of it with a HIP event pair on its stream."""
+        self.torch.cuda.synchronize()
+        lib.acfun_prof_enable(1)
+        for _ in range(steps):
+            fn()
+        self.torch.cuda.synchronize()
+        lib.acfun_prof_enable(0)
+        n = C.c_int(0)
+        ms = lib.acfun_prof_kernel_ms(kernel.encode(), C.byref(n))
+        return ms if n.value > 0 and ms > 0 else None
 
 
 def main():
@@ -106,17 +122,24 @@ def main():
         check(lib.acfun_dev_conv2d(tx.data_ptr(), N, H, H, Cin, tw.data_ptr(), tb.data_ptr(),
                                    3, 3, Cout, 1, 1, 1, ty.data_ptr(), 1, sp))
 
+    if args.traffic:
+        for _ in range(5):
+            step()
+        src = torch.empty(64 << 20, device=dev)        # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
+
     ms = T.run(step, args.steps, args.warmup)
+    kms = T.kernel_ms(lib, step, args.steps, "k_wino23")
     direct_flop = 2.0 * N * H * H * Cout * 9 * Cin
     tiles = N * ((H + 1) // 2) ** 2
     exec_flop = 2.0 * tiles * 16 * Cin * Cout
     value = direct_flop / (ms * 1e-3) / 1e12
-    achieved = exec_flop / (ms * 1e-3)
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("winograd_f23_cfg2a")
+    achieved = exec_flop / (kms * 1e-3) if kms else None
+    traffic = read_traffic(os.path.join(ROOT, "profiles", "traffic_k_wino23_cfg2a.txt"))
 
     line = {
         "metric": "fp32 TFLOPS & int8 TOPS (% MI355X peak); ResNet-50-style b64 images/s",
@@ -135,10 +158,14 @@ def main():
                                "(reference route: Winograd F(2,3))",
                    "flop_count": "direct-conv equivalent 7.40 GFLOP per step",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 3),
+        "roofline": {"bound": "mfma",
+                     "achieved": round(achieved / 1e12, 3) if achieved else None,
                      "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic,
-                     "work": "executed F(2,3) MFMA FLOPs 3.288 GFLOP per launch"},
+                     "frac": round(achieved / PEAK_FP32, 4) if achieved else None,
+                     "traffic": traffic,
+                     "kernel": "k_wino23", "kernel_ms": round(kms, 5) if kms else None,
+                     "work": "executed F(2,3) MFMA FLOPs 3.288 GFLOP per launch (2 * 25088 "
+                             "tiles * 16 points * 64 * 64)"},
     }
 
     # ---------------------------------------------------------------- other configs
@@ -151,23 +178,29 @@ def main():
         A = cuda(rng.uniform(-1, 1, (M, M)).astype(np.float32))
         Bm = cuda(rng.uniform(-1, 1, (M, M)).astype(np.float32))
         Cm = torch.empty((M, M), device=dev)
-        t = T.run(lambda: check(lib.acfun_dev_gemm_epi(M, M, M, A.data_ptr(), Bm.data_ptr(),
-                                                       Cm.data_ptr(), None, 0, sp)), steps, 5)
+        s1 = lambda: check(lib.acfun_dev_gemm_epi(M, M, M, A.data_ptr(), Bm.data_ptr(),
+                                                  Cm.data_ptr(), None, 0, sp))
+        t = T.run(s1, steps, 5)
+        k = T.kernel_ms(lib, s1, steps, "k_gemm_f32")
         f = 2.0 * M ** 3 / (t * 1e-3)
         configs["cfg1_gemm_1024"] = {"ms": round(t, 5), "TFLOPS": round(f / 1e12, 3),
-                                     "frac_fp32_peak": round(f / PEAK_FP32, 4)}
+                                     "frac_fp32_peak": round(f / PEAK_FP32, 4),
+                                     "kernel_ms": {"k_gemm_f32": k}}
 
         # 2b: F(4,3), N=8, 112x112
         x2 = cuda(rng.uniform(0, 1, (8, 112, 112, 64)).astype(np.float32))
         y2 = torch.empty((8, 112, 112, 64), device=dev)
-        t = T.run(lambda: check(lib.acfun_dev_conv2d(x2.data_ptr(), 8, 112, 112, 64, tw.data_ptr(),
-                                                     tb.data_ptr(), 3, 3, 64, 1, 1, 1,
-                                                     y2.data_ptr(), 1, sp)), steps, 5)
+        s2 = lambda: check(lib.acfun_dev_conv2d(x2.data_ptr(), 8, 112, 112, 64, tw.data_ptr(),
+                                                tb.data_ptr(), 3, 3, 64, 1, 1, 1,
+                                                y2.data_ptr(), 1, sp))
+        t = T.run(s2, steps, 5)
+        k = T.kernel_ms(lib, s2, steps, "k_wino_fused")
         f = direct_flop / (t * 1e-3)
         ex = 2.0 * 8 * 28 * 28 * 36 * 64 * 64 / (t * 1e-3)
         configs["cfg2b_conv3x3_f43"] = {"ms": round(t, 5), "TFLOPS_direct": round(f / 1e12, 3),
                                         "TFLOPS_executed": round(ex / 1e12, 3),
-                                        "frac_fp32_peak_executed": round(ex / PEAK_FP32, 4)}
+                                        "frac_fp32_peak_executed": round(ex / PEAK_FP32, 4),
+                                        "kernel_ms": {"k_wino_fused": k}}
 
         # 3a / 3b: int8 convs with float I/O
         for name, (KK, ci, co, pd) in {"cfg3a_int8_1x1": (1, 256, 512, 0),
@@ -178,14 +211,17 @@ def main():
             ws = cuda(rng.uniform(0.005, 0.05, co).astype(np.float32))
             bi = cuda((rng.standard_normal(co) * 0.01).astype(np.float32))
             yi = torch.empty((32, 28, 28, co), device=dev)
-            t = T.run(lambda: check(lib.acfun_dev_conv2d_int8(
+            s3 = lambda: check(lib.acfun_dev_conv2d_int8(
                 xi.data_ptr(), 32, 28, 28, ci, wq.data_ptr(), ws.data_ptr(), bi.data_ptr(), KK, KK,
-                co, 1, pd, yi.data_ptr(), 1, sp)), steps, 5)
+                co, 1, pd, yi.data_ptr(), 1, sp))
+            t = T.run(s3, steps, 5)
+            k = T.kernel_ms(lib, s3, steps, "k_igemm_i8")
             ops = 2.0 * 32 * 28 * 28 * co * KK * KK * ci
             byts = 4.0 * 32 * 28 * 28 * (ci + co)
             configs[name] = {"ms": round(t, 5), "TOPS": round(ops / (t * 1e-3) / 1e12, 3),
                              "frac_int8_peak": round(ops / (t * 1e-3) / PEAK_INT8, 4),
-                             "float_io_GBps": round(byts / (t * 1e-3) / 1e9, 1)}
+                             "float_io_GBps": round(byts / (t * 1e-3) / 1e9, 1),
+                             "kernel_ms": {"k_igemm_i8": k}}
 
         # 4a: depthwise 3x3/2 (BN folded) + ReLU, then 3x3/2 maxpool
         C4 = 96
@@ -200,10 +236,13 @@ def main():
                                        3, 3, C4, 2, 1, C4, y4.data_ptr(), 1, sp))
             check(lib.acfun_dev_maxpool(y4.data_ptr(), 32, 56, 56, C4, 3, 2, 1, z4.data_ptr(), 0, sp))
         t = T.run(s4, steps, 5)
+        kd = T.kernel_ms(lib, s4, steps, "k_dwconv")
+        kp = T.kernel_ms(lib, s4, steps, "k_maxpool")
         byts = 4.0 * (32 * 112 * 112 * C4 + 2 * 32 * 56 * 56 * C4 + 32 * 28 * 28 * C4)
         configs["cfg4a_dw_bn_relu_pool"] = {"ms": round(t, 5),
                                             "GBps": round(byts / (t * 1e-3) / 1e9, 1),
-                                            "frac_hbm": round(byts / (t * 1e-3) / PEAK_HBM, 4)}
+                                            "frac_hbm": round(byts / (t * 1e-3) / PEAK_HBM, 4),
+                                            "kernel_ms": {"k_dwconv": kd, "k_maxpool": kp}}
 
         # 4b: grouped 3x3 g6, 24 -> 48, N=32, 14x14, then maxpool
         x5 = cuda(rng.uniform(0, 1, (32, 14, 14, 24)).astype(np.float32))
@@ -217,8 +256,10 @@ def main():
                                        3, 3, 48, 1, 1, 6, y5.data_ptr(), 1, sp))
             check(lib.acfun_dev_maxpool(y5.data_ptr(), 32, 14, 14, 48, 3, 2, 1, z5.data_ptr(), 0, sp))
         t = T.run(s5, steps, 5)
+        kg = T.kernel_ms(lib, s5, steps, "k_gconv")
         byts = 4.0 * (32 * 14 * 14 * 24 + 2 * 32 * 14 * 14 * 48 + 32 * 7 * 7 * 48)
-        configs["cfg4b_grouped_pool"] = {"ms": round(t, 5), "GBps": round(byts / (t * 1e-3) / 1e9, 1)}
+        configs["cfg4b_grouped_pool"] = {"ms": round(t, 5), "GBps": round(byts / (t * 1e-3) / 1e9, 1),
+                                         "kernel_ms": {"k_gconv": kg}}
 
         # 5: ResNet-50-style, batch 64, fp32 and int8
         inC, inH, inW, recs = acfun0.resnet50(np.random.default_rng(5))
@@ -249,6 +290,24 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(x, w, b, direct_flop)
     print(json.dumps(line), flush=True)
+
+
+def read_traffic(path):
+    """HBM bytes per launch of the headline kernel from the committed counter
+    summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain copy of
+    known size), or None when the summary is absent."""
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for ln in f:
+            parts = ln.split()
+            if len(parts) == 2 and not ln.startswith("#"):
+                try:
+                    vals[parts[0]] = float(parts[1])
+                except ValueError:
+                    pass
+    return vals.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(x, w, b, flop):
