@@ -173,6 +173,25 @@ def main():
     if not args.headline_only:
         steps = max(5, args.steps // 2)
 
+        # 2a through the reference-compatible host-pointer API (acfun_conv2d_relu on
+        # host buffers: H2D staging, kernels, D2H, synchronize) -- PCIe-inclusive rate
+        yh = np.empty((N, H, H, Cout), np.float32)
+        Ph = lambda a: C.c_void_p(a.ctypes.data)
+        hcall = lambda: lib.acfun_conv2d_relu(Ph(x), N, H, H, Cin, Ph(w), Ph(b), 3, 3, Cout, 1, 1,
+                                              Ph(yh))
+        for _ in range(3):
+            hcall()
+        th = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            hcall()
+            th.append(time.perf_counter() - t0)
+        th = float(np.median(th)) * 1e3
+        configs["cfg2a_host_buffers"] = {"ms": round(th, 4),
+                                         "TFLOPS_direct": round(direct_flop / (th * 1e-3) / 1e12, 3),
+                                         "note": "acfun_conv2d_relu on host memory, PCIe-inclusive, "
+                                                 "median wall time"}
+
         # 1: GEMM 1024^3
         M = 1024
         A = cuda(rng.uniform(-1, 1, (M, M)).astype(np.float32))
