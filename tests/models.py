@@ -1,0 +1,89 @@
+"""Small ACFUN0 test models.
+
+fusion_v1: a version-1 model (record types 1-7 only, so the compiled reference
+loads it) that exercises every load-time fusion rule of the reference
+(src/model.cpp:199-247):
+  - Conv -> BN -> ReLU: BN folded, the ReLU stays a separate layer;
+  - Conv -> ReLU -> BN: ReLU marked, BN folded, fused act (= ReLU(BN(conv)));
+  - ReLU -> MaxPool: the ReLU is dropped;
+  - MaxPool -> ReLU: absorbed as post-ReLU;
+  - grouped conv (direct route) and depthwise conv with a folded BN (group-aware
+    fold offsets, src/model.cpp:69-95);
+  - a standalone BN (not after a conv), 1x1 and pad-0 im2col routes, the
+    Winograd F(2,3) route, FC over H*W*C and softmax over all outputs.
+Pre-activations are zero-mean, so a misplaced ReLU changes the output.
+
+int8_chain_v1: dense convs only on the int8-capable routes (int8 Winograd
+3x3/s1/p1, 1x1, im2col 3x3/s2) with folded BN and fused ReLU, plus a maxpool.
+"""
+import numpy as np
+
+from acfun_amd import acfun0
+
+
+def _conv(rng, KH, KW, Cin, Cout, s, p):
+    return ("conv", KH, KW, Cout, s, p, acfun0.conv_weight(rng, KH, KW, Cin, Cout),
+            (rng.standard_normal(Cout) * 0.1).astype(np.float32))
+
+
+def _convg(rng, KH, KW, Cin, Cout, s, p, g):
+    w = (rng.standard_normal((g, KH * KW * (Cin // g), Cout // g)) *
+         np.sqrt(2.0 / (KH * KW * (Cin // g)))).astype(np.float32)
+    return ("convg", KH, KW, Cout, s, p, g, w.reshape(-1),
+            (rng.standard_normal(Cout) * 0.1).astype(np.float32))
+
+
+def fusion_v1(rng, hw=18, drop_relu=True):
+    """drop_relu=False leaves out the ReLU between the 1x1 conv and the second
+    MaxPool, which the reference's loader drops anyway."""
+    R = [
+        _conv(rng, 3, 3, 3, 8, 1, 1),            # Cin=3 < 4 -> im2col route
+        acfun0.bn_params(rng, 8),                 # folded
+        ("relu",),                                # separate ReLU layer
+        _conv(rng, 3, 3, 8, 8, 1, 1),            # Winograd F(2,3)
+        ("relu",),                                # marked ...
+        acfun0.bn_params(rng, 8),                 # ... BN folded: ReLU(BN(conv))
+        ("relu",),                                # dropped: next is MaxPool
+        ("maxpool", 2, 2, 0),
+        ("relu",),                                # absorbed as post-ReLU
+        _convg(rng, 3, 3, 8, 16, 1, 1, 2),       # direct grouped
+        ("relu",),
+        _convg(rng, 3, 3, 16, 16, 2, 1, 16),     # depthwise 3x3/2
+        acfun0.bn_params(rng, 16),                # folded with group-aware offsets
+        ("relu",),
+        _conv(rng, 1, 1, 16, 12, 1, 0),          # 1x1 route
+        ("relu",),                                # marked, then dropped: next is MaxPool
+        ("maxpool", 3, 1, 1),
+        acfun0.bn_params(rng, 12),                # standalone BN layer
+        _conv(rng, 3, 3, 12, 8, 1, 0),           # pad 0 -> im2col route
+    ]
+    if not drop_relu:
+        R.pop(15)
+    h = hw
+    h = h // 2                                    # maxpool 2/2
+    h = (h + 2 - 3) // 2 + 1                      # depthwise s2 p1
+    h = h - 2                                     # 3x3 pad 0
+    R.append(("fc", 10, h * h * 8, (rng.standard_normal((h * h * 8, 10)) * 0.05).astype(np.float32),
+              (rng.standard_normal(10) * 0.1).astype(np.float32)))
+    R.append(("softmax",))
+    return 3, hw, hw, R
+
+
+def int8_chain_v1(rng, hw=20, cin=8):
+    R = [
+        _conv(rng, 3, 3, cin, 16, 1, 1),         # int8 Winograd route
+        acfun0.bn_params(rng, 16),
+        ("relu",),
+        _conv(rng, 1, 1, 16, 24, 1, 0),          # 1x1 route
+        ("relu",),
+        _conv(rng, 3, 3, 24, 16, 2, 1),          # im2col + int8 GEMM route
+        ("relu",),
+        ("maxpool", 3, 2, 1),
+        _conv(rng, 3, 3, 16, 8, 1, 1),
+    ]
+    return cin, hw, hw, R
+
+
+def small_resnet_v2(rng, hw=32):
+    """A version-2 residual model (Input/Add/GlobalAvgPool records)."""
+    return acfun0.resnet50(rng, in_hw=hw, width=8, blocks=(1, 2, 1, 1), classes=10)

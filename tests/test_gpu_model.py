@@ -1,0 +1,158 @@
+"""GPU parity of the ACFUN0 model path (loader fusion + executor, model.cpp)
+through the C ABI: against the compiled reference's own executor on version-1
+models, against the oracle executor (tests/test_model_pins.py pins it to the
+reference) on version-2 residual models and on the int8 mode.
+
+Bars: int8 convolution chains bit-exact; fp32 models within the Winograd
+tolerance 1e-3 (normwise, on the model output)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle.model as omodel
+from acfun_amd import acfun0, capi
+from tests import models
+from tests.helpers import P, assert_bitexact, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _write(tmp_path, name, inC, H, W, recs, version):
+    path = str(tmp_path / name)
+    acfun0.write(path, inC, H, W, recs, version=version)
+    return path
+
+
+def _infer_each(lib, m, x):
+    outs = []
+    for img in x:
+        y = np.full(1 << 16, np.nan, np.float32)
+        n = lib.acfun_model_infer(m, P(np.ascontiguousarray(img)), P(y))
+        assert n > 0, capi.last_error()
+        outs.append(y[:n].copy())
+    return np.stack(outs)
+
+
+def _load(lib, path, flags=0):
+    m = lib.acfun_model_load_ex(path.encode(), flags)
+    assert m, capi.last_error()
+    return m
+
+
+def test_model_v1_matches_reference(gpu, ref, rng, tmp_path):
+    inC, H, W, recs = models.fusion_v1(rng)
+    path = _write(tmp_path, "fusion.acfun", inC, H, W, recs, 1)
+    x = rng.uniform(-1, 1, (3, H, W, inC)).astype(np.float32)
+    mr = ref.acfun_model_load(path.encode())
+    want = _infer_each(ref, mr, x)
+    ref.acfun_model_destroy(mr)
+    m = gpu.acfun_model_load(path.encode())
+    assert m, capi.last_error()
+    try:
+        assert gpu.acfun_model_output_size(m) == 0       # as the reference: known after infer
+        dims = [C.c_int(0), C.c_int(0), C.c_int(0)]
+        gpu.acfun_model_input_dims(m, *[C.byref(d) for d in dims])
+        assert [d.value for d in dims] == [inC, H, W]
+        got = _infer_each(gpu, m, x)
+        assert gpu.acfun_model_output_size(m) == want.shape[1]
+    finally:
+        gpu.acfun_model_destroy(m)
+    assert got.shape == want.shape
+    assert rel_err(got, want) < TOL, rel_err(got, want)
+
+
+def test_model_batch_equals_single(gpu, rng, tmp_path):
+    inC, H, W, recs = models.fusion_v1(rng)
+    path = _write(tmp_path, "fusion.acfun", inC, H, W, recs, 1)
+    x = rng.uniform(-1, 1, (4, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path)
+    try:
+        single = _infer_each(gpu, m, x)
+        batch = np.full_like(single, np.nan)
+        assert gpu.acfun_model_infer_batch(m, 4, P(x), P(batch)) == single.shape[1]
+    finally:
+        gpu.acfun_model_destroy(m)
+    assert rel_err(batch, single) < 1e-5, rel_err(batch, single)
+
+
+def test_model_device_batch(gpu, rng, tmp_path):
+    import torch
+    inC, H, W, recs = models.fusion_v1(rng)
+    path = _write(tmp_path, "fusion.acfun", inC, H, W, recs, 1)
+    x = rng.uniform(-1, 1, (3, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path)
+    try:
+        host = np.full((3, 10), np.nan, np.float32)
+        assert gpu.acfun_model_infer_batch(m, 3, P(x), P(host)) == 10
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.full((3, 10), float("nan"), device="cuda")
+        s = torch.cuda.current_stream()
+        assert gpu.acfun_dev_model_infer_batch(m, 3, dx.data_ptr(), dy.data_ptr(),
+                                               s.cuda_stream) == 10
+        s.synchronize()
+    finally:
+        gpu.acfun_model_destroy(m)
+    assert_bitexact(dy.cpu().numpy(), host, "device vs host batch")
+
+
+def test_model_v2_residual_matches_oracle(gpu, rng, tmp_path):
+    inC, H, W, recs = models.small_resnet_v2(rng)
+    path = _write(tmp_path, "res.acfun", inC, H, W, recs, 2)
+    x = rng.uniform(0, 1, (2, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path)
+    try:
+        got = np.full((2, 10), np.nan, np.float32)
+        assert gpu.acfun_model_infer_batch(m, 2, P(x), P(got)) == 10, capi.last_error()
+    finally:
+        gpu.acfun_model_destroy(m)
+    want = omodel.run(open(path, "rb").read(), x)
+    assert rel_err(got, want) < TOL, rel_err(got, want)
+
+
+def test_model_int8_chain_exact(gpu, rng, tmp_path):
+    """int8 mode (flags=1): every dense conv quantized at load, run through the
+    acfun_conv2d_int8 rules with the batch's dynamic activation scale."""
+    inC, H, W, recs = models.int8_chain_v1(rng)
+    path = _write(tmp_path, "i8.acfun", inC, H, W, recs, 1)
+    for n in (1, 3):
+        x = rng.uniform(0, 1, (n, H, W, inC)).astype(np.float32)
+        want = omodel.run(open(path, "rb").read(), x, int8=True)
+        m = _load(gpu, path, 1)
+        try:
+            got = np.full(want.shape, np.nan, np.float32)
+            assert gpu.acfun_model_infer_batch(m, n, P(x), P(got)) == want.shape[1]
+        finally:
+            gpu.acfun_model_destroy(m)
+        assert_bitexact(got, want, f"int8 chain, batch {n}")
+
+
+def test_model_rejects_truncated_file(gpu, rng, tmp_path):
+    inC, H, W, recs = models.fusion_v1(rng)
+    blob = acfun0.encode(inC, H, W, recs, version=1)
+    for cut in (10, 30, len(blob) // 2, len(blob) - 4):
+        path = str(tmp_path / f"cut{cut}.acfun")
+        with open(path, "wb") as f:
+            f.write(blob[:cut])
+        assert not gpu.acfun_model_load(path.encode())
+        assert capi.last_error()
+    assert not gpu.acfun_model_load(str(tmp_path / "missing.acfun").encode())
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_resnet50_224_matches_oracle(gpu, rng, tmp_path, int8):
+    """Config 5's full graph (ResNet-50-style v1.5, 224x224) on one image."""
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5))
+    path = _write(tmp_path, "r50.acfun", inC, H, W, recs, 2)
+    x = rng.uniform(0, 1, (1, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path, 1 if int8 else 0)
+    try:
+        got = np.full((1, 1000), np.nan, np.float32)
+        assert gpu.acfun_model_infer_batch(m, 1, P(x), P(got)) == 1000, capi.last_error()
+    finally:
+        gpu.acfun_model_destroy(m)
+    want = omodel.run(open(path, "rb").read(), x, int8=int8)
+    assert rel_err(got, want) < TOL, rel_err(got, want)
+    assert abs(float(got.sum()) - 1.0) < 1e-4

@@ -1,0 +1,133 @@
+"""CPU pins of the oracle's ACFUN0 executor (oracle/model.py) against the
+compiled reference's loader and executor (src/model.cpp:106-349 via
+oracle/_ref): same file, same images, per-image inference."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle.model as omodel
+from acfun_amd import acfun0
+
+from tests import models
+from tests.helpers import P, rel_err
+
+
+def _ref_infer(ref, path, x):
+    m = ref.acfun_model_load(path.encode())
+    assert m, "reference rejected the model"
+    try:
+        # acfun_model_output_size is 0 until the first inference (src/model.cpp:265,346),
+        # so infer into a large buffer and keep the count it returns
+        assert ref.acfun_model_output_size(m) == 0
+        outs = []
+        for img in x:
+            y = np.full(1 << 16, np.nan, np.float32)
+            n = ref.acfun_model_infer(m, P(np.ascontiguousarray(img)), P(y))
+            assert 0 < n == ref.acfun_model_output_size(m)
+            outs.append(y[:n].copy())
+        return np.stack(outs)
+    finally:
+        ref.acfun_model_destroy(m)
+
+
+def test_oracle_model_matches_reference_v1(ref, rng, tmp_path):
+    inC, H, W, recs = models.fusion_v1(rng)
+    path = str(tmp_path / "fusion.acfun")
+    acfun0.write(path, inC, H, W, recs, version=1)
+    x = rng.uniform(-1, 1, (3, H, W, inC)).astype(np.float32)
+    want = _ref_infer(ref, path, x)
+    got = omodel.run(open(path, "rb").read(), x)
+    assert got.shape == want.shape
+    # fp32 routes (Winograd, im2col GEMM) vs the oracle's f64 convolutions
+    assert rel_err(got, want) < 1e-4, rel_err(got, want)
+    np.testing.assert_allclose(got.sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_fusion_rules(ref, rng, tmp_path):
+    """The fused graph of fusion_v1 as the reference's rules give it, and the
+    dropped ReLU made observable: the reference computes the same output with
+    and without a ReLU between a conv and a MaxPool (with no ReLU after the
+    pool, a kept ReLU would change it)."""
+    seed = int(rng.integers(1 << 30))
+    inC, H, W, recs = models.fusion_v1(np.random.default_rng(seed))
+    blob = acfun0.encode(inC, H, W, recs, version=1)
+    layers = omodel.fuse(omodel.parse(blob)[4])
+    # conv+bn | relu | conv+relu+bn | pool+relu | convg+relu | dw+bn | relu |
+    # 1x1 (relu dropped) | pool | bn | conv | fc | softmax
+    assert [F["type"] for F in layers] == [1, 3, 1, 4, 7, 7, 3, 1, 4, 6, 1, 2, 5]
+    assert [F["act"] for F in layers] == [0, 0, 1, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0]
+    assert [F["post_relu"] for F in layers] == [0, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0]
+
+    x = rng.uniform(-1, 1, (2, H, W, inC)).astype(np.float32)
+    pa = str(tmp_path / "a.acfun")
+    acfun0.write(pa, inC, H, W, recs, version=1)
+    _, _, _, recs_b = models.fusion_v1(np.random.default_rng(seed), drop_relu=False)
+    pb = str(tmp_path / "b.acfun")
+    acfun0.write(pb, inC, H, W, recs_b, version=1)
+    ya, yb = _ref_infer(ref, pa, x), _ref_infer(ref, pb, x)
+    np.testing.assert_array_equal(ya, yb)
+    np.testing.assert_array_equal(omodel.run(open(pa, "rb").read(), x),
+                                  omodel.run(open(pb, "rb").read(), x))
+    # the same ReLU placed after the pool is kept, and it matters
+    recs_c = list(recs_b)
+    recs_c.insert(16, ("relu",))
+    assert recs_c[15][0] == "maxpool" and recs_c[17][0] == "bn"
+    pc = str(tmp_path / "c.acfun")
+    acfun0.write(pc, inC, H, W, recs_c, version=1)
+    yc = _ref_infer(ref, pc, x)
+    assert np.max(np.abs(yc - ya)) > 1e-5       # fp32 noise here is ~1e-7
+    assert rel_err(omodel.run(open(pc, "rb").read(), x), yc) < 1e-4
+
+
+def test_reference_rejects_version2_records(ref, rng, tmp_path):
+    """Record types 8-10 are this library's extension: the reference loader
+    refuses them (src/model.cpp:193), so v2 models are pinned by the oracle's
+    composition of reference-pinned operators instead."""
+    inC, H, W, recs = models.small_resnet_v2(rng)
+    path = str(tmp_path / "res.acfun")
+    acfun0.write(path, inC, H, W, recs, version=2)
+    assert not ref.acfun_model_load(path.encode())
+
+
+def test_oracle_int8_chain_uses_reference_int8_conv(ref, rng, tmp_path):
+    """The oracle's int8 model = per-layer acfun_quantize_weights + acfun_conv2d_int8
+    of the compiled reference, bit for bit (fp32 maxpool between)."""
+    inC, H, W, recs = models.int8_chain_v1(rng)
+    path = str(tmp_path / "i8.acfun")
+    acfun0.write(path, inC, H, W, recs, version=1)
+    x = rng.uniform(0, 1, (1, H, W, inC)).astype(np.float32)
+    got = omodel.run(open(path, "rb").read(), x, int8=True)
+    # the same chain through the reference's own API
+    layers = omodel.fuse(omodel.parse(open(path, "rb").read())[4])
+    cur = x
+    for F in layers:
+        if F["type"] == 1:
+            KH, KW, Cout, s, p = F["p"][:5]
+            N, h, w_, ci = cur.shape
+            K = KH * KW * ci
+            wf = np.ascontiguousarray(F["w"], np.float32).reshape(K, Cout)
+            sc = np.empty(Cout, np.float32)
+            q = np.empty((K, Cout), np.int8)
+            ref.acfun_quantize_weights(P(wf), K, Cout, P(sc), P(q))
+            OH = (h + 2 * p - KH) // s + 1
+            OW = (w_ + 2 * p - KW) // s + 1
+            y = np.empty((N, OH, OW, Cout), np.float32)
+            ref.acfun_conv2d_int8(P(np.ascontiguousarray(cur)), N, h, w_, ci, P(q), P(sc),
+                                  P(np.ascontiguousarray(F["b"], np.float32)), KH, KW, Cout, s,
+                                  p, C.c_float(0.0), P(y), F["act"])
+            cur = y
+        elif F["type"] == 4:
+            pool, s, p = F["p"][:3]
+            N, h, w_, ci = cur.shape
+            OH = (h + 2 * p - pool) // s + 1
+            y = np.empty((N, OH, OH, ci), np.float32)
+            fn = ref.acfun_maxpool_relu if F["post_relu"] else ref.acfun_maxpool
+            fn(P(np.ascontiguousarray(cur)), N, h, w_, ci, pool, s, p, P(y))
+            cur = y
+        elif F["type"] == 3:                 # Conv -> BN -> ReLU leaves a separate ReLU
+            cur = np.ascontiguousarray(cur).copy()
+            ref.acfun_relu(P(cur), cur.size)
+        else:
+            pytest.fail(f"unexpected layer {F['type']}")
+    np.testing.assert_array_equal(got, cur.reshape(1, -1))
