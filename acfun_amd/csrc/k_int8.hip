@@ -343,25 +343,28 @@ __global__ void k_u8_to_s8(const uint8_t* __restrict__ x, long long pix, int Cin
 }
 
 // wq [taps*Cin][N] -> Bt [N][ldb], row k' = tap*Cinp + ic (zero for ic >= Cin
-// and for k' >= taps*Cinp).
-__global__ void k_prep_weights(const int8_t* __restrict__ wq, int taps, int Cin, int Cinp, int N,
-                               int8_t* __restrict__ Bt, int ldb) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)N * ldb) return;
-    int n = (int)(i / ldb);
-    int kp = (int)(i - (long long)n * ldb);
-    int tap = kp / Cinp, ic = kp - tap * Cinp;
-    int8_t v = 0;
-    if (tap < taps && ic < Cin) v = wq[((long long)tap * Cin + ic) * N + n];
-    Bt[i] = v;
-}
-
-__global__ void k_colsum(const int8_t* __restrict__ wq, int K, int N, int* __restrict__ Sw) {
-    int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= N) return;
-    int s = 0;
-    for (int k = 0; k < K; ++k) s += wq[(long long)k * N + j];
-    Sw[j] = s;
+// and for k' >= taps*Cinp), and Sw[n] = sum_k wq[k][n] (exact i32).  One
+// 256-thread block per output channel n: the row is written contiguously and
+// summed in the same pass.
+__global__ __launch_bounds__(256) void k_prep_weights(const int8_t* __restrict__ wq, int taps,
+                                                      int Cin, int Cinp, int N,
+                                                      int8_t* __restrict__ Bt, int ldb,
+                                                      int* __restrict__ Sw) {
+    const int n = blockIdx.x;
+    int sum = 0;
+    for (int kp = threadIdx.x; kp < ldb; kp += 256) {
+        int tap = kp / Cinp, ic = kp - tap * Cinp;
+        int8_t v = 0;
+        if (tap < taps && ic < Cin) v = wq[((long long)tap * Cin + ic) * N + n];
+        Bt[(long long)n * ldb + kp] = v;
+        sum += v;
+    }
+    __shared__ int red[4];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) Sw[n] = red[0] + red[1] + red[2] + red[3];
 }
 
 // acfun_quantize_weights (src/conv_int8.cpp:24-37): one lane per column.
@@ -435,11 +438,9 @@ bool prep_weights(const int8_t* wq, int taps, int Cin, int Cinp, int N, hipStrea
     w.bt = Scratch((size_t)N * w.ldb, s);
     w.sw = Scratch((size_t)N * sizeof(int), s);
     if (!w.bt.p || !w.sw.p) return false;
-    hipLaunchKernelGGL(k_prep_weights, g1((long long)N * w.ldb), dim3(256), 0, s, wq, taps, Cin, Cinp,
-                       N, w.bt.as<int8_t>(), w.ldb);
-    if (!check_launch("k_prep_weights")) return false;
-    hipLaunchKernelGGL(k_colsum, g1(N), dim3(256), 0, s, wq, taps * Cin, N, w.sw.as<int>());
-    return check_launch("k_colsum");
+    hipLaunchKernelGGL(k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N,
+                       w.bt.as<int8_t>(), w.ldb, w.sw.as<int>());
+    return check_launch("k_prep_weights");
 }
 
 }  // namespace
@@ -497,7 +498,8 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
 }
 
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
-                     const float* bias, int Cout, float* out, int act, hipStream_t s) {
+                     const float* bias, int Cout, float* out, int act, hipStream_t s,
+                     const I8Weights* pre) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
                       g.W >= 3 && g.Cin >= 4 && Cout >= 4;
@@ -514,28 +516,36 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     float* beta = alpha + Cout;
     float* alpha_w = beta + Cout;
     PrepW w;
-    if (!prep_weights(wq, g.KH * g.KW, g.Cin, Cinp, Cout, s, w)) return false;
+    const int8_t* bt;
+    const int* sw;
+    int ldb;
+    if (pre && pre->bt && pre->taps == g.KH * g.KW && pre->Cin == g.Cin && pre->N == Cout) {
+        bt = pre->bt; sw = pre->sw; ldb = pre->ldb;
+    } else {
+        if (!prep_weights(wq, g.KH * g.KW, g.Cin, Cinp, Cout, s, w)) return false;
+        bt = w.bt.as<int8_t>(); sw = w.sw.as<int>(); ldb = w.ldb;
+    }
     hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, s, bits, 1, 0u);
     if (!check_launch("k_fill_u32")) return false;
     int nb = (int)((inN / 4 + 255) / 256);
     nb = nb < 1 ? 1 : (nb > 4 * num_cus() ? 4 * num_cus() : nb);
     hipLaunchKernelGGL(k_absmax, dim3(nb), dim3(256), 0, s, in, inN, bits);
     if (!check_launch("k_absmax")) return false;
-    hipLaunchKernelGGL(k_int8_params, g1(Cout), dim3(256), 0, s, bits, ws, bias, w.sw.as<int>(),
+    hipLaunchKernelGGL(k_int8_params, g1(Cout), dim3(256), 0, s, bits, ws, bias, sw,
                        Cout, alpha, beta, alpha_w, scal);
     if (!check_launch("k_int8_params")) return false;
     hipLaunchKernelGGL(k_quant_act, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp,
                        q.as<int8_t>(), scal, wino ? 2 : 0, g.Cin & ~15);
     if (!check_launch("k_quant_act")) return false;
     I8P p{};
-    p.A = q.as<int8_t>(); p.Bt = w.bt.as<int8_t>(); p.M = g.N * g.OH * g.OW; p.N = Cout;
-    p.K = g.KH * g.KW * Cinp; p.ldb = w.ldb;
+    p.A = q.as<int8_t>(); p.Bt = bt; p.M = g.N * g.OH * g.OW; p.N = Cout;
+    p.K = g.KH * g.KW * Cinp; p.ldb = ldb;
     p.H = g.H; p.W = g.W; p.Cinp = Cinp; p.KW = g.KW; p.stride = g.stride; p.pad = g.pad;
     p.OH = g.OH; p.OW = g.OW; p.act = act; p.scal = scal; p.Cf = out; p.ldc = Cout;
     if (wino) {
         p.epi = EPI_WINO; p.alpha = alpha_w; p.bias = bias;
     } else {
-        p.epi = EPI_GEMM; p.alpha = alpha; p.beta = beta; p.Sw = w.sw.as<int>();
+        p.epi = EPI_GEMM; p.alpha = alpha; p.beta = beta; p.Sw = sw;
     }
     return launch_i8(p, true, true, s);
 }
@@ -562,6 +572,27 @@ bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8
     p.H = H; p.W = W; p.Cinp = Cinp; p.KW = 3; p.stride = 1; p.pad = 1; p.OH = H; p.OW = W;
     p.act = act; p.Cf = out; p.ldc = Cout; p.epi = EPI_WINO; p.alpha = aw.as<float>(); p.bias = bias;
     return launch_i8(p, true, true, s);
+}
+
+bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStream_t s) {
+    i8_release(w);
+    int Cinp = rup(Cin, 16);
+    w.ldb = rup(taps * Cinp, 16);
+    if (!check(hipMalloc((void**)&w.bt, (size_t)N * w.ldb), "hipMalloc(int8 weights)") ||
+        !check(hipMalloc((void**)&w.sw, (size_t)N * sizeof(int)), "hipMalloc(int8 sums)")) {
+        i8_release(w);
+        return false;
+    }
+    w.taps = taps; w.Cin = Cin; w.N = N;
+    hipLaunchKernelGGL(k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N, w.bt,
+                       w.ldb, w.sw);
+    return check_launch("k_prep_weights");
+}
+
+void i8_release(I8Weights& w) {
+    if (w.bt) (void)hipFree(w.bt);
+    if (w.sw) (void)hipFree(w.sw);
+    w = I8Weights{};
 }
 
 }  // namespace acfun

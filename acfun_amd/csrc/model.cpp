@@ -48,6 +48,7 @@ struct Layer {
     // int8 variant of a conv: quantized weights and per-channel scales
     int8_t* wq = nullptr;
     float* ws = nullptr;
+    I8Weights i8;        // wq prepared for the int8 GEMM once, at load
 };
 
 struct Raw {
@@ -139,6 +140,7 @@ void free_layers(AcfunModel* m) {
         if (L.b) hipFree(L.b);
         if (L.wq) hipFree(L.wq);
         if (L.ws) hipFree(L.ws);
+        i8_release(L.i8);
     }
     m->layers.clear();
 }
@@ -277,7 +279,10 @@ AcfunModel* load_impl(const char* path, int flags) {
                 quantize_cols(hw, K, Cout, sc, q);
                 if (!upload(sc.data(), sc.size(), &F.ws) ||
                     !check(hipMalloc((void**)&F.wq, q.size()), "hipMalloc(wq)") ||
-                    !check(hipMemcpy(F.wq, q.data(), q.size(), hipMemcpyHostToDevice), "H2D wq"))
+                    !check(hipMemcpy(F.wq, q.data(), q.size(), hipMemcpyHostToDevice), "H2D wq") ||
+                    !i8_prepare(F.wq, L.p[0] * L.p[1], K / (L.p[0] * L.p[1]), Cout, F.i8,
+                                lib_stream()) ||
+                    !check(hipStreamSynchronize(lib_stream()), "int8 weight prep"))
                     fail = true;
             }
         } else if (L.type == 3) {  // :229-233
@@ -395,7 +400,7 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                 int groups = F.type == 7 ? F.p[5] : 1;
                 if (m->int8 && F.type == 1 && F.wq) {
                     ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
-                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, F.act, s);
+                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, F.act, s, &F.i8);
                 } else {
                     ok = conv2d_route_f32(x, N, in.H, in.W, in.C, F.w, F.b, F.p[0], F.p[1], o.C,
                                           F.p[3], F.p[4], groups > 1 ? groups : 1, y, F.act, s);

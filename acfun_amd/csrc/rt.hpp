@@ -149,8 +149,19 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
                           const float* alpha, const float* beta, int Cout, float* out, int act,
                           hipStream_t s);
 // acfun_conv2d_int8 end to end on device (absmax, params, quantize, conv).
+// int8 conv weights prepared once for k_igemm_i8: Bt [N][ldb] (row k' = tap*Cinp + ic,
+// zero padded) and Sw[N] = the quantized weights' column sums, in memory owned
+// by the handle (hipMalloc) until i8_release (hipFree, which waits for the device).
+struct I8Weights {
+    int8_t* bt = nullptr;
+    int* sw = nullptr;
+    int ldb = 0, taps = 0, Cin = 0, N = 0;
+};
+bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStream_t s);
+void i8_release(I8Weights& w);
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
-                     const float* bias, int Cout, float* out, int act, hipStream_t s);
+                     const float* bias, int Cout, float* out, int act, hipStream_t s,
+                     const I8Weights* pre = nullptr);
 // The int8 Winograd-route entry with caller-supplied scales.
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,
                        const float* ws, const float* bias, int Cout, float s_in, float inv_s,
