@@ -89,6 +89,160 @@ __global__ void k_dwconv3_c4(const float4* __restrict__ in, int N, int H, int W,
     out[idx] = acc;
 }
 
+// Depthwise 3x3, stride S (1 or 2), C % 4 == 0: a lane owns 4 channels and an
+// OHB x OWB = 2 x 4 block of outputs.  Its 36 weights stay in registers and
+// each of the (OHB-1)*S+3 input rows is loaded once, as (OWB-1)*S+3 columns,
+// for every output it feeds.  Per channel the arithmetic is the reference's
+// AVX-512 path (src/dw_avx512.cpp:20-69): acc = bias, then one fmaf per
+// in-range tap in kh, kw order; out-of-range taps are skipped.
+// Lane index = ((n*nOHB + ohb)*nOWB + owb)*C4 + c4 (channel quads fastest,
+// so a wave's loads and stores cover whole pixels).
+template <int S>
+__global__ __launch_bounds__(256) void k_dwconv3_blk(const float4* __restrict__ in, int H, int W,
+                                                     int C4, const float* __restrict__ w,
+                                                     const float* __restrict__ bias, int pad,
+                                                     int OH, int OW, int nOHB, int nOWB,
+                                                     int total, float4* __restrict__ out, int act) {
+    constexpr int OWB = 4, OHB = 2, NCOL = (OWB - 1) * S + 3, NROW = (OHB - 1) * S + 3;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;
+    int q = t / C4;
+    const int c4 = t - q * C4;
+    const int owb = q % nOWB;
+    q /= nOWB;
+    const int ohb = q % nOHB;
+    const int n = q / nOHB;
+    const int ow0 = owb * OWB, oh0 = ohb * OHB;
+    const int c = c4 * 4;
+    float wk[4][9];
+    {
+        const float4* w4 = (const float4*)(w + (size_t)c * 9);   // 36 floats, 16-byte aligned
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            float4 v = w4[i];
+            wk[(4 * i + 0) / 9][(4 * i + 0) % 9] = v.x;
+            wk[(4 * i + 1) / 9][(4 * i + 1) % 9] = v.y;
+            wk[(4 * i + 2) / 9][(4 * i + 2) % 9] = v.z;
+            wk[(4 * i + 3) / 9][(4 * i + 3) % 9] = v.w;
+        }
+    }
+    float4 b4 = bias ? make_float4(bias[c], bias[c + 1], bias[c + 2], bias[c + 3])
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc[OHB][OWB];
+#pragma unroll
+    for (int r = 0; r < OHB; ++r)
+#pragma unroll
+        for (int o = 0; o < OWB; ++o) acc[r][o] = b4;
+    const float4* img = in + (size_t)n * H * W * C4 + c4;
+    const int iw0 = ow0 * S - pad, ih0 = oh0 * S - pad;
+#pragma unroll
+    for (int ir = 0; ir < NROW; ++ir) {
+        const int ih = ih0 + ir;
+        const bool rok = (unsigned)ih < (unsigned)H;
+        float4 col[NCOL];
+        bool cok[NCOL];
+#pragma unroll
+        for (int j = 0; j < NCOL; ++j) {
+            const int iw = iw0 + j;
+            cok[j] = rok && (unsigned)iw < (unsigned)W;
+            col[j] = cok[j] ? img[((size_t)ih * W + iw) * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int r = 0; r < OHB; ++r) {
+            const int kh = ir - r * S;                   // tap row of output row oh0 + r
+            if (kh < 0 || kh > 2) continue;
+#pragma unroll
+            for (int o = 0; o < OWB; ++o) {
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int j = o * S + kw;
+                    const int tp = kh * 3 + kw;
+                    if (cok[j]) {
+                        acc[r][o].x = fmaf(col[j].x, wk[0][tp], acc[r][o].x);
+                        acc[r][o].y = fmaf(col[j].y, wk[1][tp], acc[r][o].y);
+                        acc[r][o].z = fmaf(col[j].z, wk[2][tp], acc[r][o].z);
+                        acc[r][o].w = fmaf(col[j].w, wk[3][tp], acc[r][o].w);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < OHB; ++r) {
+        if (oh0 + r >= OH) break;
+        float4* dst = out + (((size_t)n * OH + oh0 + r) * OW + ow0) * C4 + c4;
+#pragma unroll
+        for (int o = 0; o < OWB; ++o) {
+            if (ow0 + o >= OW) break;
+            float4 v = acc[r][o];
+            if (act == 1) {
+                v.x = vmax(v.x, 0.f); v.y = vmax(v.y, 0.f); v.z = vmax(v.z, 0.f); v.w = vmax(v.w, 0.f);
+            }
+            dst[(size_t)o * C4] = v;
+        }
+    }
+}
+
+// MaxPool 3x3 stride 2 for C % 4 == 0 with every channel on the max_ps rule
+// (vec_end == C): a lane owns 4 channels and 4 consecutive outputs of a row;
+// in-range taps only, initial -1e30 (src/maxpool_avx512.cpp:15-62).
+// Lane index = ((n*OH + oh)*nOWB + owb)*C4 + c4.
+__global__ __launch_bounds__(256) void k_maxpool3s2_row(const float4* __restrict__ in, int H,
+                                                        int W, int C4, int pad, int OH, int OW,
+                                                        int nOWB, int total,
+                                                        float4* __restrict__ out, int post_relu) {
+    constexpr int OWB = 4, S = 2, NCOL = (OWB - 1) * S + 3;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;
+    int q = t / C4;
+    const int c4 = t - q * C4;
+    const int owb = q % nOWB;
+    const int row = q / nOWB;                        // n*OH + oh
+    const int n = row / OH, oh = row - n * OH;
+    const int ow0 = owb * OWB;
+    float4 mx[OWB];
+#pragma unroll
+    for (int o = 0; o < OWB; ++o) mx[o] = make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
+    const float4* img = in + (size_t)n * H * W * C4 + c4;
+    const int iw0 = ow0 * S - pad;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+        const int ih = oh * S - pad + kh;
+        if ((unsigned)ih >= (unsigned)H) continue;
+        float4 col[NCOL];
+        bool cok[NCOL];
+#pragma unroll
+        for (int j = 0; j < NCOL; ++j) {
+            const int iw = iw0 + j;
+            cok[j] = (unsigned)iw < (unsigned)W;
+            col[j] = cok[j] ? img[((size_t)ih * W + iw) * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int o = 0; o < OWB; ++o) {
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const int j = o * S + kw;
+                if (cok[j]) {
+                    mx[o].x = vmax(mx[o].x, col[j].x);
+                    mx[o].y = vmax(mx[o].y, col[j].y);
+                    mx[o].z = vmax(mx[o].z, col[j].z);
+                    mx[o].w = vmax(mx[o].w, col[j].w);
+                }
+            }
+        }
+    }
+    float4* dst = out + ((size_t)row * OW + ow0) * C4 + c4;
+#pragma unroll
+    for (int o = 0; o < OWB; ++o) {
+        if (ow0 + o >= OW) break;
+        float4 v = mx[o];
+        if (post_relu) {
+            v.x = vmax(v.x, 0.f); v.y = vmax(v.y, 0.f); v.z = vmax(v.z, 0.f); v.w = vmax(v.w, 0.f);
+        }
+        dst[(size_t)o * C4] = v;
+    }
+}
+
 // Grouped direct conv, weights [g][KH*KW*Cin_p][Cout_p].  vec_end / fma_all
 // encode which channels the reference's dispatcher (src/group_conv.cpp:60-79)
 // runs through a fused-multiply-add vector kernel.
@@ -267,6 +421,23 @@ bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, con
     int OW = (W + 2 * pad - KW) / stride + 1;
     if (OH <= 0 || OW <= 0 || KH <= 0 || KW <= 0) return true;
     bool al = (((uintptr_t)in | (uintptr_t)out) & 15u) == 0;
+    const bool w_al = ((uintptr_t)w & 15u) == 0;
+    const int C4 = C / 4;
+    const long long nblk = (long long)N * ((OH + 1) / 2) * ((OW + 3) / 4) * C4;
+    if (KH == 3 && KW == 3 && C % 4 == 0 && al && w_al && (stride == 1 || stride == 2) &&
+        nblk < (1ll << 31) && (long long)N * H * W * C < (1ll << 31)) {
+        const int nOHB = (OH + 1) / 2, nOWB = (OW + 3) / 4, total = (int)nblk;
+        KTimer kt("k_dwconv", s);
+        if (stride == 1)
+            hipLaunchKernelGGL(k_dwconv3_blk<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                               s, (const float4*)in, H, W, C4, w, bias, pad, OH, OW, nOHB, nOWB,
+                               total, (float4*)out, act);
+        else
+            hipLaunchKernelGGL(k_dwconv3_blk<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                               s, (const float4*)in, H, W, C4, w, bias, pad, OH, OW, nOHB, nOWB,
+                               total, (float4*)out, act);
+        return check_launch("k_dwconv3_blk");
+    }
     if (KH == 3 && KW == 3 && C % 4 == 0 && al) {
         long long total = (long long)N * OH * OW * (C / 4);
         KTimer kt("k_dwconv", s);
@@ -306,6 +477,17 @@ bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stri
     int OW = (W + 2 * pad - pool) / stride + 1;
     if (OH <= 0 || OW <= 0) return true;
     int vec_end = C >= 16 ? (C & ~15) : (C >= 8 ? (C & ~7) : 0);
+    const long long nq = (long long)N * OH * ((OW + 3) / 4) * (C / 4);
+    if (pool == 3 && stride == 2 && vec_end == C && C % 4 == 0 &&
+        (((uintptr_t)in | (uintptr_t)out) & 15u) == 0 && nq < (1ll << 31) &&
+        (long long)N * H * W * C < (1ll << 31)) {
+        const int total = (int)nq;
+        KTimer kt("k_maxpool", s);
+        hipLaunchKernelGGL(k_maxpool3s2_row, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           (const float4*)in, H, W, C / 4, pad, OH, OW, (OW + 3) / 4, total,
+                           (float4*)out, post_relu);
+        return check_launch("k_maxpool3s2_row");
+    }
     long long total = (long long)N * OH * OW * C;
     KTimer kt("k_maxpool", s);
     hipLaunchKernelGGL(k_maxpool, grid1d(total), dim3(256), 0, s, in, N, H, W, C, pool, stride,
