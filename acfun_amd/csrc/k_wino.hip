@@ -13,6 +13,8 @@
 // bias and ReLU, so the input is read once and the output written once.
 #include "rt.hpp"
 
+#include <type_traits>
+
 namespace acfun {
 namespace {
 
@@ -647,6 +649,286 @@ __global__ __launch_bounds__(512) void k_wino23(
     }
 }
 
+// F(2,3), one 32-tile x 32-channel unit per 256-thread workgroup, three
+// workgroups per CU.
+//
+// Block = R x TC tiles (R*TC = 32, TC = 16 or 8, both compile-time) of one
+// image x 32 output channels.  Wave i accumulates the 4 points of row i of
+// the 4x4 Winograd grid for all 32 tiles (v_mfma_f32_32x32x2f32, M = tiles,
+// N = channels, K = 2 channels: 4 x 16 accumulators).  Input channels are
+// consumed in chunks of 8 (one MFMA k-step pair per lane half g = lane/32
+// holding a quad of 4 channels).  The (2R+2) x (2TC+2) pixels of a chunk are
+// DMA'd (buffer_load ... lds, zeros past the resources' ends) two chunks
+// ahead into one of three X buffers, the filter chunk U[16][32][8] (an L2
+// hit) one chunk ahead into one of two U buffers; the wait before a chunk
+// leaves the newest X loads in flight.  LDS is 53 KB, so three workgroups
+// share a CU and one's loads, barriers and stores overlap the others' MFMAs.
+//
+// LDS layouts (16-byte quads): X [row][plane = col%2][kk = col/2][2 quads]
+// with kk padded to TC+1 and quad q at slot q ^ ((kk >> log2(TC/2)) & 1);
+// U [point][co][2 quads] with quad q at slot q ^ ((co >> 3) & 1).  Both
+// make every 16-lane ds_read_b128 group hit 64 distinct banks.
+//
+// Epilogue: wave i reduces its row with AT (S_i[c] = sum_j AT[c][j] M[i][j])
+// into LDS; every thread then forms Y[0][c] = S0+S1+S2, Y[1][c] = S1-S2+S3 for
+// one tile and 4 channels, adds bias, applies ReLU and stores 16-byte quads.
+template <int TC, int ROW>
+struct W23Row;   // BT row ROW of a patch column: t = d[A] -/+ d[B]
+template <int TC> struct W23Row<TC, 0> { static constexpr int A = 0, B = 2, PLUS = 0; };
+template <int TC> struct W23Row<TC, 1> { static constexpr int A = 1, B = 2, PLUS = 1; };
+template <int TC> struct W23Row<TC, 2> { static constexpr int A = 2, B = 1, PLUS = 0; };
+template <int TC> struct W23Row<TC, 3> { static constexpr int A = 3, B = 1, PLUS = 0; };
+
+template <int TC>
+struct W23Cfg {
+    static constexpr int R = 32 / TC;
+    static constexpr int NR = 2 * R + 2;               // staged pixel rows
+    static constexpr int TCP = TC + 1;                 // kk per plane (padded)
+    static constexpr int SWZ = TC == 16 ? 3 : 2;       // swizzle bit of kk
+    static constexpr int XSLOTS = NR * 2 * TCP * 2;
+    static constexpr int XBLK = (XSLOTS + 63) / 64;    // 64-slot DMA blocks
+    static constexpr int XFL = XSLOTS * 4;             // floats (the last block's extra lanes
+                                                       // are masked off)
+    static constexpr int UFL = 16 * 32 * 2 * 4;        // 4096 floats
+    static constexpr int UOFF = 3 * XFL;               // X: 3 buffers, then U: 2 buffers
+    static constexpr int KX = (XBLK + 3) / 4;          // X blocks per wave (at most)
+    static constexpr int SST = 40;                     // epilogue tile stride (floats)
+    static constexpr int LDS = (3 * XFL + 2 * UFL) * 4;  // bytes
+    static_assert(4 * 2 * 32 * SST <= 3 * XFL + 2 * UFL, "epilogue tile fits the staging buffers");
+    static_assert(3 * LDS <= 160 * 1024, "three workgroups per CU");
+};
+
+template <int TC>
+__global__ __launch_bounds__(256, 3) void k_wino23u(
+    const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
+    float* __restrict__ out, int H, int W, int Cin, int Cinp, int Cout, int rblocks, int act) {
+    using CF = W23Cfg<TC>;
+    constexpr int R = CF::R, TCP = CF::TCP;
+    constexpr unsigned kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // = transform row
+    const int li = lane & 31, g = lane >> 5;
+    const int n = blockIdx.y / rblocks;
+    const int ty0 = (blockIdx.y - n * rblocks) * R;
+    const int tx0 = blockIdx.x * TC;
+    const int cob = blockIdx.z * 32;
+    const float* __restrict__ img = in + (long long)n * H * W * Cin;
+
+    // ---- DMA descriptors.  X: wave w issues blocks w, w+4, ... of XSLOTS
+    // 16-byte slots; slot -> (row, plane, kk, quad slot) -> pixel + channel
+    // quad.  U: wave w issues blocks w, w+4, w+8, w+12 = points w+4t; lane l
+    // covers channel row l/2, quad slot l&1.
+    unsigned xv[CF::KX];
+    unsigned xq = 0;
+#pragma unroll
+    for (int k = 0; k < CF::KX; ++k) {
+        const int sl = (wave + 4 * k) * 64 + lane;
+        const int qslot = sl & 1;
+        const int pk = sl >> 1;                         // (row*2 + plane)*TCP + kk
+        const int rp = pk / TCP, kk = pk - rp * TCP;
+        const int row = rp >> 1, plane = rp & 1;
+        const int q = qslot ^ ((kk >> CF::SWZ) & 1);
+        const int ih = 2 * ty0 - 1 + row, iw = 2 * tx0 - 1 + 2 * kk + plane;
+        const bool ok = sl < CF::XSLOTS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+        xv[k] = ok ? (unsigned)((ih * W + iw) * Cin + 4 * q) * 4u : kOOB;
+        xq |= (unsigned)q << k;
+    }
+    unsigned uv;
+    {
+        const int co = lane >> 1;
+        const int q = (lane & 1) ^ ((co >> 3) & 1);
+        uv = cob + co < Cout ? (unsigned)((cob + co) * Cinp + 4 * q) * 4u : kOOB;
+    }
+    const unsigned upt = 4u * Cout * Cinp;             // bytes per point
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, H * W * Cin * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ures =
+        __builtin_amdgcn_make_buffer_rsrc((void*)U, (short)0, (int)(16 * upt), 0x00020000);
+    const bool ragged = (Cin & 7) != 0;
+    // X blocks this wave issues per chunk (uniform): KX or KX-1
+    const int nxw = CF::XBLK > wave + 4 * (CF::KX - 1) ? CF::KX : CF::KX - 1;
+    auto dma_u = [&](int t, int c0, float* base) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ures, (lds_void*)(base + (wave + 4 * t) * 256), 16, uv,
+            c0 * 4 + (unsigned)(wave + 4 * t) * upt, 0, 0);
+    };
+    auto dma_x = [&](int k, int c0, float* base) {
+        const int blk = wave + 4 * k;
+        if (blk >= CF::XBLK) return;
+        unsigned v = xv[k];
+        if (ragged && c0 + 8 > Cin && c0 + 4 * (int)((xq >> k) & 1) >= Cin) v = kOOB;
+        // lanes past the region are masked off, so X buffers need no padding
+        if (blk * 64 + lane < CF::XSLOTS)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + blk * 256), 16, v, c0 * 4,
+                                                     0, 0);
+    };
+    // prologue: U(0), then X(0), then X(1) -- the order the waits below assume
+#pragma unroll
+    for (int t = 0; t < 4; ++t) dma_u(t, 0, smem + CF::UOFF);
+#pragma unroll
+    for (int k = 0; k < CF::KX; ++k) dma_x(k, 0, smem);
+    const int nch = Cinp / 8;
+    if (nch > 1) {
+#pragma unroll
+        for (int k = 0; k < CF::KX; ++k) dma_x(k, 8, smem + CF::XFL);
+    }
+
+    // ---- per-lane LDS read offsets (floats, buffer 0)
+    const int sr = li / TC, stx = li % TC;
+    int xoff[2][2];                                    // [kk = stx + jj][plane]
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int kk = stx + jj;
+        const int qs = g ^ ((kk >> CF::SWZ) & 1);
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) xoff[jj][pl] = (((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
+    }
+    const int uoff = (li * 2 + (g ^ ((li >> 3) & 1))) * 4;
+
+    f16v acc[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+
+    auto run = [&](auto rowc) {
+        constexpr int ROW = decltype(rowc)::value;
+        using RW = W23Row<TC, ROW>;
+        int xb = 0;                                    // X buffer of chunk ch (ch % 3)
+        for (int ch = 0; ch < nch; ++ch) {
+            // Outstanding in issue order: ..., X(ch) [two chunks ago], U(ch), X(ch+1).
+            // Wait for all but this wave's X(ch+1) loads, then for every wave.
+            if (ch + 1 < nch) {
+                if (nxw == 2) __builtin_amdgcn_s_waitcnt(0x0F72);        // vmcnt(2)
+                else if (nxw == 1) __builtin_amdgcn_s_waitcnt(0x0F71);   // vmcnt(1)
+                else __builtin_amdgcn_s_waitcnt(0x0F70);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
+            }
+            // Workgroup barrier ordering LDS only: __syncthreads() would also wait
+            // for the X loads still in flight.  This wave's LDS reads have
+            // completed (lgkmcnt(0)); the memory clobber keeps the compiler from
+            // moving LDS accesses across it.
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            const float* X = smem + xb * CF::XFL;
+            const float* Ub = smem + CF::UOFF + (ch & 1) * CF::UFL;
+            float* nu = smem + CF::UOFF + ((ch + 1) & 1) * CF::UFL;   // U(ch+1)
+            const int xb2 = xb == 0 ? 2 : xb - 1;                     // (ch + 2) % 3
+            float* nx = smem + xb2 * CF::XFL;                          // X(ch+2)
+            const bool du = ch + 1 < nch, dx = ch + 2 < nch;
+            f4 bf[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) bf[a] = *(const f4*)&Ub[uoff + (4 * ROW + a) * 256];
+            f4 t[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int o = xoff[j >> 1][j & 1];
+                f4 dA = *(const f4*)&X[o + RW::A * 2 * TCP * 8];
+                f4 dB = *(const f4*)&X[o + RW::B * 2 * TCP * 8];
+                t[j] = RW::PLUS ? dA + dB : dA - dB;
+            }
+            f4 dh[4];
+            dh[0] = t[0] - t[2];
+            dh[1] = t[1] + t[2];
+            dh[2] = t[2] - t[1];
+            dh[3] = t[3] - t[1];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(dh[a][s2], bf[a][s2], acc[a], 0, 0, 0);
+                    const int item = a * 4 + s2;             // U(ch+1) first, then X(ch+2)
+                    if (item < 4) {
+                        if (du) dma_u(item, (ch + 1) * 8, nu);
+                    } else if (item < 4 + CF::KX) {
+                        if (dx) dma_x(item - 4, (ch + 2) * 8, nx);
+                    }
+                }
+            }
+            xb = xb == 2 ? 0 : xb + 1;
+        }
+    };
+    switch (wave) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
+    }
+
+    // ---- epilogue.  Lane l, register r <-> MFMA row (tile) 8*(r/4)+4*(l/32)+r%4,
+    // column (channel) l%32.  S layout [row 4][c 2][tile 32][SST floats].
+    __syncthreads();                     // staging buffers are free
+    {
+        float* p = smem + (wave * 2) * 32 * CF::SST + (4 * g) * CF::SST + li;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tt = 8 * (r >> 2) + (r & 3);
+            float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
+            p[tt * CF::SST] = m0 + m1 + m2;                    // S_i[0]
+            p[(32 + tt) * CF::SST] = m1 - m2 + m3;             // S_i[1]
+        }
+    }
+    __syncthreads();
+    {
+        const int tile = tid >> 3, cq = tid & 7;
+        const int c = cob + 4 * cq;
+        const int tsr = tile / TC, tsx = tile % TC;
+        const int oh0 = 2 * (ty0 + tsr), ow0 = 2 * (tx0 + tsx);
+        f4 S[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc)
+                S[i][cc] = *(const f4*)&smem[((i * 2 + cc) * 32 + tile) * CF::SST + 4 * cq];
+        f4 bq = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bq[e] = c + e < Cout ? bias[c + e] : 0.f;
+        }
+        if (c < Cout) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    const int oh = oh0 + r, ow = ow0 + cc;
+                    if (oh >= H || ow >= W) continue;
+                    f4 v = r == 0 ? S[0][cc] + S[1][cc] + S[2][cc] : S[1][cc] - S[2][cc] + S[3][cc];
+                    v = v + bq;
+                    if (act == 1) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : 0.f;
+                    }
+                    float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + c;
+                    if (c + 4 <= Cout && (Cout & 3) == 0) {
+                        *(f4*)dst = v;
+                    } else {
+                        for (int e = 0; e < 4 && c + e < Cout; ++e) dst[e] = v[e];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int TC>
+bool launch_wino23u(const float* in, const float* U, const float* bias, float* out, int N, int H,
+                    int W, int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s) {
+    using CF = W23Cfg<TC>;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_wino23u<TC>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, CF::LDS);
+    }
+    const int rblocks = (tH + CF::R - 1) / CF::R;
+    dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
+    KTimer kt("k_wino23", s);
+    hipLaunchKernelGGL(k_wino23u<TC>, grid, dim3(256), CF::LDS, s, in, U, bias, out, H, W, Cin, Cinp,
+                       Cout, rblocks, act);
+    return check_launch("k_wino23u");
+}
+
 bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
                 int Cout, float* out, int act, hipStream_t s) {
     int tH = (H + 1) / 2, tW = (W + 1) / 2;
@@ -661,6 +943,18 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     hipLaunchKernelGGL(k_wino_filter_t<2>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w, Cin,
                        Cinp, Cout, U.as<float>());
     if (!check_launch("k_wino_filter_t")) return false;
+    // 32-tile units (three workgroups per CU) when the image is wide enough to
+    // fill them; buffer resources address one image and the filter with 32-bit
+    // byte offsets.
+    if ((long long)H * W * Cin * 4 < (1ll << 31) && 16ll * Cout * Cinp * 4 < (1ll << 31) &&
+        (long long)N * ((tH + 1) / 2) < 65536) {
+        if (tW >= 12)
+            return launch_wino23u<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
+                                      act, s);
+        if (tW >= 6)
+            return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
+                                     act, s);
+    }
     // Block: TC tile columns x R tile rows of one image, R*TC <= 128 slots and
     // two LDS buffers (padded X region + 16*32*16 filter floats) within 160 KB.
     auto buf_floats = [](int R, int TC) {

@@ -79,6 +79,9 @@ CONV_CASES = [
     (1, 9, 11, 6, 3, 3, 5, 1, 0, 1, 7, GEMM_TOL),        # 3x3 pad 0 -> im2col, odd channels
     (2, 20, 18, 16, 3, 3, 24, 1, 1, 1, 6, WINO_TOL),     # F(2,3)
     (1, 7, 9, 5, 3, 3, 6, 1, 1, 1, 6, WINO_TOL),         # F(2,3), odd sizes
+    (1, 29, 30, 20, 3, 3, 40, 1, 1, 1, 6, WINO_TOL),     # F(2,3) 16-wide units, odd chunk count
+    (3, 14, 13, 64, 3, 3, 64, 1, 1, 1, 6, WINO_TOL),     # F(2,3) 8-wide units, ragged edge
+    (2, 8, 8, 24, 3, 3, 36, 1, 1, 1, 6, WINO_TOL),       # F(2,3) small image (128-slot kernel)
     (1, 112, 112, 64, 3, 3, 64, 1, 1, 1, 5, WINO_TOL),   # F(4,3)
     (1, 113, 115, 64, 3, 3, 72, 1, 1, 1, 5, WINO_TOL),   # F(4,3), ragged tiles
     (2, 10, 10, 256, 3, 3, 256, 1, 1, 2, 3, GEMM_TOL),   # grouped, Cin_per=128 > 64 -> split
