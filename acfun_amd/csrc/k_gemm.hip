@@ -314,8 +314,7 @@ template <int BM, int BN, bool CONV, bool VA, bool VB>
 bool launch_t(const GemmP& p, int batch, hipStream_t s) {
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, batch * p.splits);
     {
-        KTimer kt("k_gemm_f32", s);
-        hipLaunchKernelGGL((k_gemm_f32<BM, BN, CONV, VA, VB>), grid, dim3(256), 0, s, p);
+        ACFUN_LAUNCH("k_gemm_f32", (k_gemm_f32<BM, BN, CONV, VA, VB>), grid, dim3(256), 0, s, p);
     }
     return check_launch("k_gemm_f32");
 }
@@ -408,6 +407,8 @@ bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int 
     if (K <= 0) {  // empty reduction: C = bias / 0 (then ReLU), like the reference loops
         p.K = 0;
     }
+    if (K > 0 && gemm32_ok(M, N, K, A, lda, B, ldb))
+        return gemm32_f32(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s);
     return run<false>(p, 1, va, vb, s);
 }
 

@@ -1,0 +1,173 @@
+// k_gemm32.hip -- fp32 GEMM C[M,N] = A[M,K] * B[K,N] (+bias[n], ReLU) on
+// v_mfma_f32_32x32x2f32 with LDS-DMA staging: the engine behind acfun_gemm,
+// acfun_gemm_epi, acfun_fc and the 1x1 conv route (reference
+// src/gemm_avx512.cpp:245-337, src/layers.cpp:19-36,66-101) whenever the
+// operands are 16-byte aligned with K, N, lda, ldb multiples of 4.
+//
+// Workgroup = 64 x 64 tile of C, 4 waves in a 2 x 2 grid, each wave one
+// 32 x 32 accumulator (16 registers per lane): a single dependent MFMA chain,
+// which gfx950 issues back to back.  K is consumed in chunks of 64:
+//   A stage [64 rows][16 quads], quad q of row r at slot q ^ (r & 15);
+//   B stage [64 k][16 quads],    quad q of row k at slot q ^ ((k & 32) >> 2).
+// Both are filled by buffer_load_dwordx4 ... lds (no data VGPRs; rows and
+// columns past the matrix read zeros through the buffer range check or an
+// out-of-range offset), three stages deep, chunk c+2 issued while chunk c is
+// multiplied.  MFMA k assignment: in k-step s of a chunk, lane half h = l/32
+// carries k = 32h + s for both operands, so a lane reads its A row as eight
+// ds_read_b128 and B as one ds_read_b32 per step at an immediate offset; the
+// swizzles keep both conflict-free.  The epilogue adds bias, applies ReLU
+// (max_ps order) and stores 128 contiguous bytes per half-wave row.
+#include "rt.hpp"
+
+namespace acfun {
+namespace {
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4g __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void32;
+
+constexpr int G32_BM = 64, G32_BN = 64, G32_KC = 64;
+constexpr int G32_STAGE = 2 * 1024 * 4;           // floats per stage: A + B, 1024 quads each
+constexpr int G32_LDS = 3 * G32_STAGE * 4;        // bytes (96 KB)
+
+__global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
+                                                const float* __restrict__ B,
+                                                float* __restrict__ C,
+                                                const float* __restrict__ bias, int M, int N,
+                                                int K, int lda, int ldb, int ldc, int act) {
+    constexpr unsigned kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * G32_BM, n0 = blockIdx.x * G32_BN;
+    const int nch = (K + G32_KC - 1) / G32_KC;
+
+    // ---- DMA descriptors.  Wave w issues A blocks and B blocks w + 4t
+    // (t = 0..3); lane l of block b covers slot 64b + l = row*16 + quad slot.
+    const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + (long long)m0 * lda), (short)0,
+        (int)((long long)(M - m0) * lda * 4 < 0x7fffffff ? (long long)(M - m0) * lda * 4 : 0x7fffffff),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)B, (short)0, (int)((long long)K * ldb * 4), 0x00020000);
+    const int arow = 4 * wave + (lane >> 4);               // + 16t
+    const int aq = (lane & 15) ^ (arow & 15);              // same for every t
+    const unsigned av = (unsigned)(arow * lda + 4 * aq) * 4u;
+    const unsigned astep = 16u * lda * 4u;                 // 16 rows per t
+    const int brow = 4 * wave + (lane >> 4);               // k row within the chunk, + 16t
+    int bq[2];
+    bool bok[2];
+    unsigned bv[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {                        // t < 2: k < 32; t >= 2: k >= 32
+        bq[hh] = (lane & 15) ^ (hh << 3);
+        bok[hh] = n0 + 4 * bq[hh] < N;
+        bv[hh] = (unsigned)(brow * ldb + n0 + 4 * bq[hh]) * 4u;
+    }
+    const unsigned bstep = 16u * ldb * 4u;
+    const bool kragged = (K & (G32_KC - 1)) != 0;
+
+    // Every variable part of an address is in the per-lane offset (which the
+    // buffer range check covers); the scalar offset stays 0.
+    auto issue = [&](int t, int c, float* st) {            // item t of chunk c into stage st
+        const int k0 = c * G32_KC;
+        if (t < 4) {
+            unsigned v = av + (unsigned)k0 * 4u + (unsigned)t * astep;
+            if (kragged && k0 + 4 * aq >= K) v = kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wave + 4 * t) * 256),
+                                                     16, v, 0, 0, 0);
+        } else {
+            const int tt = t - 4, hh = tt >> 1;
+            unsigned v = bok[hh] ? bv[hh] + (unsigned)k0 * ldb * 4u + (unsigned)tt * bstep : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                bres, (lds_void32*)(st + 4096 + (wave + 4 * tt) * 256), 16, v, 0, 0, 0);
+        }
+    };
+
+    // ---- per-lane read offsets within a stage (floats)
+    const int r = lane & 31, h = lane >> 5;
+    const int rowA = 32 * wm + r;
+    int aoff[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) aoff[j] = (rowA * 16 + ((8 * h + j) ^ (rowA & 15))) * 4;
+    const int col = 32 * wn + r;
+    const int boff = 4096 + ((32 * h) * 16 + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
+
+    f16v acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+#pragma unroll
+    for (int t = 0; t < 8; ++t) issue(t, 0, sm);
+    if (nch > 1) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) issue(t, 1, sm + G32_STAGE);
+    }
+    int st = 0;
+    for (int c = 0; c < nch; ++c) {
+        // outstanding in issue order: ..., chunk c, chunk c+1 (8 items each)
+        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt(0x0F78);    // vmcnt(8)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
+        // LDS-only workgroup barrier: this wave's LDS reads are complete;
+        // the loads of chunk c+1 stay in flight.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float* S = sm + st * G32_STAGE;
+        const int st2 = st == 0 ? 2 : st - 1;                    // (c + 2) % 3
+        float* N2 = sm + st2 * G32_STAGE;
+        const bool more = c + 2 < nch;
+        f4g a[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = *(const f4g*)&S[aoff[j]];
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            const float b = S[boff + s * 64];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b, acc, 0, 0, 0);
+            if ((s & 3) == 3 && more) issue(s >> 2, c + 2, N2);
+        }
+        st = st == 2 ? 0 : st + 1;
+    }
+
+    // ---- epilogue: lane l, register e <-> row 8*(e/4) + 4*(l/32) + e%4, column l%32
+    const int n = n0 + col;
+    if (n < N) {
+        const float bn = bias ? bias[n] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < M) {
+                float v = acc[e];
+                if (bias) v = v + bn;
+                if (act == 1) v = v > 0.f ? v : 0.f;
+                C[(long long)m * ldc + n] = v;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+                int ldc, const float* bias, int act, hipStream_t s) {
+    if (M <= 0 || N <= 0) return true;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_gemm32, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  G32_LDS);
+    }
+    dim3 grid((unsigned)((N + G32_BN - 1) / G32_BN), (unsigned)((M + G32_BM - 1) / G32_BM));
+    ACFUN_LAUNCH("k_gemm_f32", k_gemm32, grid, dim3(256), G32_LDS, s, A, B, C, bias, M, N, K, lda, ldb, ldc,
+                       act);
+    return check_launch("k_gemm32");
+}
+
+bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int ldb) {
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    return K > 0 && K % 4 == 0 && N % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && al(A) && al(B) &&
+           (long long)K * ldb * 4 < 0x7fffffffll && (long long)(M + 64) * lda * 4 < (1ll << 40) &&
+           (long long)lda * 16 * 4 < 0x7fffffffll && (N + 63) / 64 < 65536 * 32 &&
+           (M + 63) / 64 < 65536;
+}
+
+}  // namespace acfun

@@ -411,11 +411,10 @@ void pick_tile(int M, int N, int* bm, int* bn) {
 template <bool CONV, bool VA>
 bool launch_i8_v(const I8P& p, int bm, int bn, hipStream_t s) {
     dim3 grid((p.N + bn - 1) / bn, (p.M + bm - 1) / bm);
-    KTimer kt("k_igemm_i8", s);
-    if (bm == 128 && bn == 128) hipLaunchKernelGGL((k_igemm_i8<128, 128, CONV, VA>), grid, dim3(256), 0, s, p);
-    else if (bm == 128) hipLaunchKernelGGL((k_igemm_i8<128, 64, CONV, VA>), grid, dim3(256), 0, s, p);
-    else if (bn == 128) hipLaunchKernelGGL((k_igemm_i8<64, 128, CONV, VA>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((k_igemm_i8<64, 64, CONV, VA>), grid, dim3(256), 0, s, p);
+    if (bm == 128 && bn == 128) ACFUN_LAUNCH("k_igemm_i8", (k_igemm_i8<128, 128, CONV, VA>), grid, dim3(256), 0, s, p);
+    else if (bm == 128) ACFUN_LAUNCH("k_igemm_i8", (k_igemm_i8<128, 64, CONV, VA>), grid, dim3(256), 0, s, p);
+    else if (bn == 128) ACFUN_LAUNCH("k_igemm_i8", (k_igemm_i8<64, 128, CONV, VA>), grid, dim3(256), 0, s, p);
+    else ACFUN_LAUNCH("k_igemm_i8", (k_igemm_i8<64, 64, CONV, VA>), grid, dim3(256), 0, s, p);
     return check_launch("k_igemm_i8");
 }
 

@@ -427,27 +427,24 @@ bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, con
     if (KH == 3 && KW == 3 && C % 4 == 0 && al && w_al && (stride == 1 || stride == 2) &&
         nblk < (1ll << 31) && (long long)N * H * W * C < (1ll << 31)) {
         const int nOHB = (OH + 1) / 2, nOWB = (OW + 3) / 4, total = (int)nblk;
-        KTimer kt("k_dwconv", s);
         if (stride == 1)
-            hipLaunchKernelGGL(k_dwconv3_blk<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+            ACFUN_LAUNCH("k_dwconv", k_dwconv3_blk<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                                s, (const float4*)in, H, W, C4, w, bias, pad, OH, OW, nOHB, nOWB,
                                total, (float4*)out, act);
         else
-            hipLaunchKernelGGL(k_dwconv3_blk<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+            ACFUN_LAUNCH("k_dwconv", k_dwconv3_blk<2>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                                s, (const float4*)in, H, W, C4, w, bias, pad, OH, OW, nOHB, nOWB,
                                total, (float4*)out, act);
         return check_launch("k_dwconv3_blk");
     }
     if (KH == 3 && KW == 3 && C % 4 == 0 && al) {
         long long total = (long long)N * OH * OW * (C / 4);
-        KTimer kt("k_dwconv", s);
-        hipLaunchKernelGGL(k_dwconv3_c4, grid1d(total), dim3(256), 0, s, (const float4*)in, N, H,
+        ACFUN_LAUNCH("k_dwconv", k_dwconv3_c4, grid1d(total), dim3(256), 0, s, (const float4*)in, N, H,
                            W, C / 4, w, bias, stride, pad, OH, OW, (float4*)out, act);
         return check_launch("k_dwconv3_c4");
     }
     long long total = (long long)N * OH * OW * C;
-    KTimer kt("k_dwconv", s);
-    hipLaunchKernelGGL(k_dwconv, grid1d(total), dim3(256), 0, s, in, N, H, W, C, w, bias, KH, KW,
+    ACFUN_LAUNCH("k_dwconv", k_dwconv, grid1d(total), dim3(256), 0, s, in, N, H, W, C, w, bias, KH, KW,
                        stride, pad, OH, OW, out, act);
     return check_launch("k_dwconv");
 }
@@ -465,8 +462,7 @@ bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, co
     int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
     int fma_all = Cout_p >= 8 ? 1 : 0;
     long long total = (long long)N * OH * OW * Cout;
-    KTimer kt("k_gconv", s);
-    hipLaunchKernelGGL(k_gconv, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH, KW,
+    ACFUN_LAUNCH("k_gconv", k_gconv, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH, KW,
                        Cout, stride, pad, groups, OH, OW, out, act, vec_end, fma_all);
     return check_launch("k_gconv");
 }
@@ -482,15 +478,13 @@ bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stri
         (((uintptr_t)in | (uintptr_t)out) & 15u) == 0 && nq < (1ll << 31) &&
         (long long)N * H * W * C < (1ll << 31)) {
         const int total = (int)nq;
-        KTimer kt("k_maxpool", s);
-        hipLaunchKernelGGL(k_maxpool3s2_row, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+        ACFUN_LAUNCH("k_maxpool", k_maxpool3s2_row, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                            (const float4*)in, H, W, C / 4, pad, OH, OW, (OW + 3) / 4, total,
                            (float4*)out, post_relu);
         return check_launch("k_maxpool3s2_row");
     }
     long long total = (long long)N * OH * OW * C;
-    KTimer kt("k_maxpool", s);
-    hipLaunchKernelGGL(k_maxpool, grid1d(total), dim3(256), 0, s, in, N, H, W, C, pool, stride,
+    ACFUN_LAUNCH("k_maxpool", k_maxpool, grid1d(total), dim3(256), 0, s, in, N, H, W, C, pool, stride,
                        pad, OH, OW, out, post_relu, vec_end);
     return check_launch("k_maxpool");
 }

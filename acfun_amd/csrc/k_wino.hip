@@ -187,6 +187,46 @@ __global__ void k_wino_filter_t(const float* __restrict__ w, int Cin, int Cinp, 
         for (int j = 0; j < A; ++j) U[(i * A + j) * plane + idx] = gh[i][j];
 }
 
+// Filter transform as a tiled transpose: a 256-lane block owns 16 output x 16
+// input channels.  Lane (o = l%16, c = l/16) reads its 9 taps with output
+// channels fastest (64-byte runs of w), transforms them, and the block writes
+// U[a][Cout][Cinp] through LDS with input channels fastest (64-byte runs).
+template <int TILE>
+__global__ __launch_bounds__(256) void k_wino_filter_tt(const float* __restrict__ w, int Cin,
+                                                         int Cinp, int Cout, float* __restrict__ U) {
+    constexpr int A = Wino<TILE>::A, AA = A * A;
+    __shared__ float tr[AA][16][17];
+    const int o0 = blockIdx.x * 16, c0 = blockIdx.y * 16;
+    const int ol = threadIdx.x & 15, cl = threadIdx.x >> 4;
+    const int o = o0 + ol, c = c0 + cl;
+    float gh[A][A];
+    if (c < Cin && o < Cout) {
+        float g[3][3];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) g[kh][kw] = w[((long long)(kh * 3 + kw) * Cin + c) * Cout + o];
+        Wino<TILE>::f_tf(g, gh);
+    } else {
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) gh[i][j] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < A; ++i)
+#pragma unroll
+        for (int j = 0; j < A; ++j) tr[i * A + j][ol][cl] = gh[i][j];
+    __syncthreads();
+    // write: lane (c = l%16, o = l/16), c fastest
+    const int wc = threadIdx.x & 15, wo = threadIdx.x >> 4;
+    const long long plane = (long long)Cout * Cinp;
+    if (o0 + wo < Cout && c0 + wc < Cinp) {
+#pragma unroll
+        for (int a = 0; a < AA; ++a) U[a * plane + (long long)(o0 + wo) * Cinp + c0 + wc] = tr[a][wo][wc];
+    }
+}
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Fused Winograd: one workgroup = TB consecutive tiles (flattened n,ty,tx
@@ -923,8 +963,7 @@ bool launch_wino23u(const float* in, const float* U, const float* bias, float* o
     }
     const int rblocks = (tH + CF::R - 1) / CF::R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
-    KTimer kt("k_wino23", s);
-    hipLaunchKernelGGL(k_wino23u<TC>, grid, dim3(256), CF::LDS, s, in, U, bias, out, H, W, Cin, Cinp,
+    ACFUN_LAUNCH("k_wino23", k_wino23u<TC>, grid, dim3(256), CF::LDS, s, in, U, bias, out, H, W, Cin, Cinp,
                        Cout, rblocks, act);
     return check_launch("k_wino23u");
 }
@@ -940,8 +979,8 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     }
     Scratch U((size_t)16 * Cout * Cinp * sizeof(float), s);
     if (!U.p) return false;
-    hipLaunchKernelGGL(k_wino_filter_t<2>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w, Cin,
-                       Cinp, Cout, U.as<float>());
+    ACFUN_LAUNCH("k_wino_filter_t", k_wino_filter_tt<2>, dim3((Cout + 15) / 16, Cinp / 16),
+                 dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
     if (!check_launch("k_wino_filter_t")) return false;
     // 32-tile units (three workgroups per CU) when the image is wide enough to
     // fill them; buffer resources address one image and the filter with 32-bit
@@ -982,8 +1021,7 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     }
     int rblocks = (tH + R - 1) / R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
-    KTimer kt("k_wino23", s);
-    hipLaunchKernelGGL(k_wino23, grid, dim3(512), lds, s, in, U.as<float>(), bias, out, N, H, W,
+    ACFUN_LAUNCH("k_wino23", k_wino23, grid, dim3(512), lds, s, in, U.as<float>(), bias, out, N, H, W,
                        Cin, Cinp, Cout, tH, tW, R, TC, act);
     return check_launch("k_wino23");
 }
@@ -998,12 +1036,11 @@ bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, co
     int Cinp = (Cin + KC - 1) / KC * KC;
     Scratch U((size_t)P * Cout * Cinp * sizeof(float), s);
     if (!U.p) return false;
-    hipLaunchKernelGGL(k_wino_filter_t<TILE>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w,
+    ACFUN_LAUNCH("k_wino_filter_t", k_wino_filter_t<TILE>, dim3((Cinp * Cout + 255) / 256), dim3(256), 0, s, w,
                        Cin, Cinp, Cout, U.as<float>());
     if (!check_launch("k_wino_filter_t")) return false;
     dim3 grid((unsigned)((T + TB - 1) / TB), (Cout + 16 * NW - 1) / (16 * NW));
-    KTimer kt("k_wino_fused", s);
-    hipLaunchKernelGGL((k_wino_fused<TILE, TB, NW, KC>), grid, dim3(64 * NW), 0, s, in, U.as<float>(),
+    ACFUN_LAUNCH("k_wino_fused", (k_wino_fused<TILE, TB, NW, KC>), grid, dim3(64 * NW), 0, s, in, U.as<float>(),
                        bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act);
     return check_launch("k_wino_fused");
 }

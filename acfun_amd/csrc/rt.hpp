@@ -3,6 +3,7 @@
 // memory pool, host<->device staging for the synchronous reference API, and
 // the launchers each kernel file exports.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -20,17 +21,21 @@ bool check(hipError_t e, const char* what);
 bool check_launch(const char* kernel);
 
 // ----------------------------------------------------------------- timing
-// Kernel timing for measurement: while enabled (acfun_prof_enable), KTimer
-// records a HIP event pair around one launch on its stream; the pairs are
-// summed per kernel name by acfun_prof_kernel_ms.  Disabled: no events.
-void prof_begin(const char* kernel, hipStream_t s);
-void prof_end(const char* kernel, hipStream_t s);
-struct KTimer {
-    const char* k;
-    hipStream_t s;
-    KTimer(const char* kernel, hipStream_t st) : k(kernel), s(st) { prof_begin(k, s); }
-    ~KTimer() { prof_end(k, s); }
-};
+// Kernel timing for measurement.  While enabled (acfun_prof_enable),
+// ACFUN_LAUNCH starts a kernel with hipExtLaunchKernelGGL, whose start/stop
+// events the dispatch itself signals; acfun_prof_kernel_ms averages, per name,
+// the time from the later of its start and the previous timed kernel's stop
+// on the same stream to its stop.  Disabled: a plain launch.
+bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_t* stop);
+#define ACFUN_LAUNCH(NAME, KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                               \
+    do {                                                                                        \
+        hipEvent_t acfun_ev0_, acfun_ev1_;                                                      \
+        if (::acfun::prof_events(NAME, STREAM, &acfun_ev0_, &acfun_ev1_))                       \
+            hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, acfun_ev0_, acfun_ev1_, 0,  \
+                                  __VA_ARGS__);                                                 \
+        else                                                                                    \
+            hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                \
+    } while (0)
 
 // ----------------------------------------------------------------- device
 // Initializes the current device once (verifies it is gfx950, creates the
@@ -103,6 +108,11 @@ class HostCall {
 struct ConvShape {
     int N, H, W, Cin, KH, KW, stride, pad, OH, OW;
 };
+// 64x64-tile 32x32x2-MFMA GEMM with LDS-DMA staging (k_gemm32.hip); gemm32_ok
+// says whether its alignment and size conditions hold.
+bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int ldb);
+bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+                int ldc, const float* bias, int act, hipStream_t s);
 bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
               int ldc, const float* bias, int act, hipStream_t s);
 bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const float* bias,

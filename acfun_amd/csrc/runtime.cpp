@@ -33,37 +33,37 @@ bool check_launch(const char* kernel) { return check(hipGetLastError(), kernel);
 
 // ------------------------------------------------------------------ timing
 namespace {
-struct ProfKernel {
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;   // created on demand, reused
-    size_t used = 0;
-    bool open = false;
+struct ProfLaunch {
+    hipEvent_t start, stop;
+    hipEvent_t prev;     // stop event of the previous timed launch on the stream (or null)
 };
+struct ProfKernel {
+    std::vector<ProfLaunch> ev;                           // events created on demand, reused
+    size_t used = 0;
+};
+std::map<hipStream_t, hipEvent_t> g_prof_last;            // last timed stop event per stream
 bool g_prof_on = false;
 std::map<std::string, ProfKernel> g_prof;
 std::mutex g_prof_mu;
 }  // namespace
 
-void prof_begin(const char* kernel, hipStream_t s) {
-    if (!g_prof_on) return;
+bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_t* stop) {
+    if (!g_prof_on) return false;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     ProfKernel& k = g_prof[kernel];
     if (k.used == k.ev.size()) {
         hipEvent_t a, b;
-        if (hipEventCreate(&a) != hipSuccess) return;
-        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return; }
-        k.ev.emplace_back(a, b);
+        if (hipEventCreate(&a) != hipSuccess) return false;
+        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return false; }
+        k.ev.push_back(ProfLaunch{a, b, nullptr});
     }
-    if (hipEventRecord(k.ev[k.used].first, s) == hipSuccess) k.open = true;
-}
-
-void prof_end(const char* kernel, hipStream_t s) {
-    if (!g_prof_on) return;
-    std::lock_guard<std::mutex> lk(g_prof_mu);
-    auto it = g_prof.find(kernel);
-    if (it == g_prof.end() || !it->second.open) return;
-    ProfKernel& k = it->second;
-    k.open = false;
-    if (hipEventRecord(k.ev[k.used].second, s) == hipSuccess) ++k.used;
+    ProfLaunch& L = k.ev[k.used++];
+    auto it = g_prof_last.find(s);
+    L.prev = it == g_prof_last.end() ? nullptr : it->second;
+    g_prof_last[s] = L.stop;
+    *start = L.start;
+    *stop = L.stop;
+    return true;
 }
 
 // ------------------------------------------------------------------ device
@@ -259,10 +259,8 @@ bool HostCall::finish() {
 extern "C" void acfun_prof_enable(int on) {
     std::lock_guard<std::mutex> lk(acfun::g_prof_mu);
     if (on) {                            // a new measurement starts empty; off keeps the records
-        for (auto& kv : acfun::g_prof) {
-            kv.second.used = 0;
-            kv.second.open = false;
-        }
+        for (auto& kv : acfun::g_prof) kv.second.used = 0;
+        acfun::g_prof_last.clear();
     }
     acfun::g_prof_on = on != 0;
 }
@@ -276,10 +274,16 @@ extern "C" double acfun_prof_kernel_ms(const char* kernel, int* launches) {
     double total = 0.0;
     for (size_t i = 0; i < it->second.used; ++i) {
         auto& e = it->second.ev[i];
-        if (!acfun::check(hipEventSynchronize(e.second), "acfun_prof_kernel_ms")) return -1.0;
+        if (!acfun::check(hipEventSynchronize(e.stop), "acfun_prof_kernel_ms")) return -1.0;
         float ms = 0.f;
-        if (!acfun::check(hipEventElapsedTime(&ms, e.first, e.second), "acfun_prof_kernel_ms"))
+        if (!acfun::check(hipEventElapsedTime(&ms, e.start, e.stop), "acfun_prof_kernel_ms"))
             return -1.0;
+        // A dispatch's start event can be signalled while it still waits for the
+        // previous kernel on its stream: count from that kernel's end then.
+        float since_prev = 0.f;
+        if (e.prev && hipEventElapsedTime(&since_prev, e.prev, e.stop) == hipSuccess &&
+            since_prev > 0.f && since_prev < ms)
+            ms = since_prev;
         total += ms;
     }
     if (launches) *launches = (int)it->second.used;

@@ -204,12 +204,12 @@ int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float*
                                 void* stream);
 
 /* Kernel timing for measurement.  acfun_prof_enable(1) clears the records and
- * starts bracketing each launch of the library's main kernels (k_wino23,
- * k_wino_fused, k_gemm_f32, k_igemm_i8, k_dwconv, k_gconv, k_maxpool) with a
- * HIP event pair on the launch's stream; acfun_prof_enable(0) stops.
+ * starts launching the library's main kernels (k_wino23, k_wino_fused,
+ * k_gemm_f32, k_igemm_i8, k_dwconv, k_gconv, k_maxpool) with HIP start/stop
+ * events that the dispatch itself signals; acfun_prof_enable(0) stops.
  * acfun_prof_kernel_ms() waits for the recorded events and returns the mean
- * duration in ms of the named kernel (0 if none, -1 on a HIP error) and the
- * launch count in *launches (may be NULL). */
+ * execution time in ms of the named kernel (0 if none, -1 on a HIP error) and
+ * the launch count in *launches (may be NULL). */
 void acfun_prof_enable(int on);
 double acfun_prof_kernel_ms(const char* kernel, int* launches);
 
