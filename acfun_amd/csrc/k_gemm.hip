@@ -40,7 +40,6 @@ struct GemmP {
     int H, W, Cin, KW, stride, pad, OH, OW;
 };
 
-__device__ __forceinline__ float relu_max(float v) { return v > 0.0f ? v : 0.0f; }
 
 // Decodes a k index into (kh, kw, ic).
 struct Tap {
@@ -274,7 +273,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(GemmP p) {
                     float v = acc[i][j][r];
                     if (final_out) {
                         v = v + bv;
-                        if (p.act) v = relu_max(v);
+                        v = act_apply(v, p.act);
                     }
                     Cb[(long long)m * p.ldc + n] = v;
                 }
@@ -294,7 +293,7 @@ __global__ void k_splitk_reduce(const float* __restrict__ ws, int splits, long l
     float v = ws[i];
     for (int s = 1; s < splits; ++s) v += ws[(long long)s * plane + i];
     if (bias) v = v + bias[n];
-    if (act) v = relu_max(v);
+    v = act_apply(v, act);
     C[(long long)m * ldc + n] = v;
 }
 

@@ -11,12 +11,15 @@
 //   B stage [64 k][16 quads],    quad q of row k at slot q ^ ((k & 32) >> 2).
 // Both are filled by buffer_load_dwordx4 ... lds (no data VGPRs; rows and
 // columns past the matrix read zeros through the buffer range check or an
-// out-of-range offset), three stages deep, chunk c+2 issued while chunk c is
-// multiplied.  MFMA k assignment: in k-step s of a chunk, lane half h = l/32
+// out-of-range offset), three stages deep with chunk c+2 issued while chunk
+// c is multiplied when the grid is one wave of workgroups, else two stages
+// (two workgroups per CU) with chunk c+1 in flight.  MFMA k assignment: in k-step s of a chunk, lane half h = l/32
 // carries k = 32h + s for both operands, so a lane reads its A row as eight
 // ds_read_b128 and B as one ds_read_b32 per step at an immediate offset; the
-// swizzles keep both conflict-free.  The epilogue adds bias, applies ReLU
-// (max_ps order) and stores 128 contiguous bytes per half-wave row.
+// swizzles keep both conflict-free.  The epilogue adds bias, optionally a
+// residual tensor (a model's Add fused into the conv before it: the same two
+// roundings as a separate Add), applies ReLU (max_ps order) and stores 128
+// contiguous bytes per half-wave row.
 #include "rt.hpp"
 
 namespace acfun {
@@ -28,13 +31,15 @@ typedef __attribute__((address_space(3))) void lds_void32;
 
 constexpr int G32_BM = 64, G32_BN = 64, G32_KC = 64;
 constexpr int G32_STAGE = 2 * 1024 * 4;           // floats per stage: A + B, 1024 quads each
-constexpr int G32_LDS = 3 * G32_STAGE * 4;        // bytes (96 KB)
 
+template <int NST>
 __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 float* __restrict__ C,
-                                                const float* __restrict__ bias, int M, int N,
-                                                int K, int lda, int ldb, int ldc, int act) {
+                                                const float* __restrict__ bias,
+                                                const float* __restrict__ res, int M, int N,
+                                                int K, int lda, int ldb, int ldc, int ldr,
+                                                int act) {
     constexpr unsigned kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -98,24 +103,39 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 
+    // Bias and residual of this lane's 16 outputs, loaded first (loads complete
+    // in issue order) so their latency hides behind chunk 0's.
+    const int n = n0 + col;
+    float bn = 0.f, rv[16];
+    if (n < N && bias) bn = bias[n];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+        rv[e] = (res && n < N && m < M) ? res[(long long)m * ldr + n] : 0.f;
+    }
+
+    // NST = 3: chunk c+2 is issued while chunk c is multiplied; NST = 2 (two
+    // workgroups per CU): chunk c+1.  NST stages hold min(NST, nch) chunks.
+    constexpr int AHEAD = NST - 1;
 #pragma unroll
     for (int t = 0; t < 8; ++t) issue(t, 0, sm);
-    if (nch > 1) {
+    if (AHEAD == 2 && nch > 1) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) issue(t, 1, sm + G32_STAGE);
     }
+
     int st = 0;
     for (int c = 0; c < nch; ++c) {
-        // outstanding in issue order: ..., chunk c, chunk c+1 (8 items each)
-        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt(0x0F78);    // vmcnt(8)
-        else __builtin_amdgcn_s_waitcnt(0x0F70);                // vmcnt(0)
+        // outstanding in issue order: ..., chunk c, [chunk c+1] (8 items each)
+        if (AHEAD == 2 && c + 1 < nch) __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
         // LDS-only workgroup barrier: this wave's LDS reads are complete;
-        // the loads of chunk c+1 stay in flight.
+        // the loads of later chunks stay in flight.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const float* S = sm + st * G32_STAGE;
-        const int st2 = st == 0 ? 2 : st - 1;                    // (c + 2) % 3
-        float* N2 = sm + st2 * G32_STAGE;
-        const bool more = c + 2 < nch;
+        const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
+        float* NA = sm + sta * G32_STAGE;
+        const bool more = c + AHEAD < nch;
         f4g a[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) a[j] = *(const f4g*)&S[aoff[j]];
@@ -123,22 +143,21 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
         for (int s = 0; s < 32; ++s) {
             const float b = S[boff + s * 64];
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b, acc, 0, 0, 0);
-            if ((s & 3) == 3 && more) issue(s >> 2, c + 2, N2);
+            if ((s & 3) == 3 && more) issue(s >> 2, c + AHEAD, NA);
         }
-        st = st == 2 ? 0 : st + 1;
+        st = AHEAD == 2 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
     }
 
     // ---- epilogue: lane l, register e <-> row 8*(e/4) + 4*(l/32) + e%4, column l%32
-    const int n = n0 + col;
     if (n < N) {
-        const float bn = bias ? bias[n] : 0.f;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
             if (m < M) {
                 float v = acc[e];
                 if (bias) v = v + bn;
-                if (act == 1) v = v > 0.f ? v : 0.f;
+                if (res) v = v + rv[e];                   // fused residual Add
+                v = act_apply(v, act);
                 C[(long long)m * ldc + n] = v;
             }
         }
@@ -148,17 +167,31 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 }  // namespace
 
 bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
-                int ldc, const float* bias, int act, hipStream_t s) {
+                int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr) {
     if (M <= 0 || N <= 0) return true;
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm32, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  G32_LDS);
+        (void)hipFuncSetAttribute((const void*)k_gemm32<3>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 3 * G32_STAGE * 4);
+        (void)hipFuncSetAttribute((const void*)k_gemm32<2>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G32_STAGE * 4);
     }
     dim3 grid((unsigned)((N + G32_BN - 1) / G32_BN), (unsigned)((M + G32_BM - 1) / G32_BM));
-    ACFUN_LAUNCH("k_gemm_f32", k_gemm32, grid, dim3(256), G32_LDS, s, A, B, C, bias, M, N, K, lda, ldb, ldc,
-                       act);
+    const int nch = (K + G32_KC - 1) / G32_KC;
+    const long long tiles = (long long)grid.x * grid.y;
+    // Three stages (one workgroup per CU) only pay when the grid is a single
+    // wave of workgroups; otherwise two stages let two workgroups share a CU.
+    // LDS holds only the stages that can be in use.
+    const bool deep = nch > 2 && tiles < 2ll * num_cus();
+    const int stages = deep ? 3 : (nch < 2 ? 1 : 2);
+    const size_t lds = (size_t)stages * G32_STAGE * 4;
+    if (deep)
+        ACFUN_LAUNCH("k_gemm_f32", k_gemm32<3>, grid, dim3(256), lds, s, A, B, C, bias, res, M, N, K,
+                     lda, ldb, ldc, ldr, act);
+    else
+        ACFUN_LAUNCH("k_gemm_f32", k_gemm32<2>, grid, dim3(256), lds, s, A, B, C, bias, res, M, N, K,
+                     lda, ldb, ldc, ldr, act);
     return check_launch("k_gemm32");
 }
 

@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void k_igemm_i8(I8P p) {
                     else {
                         int u = (int)((unsigned)a + (unsigned)corr);
                         v = __fadd_rn(__fmul_rn((float)u, al), be);
-                        if (p.act) v = vmax(v, 0.0f);
+                        v = act_apply(v, p.act);
                     }
                     p.Cf[o] = v;
                 } else {
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(256) void k_igemm_i8(I8P p) {
                     if (zero) v = 0.0f;
                     else {
                         v = fmaf((float)(4LL * (long long)a), al, be);
-                        if (p.act == 1) v = vmax(v, 0.0f);
+                        v = act_apply(v, p.act);
                     }
                     p.Cf[o] = v;
                 }

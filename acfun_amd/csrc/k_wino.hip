@@ -394,7 +394,7 @@ __global__ __launch_bounds__(64 * NW) void k_wino_fused(
                     int oh = ty * TILE + i, ow = tx * TILE + j;
                     if (oh < H && ow < W) {
                         float v = y[i][j] + bv;
-                        if (act == 1) v = v > 0.f ? v : 0.f;
+                        v = act_apply(v, act);
                         out[(((long long)n * H + oh) * W + ow) * Cout + co] = v;
                     }
                 }
@@ -676,10 +676,8 @@ __global__ __launch_bounds__(512) void k_wino23(
         if (oh >= H || ow >= W || c >= Cout) continue;
         int so = ((py >> 1) * TC + (pxx >> 1)) * SS + (2 * (py & 1) + (pxx & 1)) * 32 + 4 * qd;
         f4 v = *(const f4*)&smem[so] + *(const f4*)&smem[TILE + so] + bq;
-        if (act == 1) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) v[t] = v[t] > 0.f ? v[t] : 0.f;
-        }
+        for (int t = 0; t < 4; ++t) v[t] = act_apply(v[t], act);
         float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + c;
         if (c + 4 <= Cout && (Cout & 3) == 0) {
             *(f4*)dst = v;
@@ -935,10 +933,8 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
                     if (oh >= H || ow >= W) continue;
                     f4 v = r == 0 ? S[0][cc] + S[1][cc] + S[2][cc] : S[1][cc] - S[2][cc] + S[3][cc];
                     v = v + bq;
-                    if (act == 1) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.f ? v[e] : 0.f;
-                    }
+                    for (int e = 0; e < 4; ++e) v[e] = act_apply(v[e], act);
                     float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + c;
                     if (c + 4 <= Cout && (Cout & 3) == 0) {
                         *(f4*)dst = v;

@@ -365,6 +365,37 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         cur = o;
     }
     if (L) last_use[L - 1] = L;  // the result stays until copied out
+    // Execution plan: the same arithmetic in fewer passes.
+    //  * A ReLU layer that alone consumes a dense conv's output runs in the
+    //    conv's epilogue with the layer's own rule (act 2: v < 0 -> 0).
+    //  * An Add that alone consumes the output of a 1x1/s1/p0 fp32 conv runs in
+    //    the GEMM epilogue: v = (acc + bias) + residual, then its ReLU -- the
+    //    same roundings as the separate Add.
+    //  * An Input layer aliases the tensor it names (no copy).
+    // A fused or aliasing layer owns no buffer; its tensor is alias[i] (-1 =
+    // the model input), kept alive as long as the alias is used.
+    std::vector<int> alias(L, -2), act_of(L, -1), res_of(L, -3);
+    for (int i = 0; i + 1 < L; ++i) {
+        const Layer& F = m->layers[i];
+        const Layer& G = m->layers[i + 1];
+        if (F.type != 1 || F.act != 0 || last_use[i] != i + 1) continue;
+        if (G.type == 3) {
+            act_of[i] = 2;                           // the separate layer's ReLU rule
+            alias[i + 1] = i;
+            ++i;
+        } else if (G.type == 8 && F.type == 1 && !(m->int8 && F.wq) && F.p[0] == 1 && F.p[1] == 1 &&
+                   F.p[3] == 1 && F.p[4] == 0 && G.from != i && out[i].C % 4 == 0 && i > 0 &&
+                   m->layers[i - 1].type != 10 && (out[i - 1].C % 4) == 0) {
+            res_of[i] = G.from;
+            act_of[i] = G.p[1] ? 2 : 0;              // k_add_relu's rule: v < 0 -> 0
+            alias[i + 1] = i;
+            ++i;
+        }
+    }
+    for (int i = 0; i < L; ++i)
+        if (m->layers[i].type == 10) alias[i] = m->layers[i].from;
+    for (int i = L - 1; i >= 0; --i)
+        if (alias[i] >= 0) last_use[alias[i]] = std::max(last_use[alias[i]], last_use[i]);
     // Execute.
     std::vector<float*> buf(L, nullptr);
     std::vector<Scratch> hold(L);
@@ -378,9 +409,18 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         if (F.type == 10) { x = tensor_of(F.from); xi = F.from; in = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from]; }
         Dims o = out[i];
         size_t cap = (size_t)N * o.H * o.W * o.C;
+        if (alias[i] != -2) {                        // fused into the previous layer, or an Input
+            buf[i] = const_cast<float*>(tensor_of(alias[i]));
+            for (int j = 0; j < i; ++j)
+                if (buf[j] && last_use[j] == i && hold[j].p) { hold[j] = Scratch(); buf[j] = nullptr; }
+            cur = o;
+            x = buf[i];
+            xi = i;
+            continue;
+        }
         bool inplace = (F.type == 3 || F.type == 5 || F.type == 6 || F.type == 10);
         float* y;
-        if (inplace && F.type != 10 && xi >= 0 && last_use[xi] == i) {
+        if (inplace && F.type != 10 && xi >= 0 && last_use[xi] == i && hold[xi].p) {
             // take over the input buffer
             y = buf[xi];
             hold[i] = std::move(hold[xi]);
@@ -398,12 +438,21 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         switch (F.type) {
             case 1: case 7: {
                 int groups = F.type == 7 ? F.p[5] : 1;
-                if (m->int8 && F.type == 1 && F.wq) {
+                const int act = act_of[i] >= 0 ? act_of[i] : F.act;
+                const long long M = (long long)N * in.H * in.W;
+                if (res_of[i] != -3 && M < (1ll << 31) &&
+                    gemm32_ok((int)M, o.C, in.C, x, in.C, F.w, o.C)) {
+                    ok = gemm32_f32((int)M, o.C, in.C, x, in.C, F.w, o.C, y, o.C, F.b, act, s,
+                                    tensor_of(res_of[i]), o.C);
+                } else if (res_of[i] != -3) {
+                    set_error("model: residual fusion precondition failed at layer %d", i);
+                    return 0;
+                } else if (m->int8 && F.type == 1 && F.wq) {
                     ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
-                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, F.act, s, &F.i8);
+                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8);
                 } else {
                     ok = conv2d_route_f32(x, N, in.H, in.W, in.C, F.w, F.b, F.p[0], F.p[1], o.C,
-                                          F.p[3], F.p[4], groups > 1 ? groups : 1, y, F.act, s);
+                                          F.p[3], F.p[4], groups > 1 ? groups : 1, y, act, s);
                 }
                 break;
             }
@@ -436,7 +485,10 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         if (!ok) return 0;
         // release inputs whose last consumer was this layer
         for (int j = 0; j < i; ++j)
-            if (buf[j] && last_use[j] == i) { hold[j] = Scratch(); buf[j] = nullptr; }
+            if (buf[j] && last_use[j] == i) {
+                hold[j] = Scratch();
+                buf[j] = nullptr;
+            }
         cur = o;
         x = y;
         xi = i;

@@ -37,6 +37,16 @@ bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_
             hipLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, __VA_ARGS__);                \
     } while (0)
 
+// ----------------------------------------------------------------- activation
+// Epilogue activation codes: 0 none; 1 ReLU as the reference's fused epilogues
+// compute it (max_ps: v > 0 ? v : 0, so NaN and -0.0 become +0); 2 ReLU as a
+// separate layer computes it (acfun_relu, src/layers.cpp:10-12: v < 0 -> 0,
+// keeping NaN and -0.0), used when the model executor fuses a ReLU layer or a
+// residual Add's ReLU into the conv before it.
+__device__ __forceinline__ float act_apply(float v, int act) {
+    return act == 1 ? (v > 0.f ? v : 0.f) : (act == 2 ? (v < 0.f ? 0.f : v) : v);
+}
+
 // ----------------------------------------------------------------- device
 // Initializes the current device once (verifies it is gfx950, creates the
 // library stream).  Returns false (and sets the error) when no usable GPU.
@@ -112,7 +122,8 @@ struct ConvShape {
 // says whether its alignment and size conditions hold.
 bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int ldb);
 bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
-                int ldc, const float* bias, int act, hipStream_t s);
+                int ldc, const float* bias, int act, hipStream_t s, const float* res = nullptr,
+                int ldr = 0);
 bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
               int ldc, const float* bias, int act, hipStream_t s);
 bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const float* bias,
