@@ -190,8 +190,11 @@ __global__ void k_wino_filter_t(const float* __restrict__ w, int Cin, int Cinp, 
 // Filter transform as a tiled transpose: a 256-lane block owns 16 output x 16
 // input channels.  Lane (o = l%16, c = l/16) reads its 9 taps with output
 // channels fastest (64-byte runs of w), transforms them, and the block writes
-// U[a][Cout][Cinp] through LDS with input channels fastest (64-byte runs).
-template <int TILE>
+// through LDS with input channels fastest: U[a][Cout][Cinp] (64-byte runs), or
+// with CHUNK8 the chunked layout U[Cinp/8][a][Cout][8], in which the filter
+// slice one 8-channel chunk of a kernel needs for one point and 32 output
+// channels is a single contiguous kilobyte.
+template <int TILE, bool CHUNK8>
 __global__ __launch_bounds__(256) void k_wino_filter_tt(const float* __restrict__ w, int Cin,
                                                          int Cinp, int Cout, float* __restrict__ U) {
     constexpr int A = Wino<TILE>::A, AA = A * A;
@@ -222,8 +225,15 @@ __global__ __launch_bounds__(256) void k_wino_filter_tt(const float* __restrict_
     const int wc = threadIdx.x & 15, wo = threadIdx.x >> 4;
     const long long plane = (long long)Cout * Cinp;
     if (o0 + wo < Cout && c0 + wc < Cinp) {
+        const int c = c0 + wc;
+        if (CHUNK8) {
+            const long long base = (long long)(c >> 3) * AA * Cout * 8 + (long long)(o0 + wo) * 8 + (c & 7);
 #pragma unroll
-        for (int a = 0; a < AA; ++a) U[a * plane + (long long)(o0 + wo) * Cinp + c0 + wc] = tr[a][wo][wc];
+            for (int a = 0; a < AA; ++a) U[base + (long long)a * Cout * 8] = tr[a][wo][wc];
+        } else {
+#pragma unroll
+            for (int a = 0; a < AA; ++a) U[a * plane + (long long)(o0 + wo) * Cinp + c] = tr[a][wo][wc];
+        }
     }
 }
 
@@ -695,21 +705,28 @@ __global__ __launch_bounds__(512) void k_wino23(
 // the 4x4 Winograd grid for all 32 tiles (v_mfma_f32_32x32x2f32, M = tiles,
 // N = channels, K = 2 channels: 4 x 16 accumulators).  Input channels are
 // consumed in chunks of 8 (one MFMA k-step pair per lane half g = lane/32
-// holding a quad of 4 channels).  The (2R+2) x (2TC+2) pixels of a chunk are
-// DMA'd (buffer_load ... lds, zeros past the resources' ends) two chunks
-// ahead into one of three X buffers, the filter chunk U[16][32][8] (an L2
-// hit) one chunk ahead into one of two U buffers; the wait before a chunk
-// leaves the newest X loads in flight.  LDS is 53 KB, so three workgroups
-// share a CU and one's loads, barriers and stores overlap the others' MFMAs.
+// holding a quad of 4 channels).
+//
+// Software pipeline, per wave and chunk c:
+//   wait for the wave's own U(c) and X(c+1) loads;  DMA U(c+1) -- only the
+//   wave's 4 points, into its private double buffer, so U needs no barrier;
+//   MFMAs of points 0-1;  workgroup barrier (everyone's X(c+1) has landed and
+//   nobody reads X(c) any more);  DMA X(c+3) into X(c)'s buffer;  LDS reads
+//   of X(c+1);  MFMAs of points 2-3;  input transform of X(c+1) in registers.
+// The MFMAs issued before the barrier and after the reads cover the barrier
+// and the LDS latency, and X (the (2R+2) x (2TC+2) pixels of a chunk, DMA'd by
+// buffer_load ... lds with zeros past the resources' ends) is prefetched two
+// chunks ahead through three buffers.  LDS is 53 KB: three workgroups per CU.
 //
 // LDS layouts (16-byte quads): X [row][plane = col%2][kk = col/2][2 quads]
 // with kk padded to TC+1 and quad q at slot q ^ ((kk >> log2(TC/2)) & 1);
-// U [point][co][2 quads] with quad q at slot q ^ ((co >> 3) & 1).  Both
-// make every 16-lane ds_read_b128 group hit 64 distinct banks.
+// U, per wave, [point][co][2 quads] with quad q at slot q ^ ((co >> 3) & 1).
+// Both make every 16-lane ds_read_b128 group hit 64 distinct banks.
 //
 // Epilogue: wave i reduces its row with AT (S_i[c] = sum_j AT[c][j] M[i][j])
 // into LDS; every thread then forms Y[0][c] = S0+S1+S2, Y[1][c] = S1-S2+S3 for
-// one tile and 4 channels, adds bias, applies ReLU and stores 16-byte quads.
+// one tile and 4 channels, adds the bias (loaded at the start), applies the
+// activation and stores 16-byte quads.
 template <int TC, int ROW>
 struct W23Row;   // BT row ROW of a patch column: t = d[A] -/+ d[B]
 template <int TC> struct W23Row<TC, 0> { static constexpr int A = 0, B = 2, PLUS = 0; };
@@ -725,21 +742,33 @@ struct W23Cfg {
     static constexpr int SWZ = TC == 16 ? 3 : 2;       // swizzle bit of kk
     static constexpr int XSLOTS = NR * 2 * TCP * 2;
     static constexpr int XBLK = (XSLOTS + 63) / 64;    // 64-slot DMA blocks
-    static constexpr int XFL = XSLOTS * 4;             // floats (the last block's extra lanes
-                                                       // are masked off)
-    static constexpr int UFL = 16 * 32 * 2 * 4;        // 4096 floats
-    static constexpr int UOFF = 3 * XFL;               // X: 3 buffers, then U: 2 buffers
+    static constexpr int XFL = XBLK * 256;             // floats: whole DMA blocks (the slots
+                                                       // past XSLOTS load zeros, never read)
     static constexpr int KX = (XBLK + 3) / 4;          // X blocks per wave (at most)
     static constexpr int SST = 40;                     // epilogue tile stride (floats)
-    static constexpr int LDS = (3 * XFL + 2 * UFL) * 4;  // bytes
-    static_assert(4 * 2 * 32 * SST <= 3 * XFL + 2 * UFL, "epilogue tile fits the staging buffers");
+    static constexpr int EPI = 4 * 2 * 32 * SST;       // epilogue staging (floats)
+    static constexpr int LDS = (3 * XFL > EPI ? 3 * XFL : EPI) * 4;  // bytes
     static_assert(3 * LDS <= 160 * 1024, "three workgroups per CU");
+    template <int WAVE>                                // X blocks wave WAVE issues per chunk
+    static constexpr int nxw() { return XBLK > WAVE + 4 * (KX - 1) ? KX : KX - 1; }
 };
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0..4 (the count is an immediate)
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    }
+}
 
 template <int TC>
 __global__ __launch_bounds__(256, 3) void k_wino23u(
     const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
-    float* __restrict__ out, int H, int W, int Cin, int Cinp, int Cout, int rblocks, int act) {
+    float* __restrict__ out, int H, int W, int Cin, int Cinp, int Cout, int rblocks, int act,
+    int gx, int gy) {
     using CF = W23Cfg<TC>;
     constexpr int R = CF::R, TCP = CF::TCP;
     constexpr unsigned kOOB = 0x80000000u;
@@ -747,72 +776,12 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // = transform row
     const int li = lane & 31, g = lane >> 5;
-    const int n = blockIdx.y / rblocks;
-    const int ty0 = (blockIdx.y - n * rblocks) * R;
-    const int tx0 = blockIdx.x * TC;
-    const int cob = blockIdx.z * 32;
-    const float* __restrict__ img = in + (long long)n * H * W * Cin;
-
-    // ---- DMA descriptors.  X: wave w issues blocks w, w+4, ... of XSLOTS
-    // 16-byte slots; slot -> (row, plane, kk, quad slot) -> pixel + channel
-    // quad.  U: wave w issues blocks w, w+4, w+8, w+12 = points w+4t; lane l
-    // covers channel row l/2, quad slot l&1.
-    unsigned xv[CF::KX];
-    unsigned xq = 0;
-#pragma unroll
-    for (int k = 0; k < CF::KX; ++k) {
-        const int sl = (wave + 4 * k) * 64 + lane;
-        const int qslot = sl & 1;
-        const int pk = sl >> 1;                         // (row*2 + plane)*TCP + kk
-        const int rp = pk / TCP, kk = pk - rp * TCP;
-        const int row = rp >> 1, plane = rp & 1;
-        const int q = qslot ^ ((kk >> CF::SWZ) & 1);
-        const int ih = 2 * ty0 - 1 + row, iw = 2 * tx0 - 1 + 2 * kk + plane;
-        const bool ok = sl < CF::XSLOTS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-        xv[k] = ok ? (unsigned)((ih * W + iw) * Cin + 4 * q) * 4u : kOOB;
-        xq |= (unsigned)q << k;
-    }
-    unsigned uv;
-    {
-        const int co = lane >> 1;
-        const int q = (lane & 1) ^ ((co >> 3) & 1);
-        uv = cob + co < Cout ? (unsigned)((cob + co) * Cinp + 4 * q) * 4u : kOOB;
-    }
-    const unsigned upt = 4u * Cout * Cinp;             // bytes per point
-    const __amdgpu_buffer_rsrc_t xres =
-        __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, H * W * Cin * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t ures =
-        __builtin_amdgcn_make_buffer_rsrc((void*)U, (short)0, (int)(16 * upt), 0x00020000);
-    const bool ragged = (Cin & 7) != 0;
-    // X blocks this wave issues per chunk (uniform): KX or KX-1
-    const int nxw = CF::XBLK > wave + 4 * (CF::KX - 1) ? CF::KX : CF::KX - 1;
-    auto dma_u = [&](int t, int c0, float* base) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ures, (lds_void*)(base + (wave + 4 * t) * 256), 16, uv,
-            c0 * 4 + (unsigned)(wave + 4 * t) * upt, 0, 0);
-    };
-    auto dma_x = [&](int k, int c0, float* base) {
-        const int blk = wave + 4 * k;
-        if (blk >= CF::XBLK) return;
-        unsigned v = xv[k];
-        if (ragged && c0 + 8 > Cin && c0 + 4 * (int)((xq >> k) & 1) >= Cin) v = kOOB;
-        // lanes past the region are masked off, so X buffers need no padding
-        if (blk * 64 + lane < CF::XSLOTS)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + blk * 256), 16, v, c0 * 4,
-                                                     0, 0);
-    };
-    // prologue: U(0), then X(0), then X(1) -- the order the waits below assume
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dma_u(t, 0, smem + CF::UOFF);
-#pragma unroll
-    for (int k = 0; k < CF::KX; ++k) dma_x(k, 0, smem);
     const int nch = Cinp / 8;
-    if (nch > 1) {
-#pragma unroll
-        for (int k = 0; k < CF::KX; ++k) dma_x(k, 8, smem + CF::XFL);
-    }
-
-    // ---- per-lane LDS read offsets (floats, buffer 0)
+    const unsigned upt = 32u * Cout;                   // bytes per point of one chunk
+    const __amdgpu_buffer_rsrc_t ures =
+        __builtin_amdgcn_make_buffer_rsrc((void*)U, (short)0, (int)(16u * upt * (Cinp >> 3)), 0x00020000);
+    const bool ragged = (Cin & 7) != 0;
+    // per-lane LDS read offsets (floats, X buffer 0)
     const int sr = li / TC, stx = li % TC;
     int xoff[2][2];                                    // [kk = stx + jj][plane]
 #pragma unroll
@@ -822,109 +791,197 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) xoff[jj][pl] = (((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
     }
-    const int uoff = (li * 2 + (g ^ ((li >> 3) & 1))) * 4;
+    const int etile = tid >> 3, ecq = 4 * (tid & 7);   // epilogue: one tile x 4 channels
 
-    f16v acc[4];
+    // Unit u, input-channel chunks [c0, c1).  Units are numbered with the
+    // column block fastest, then image x row block, then channel block.
+    auto unit = [&](int u, int c0, int c1) {
+        const int bx = u % gx, byz = u / gx;
+        const int by = byz % gy, bz = byz / gy;
+        const int n = by / rblocks;
+        const int ty0 = (by - n * rblocks) * R;
+        const int tx0 = bx * TC;
+        const int cob = bz * 32;
+        const float* __restrict__ img = in + (long long)n * H * W * Cin;
+        const int ec = cob + ecq;
+        // bias first, so its latency hides behind the main loop
+        f4 bq = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+            for (int e = 0; e < 4; ++e) bq[e] = ec + e < Cout ? bias[ec + e] : 0.f;
+        }
 
-    auto run = [&](auto rowc) {
-        constexpr int ROW = decltype(rowc)::value;
-        using RW = W23Row<TC, ROW>;
-        int xb = 0;                                    // X buffer of chunk ch (ch % 3)
-        for (int ch = 0; ch < nch; ++ch) {
-            // Outstanding in issue order: ..., X(ch) [two chunks ago], U(ch), X(ch+1).
-            // Wait for all but this wave's X(ch+1) loads, then for every wave.
-            if (ch + 1 < nch) {
-                if (nxw == 2) __builtin_amdgcn_s_waitcnt(0x0F72);        // vmcnt(2)
-                else if (nxw == 1) __builtin_amdgcn_s_waitcnt(0x0F71);   // vmcnt(1)
-                else __builtin_amdgcn_s_waitcnt(0x0F70);
-            } else {
-                __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0)
+        // ---- DMA descriptors.  X: wave w issues blocks w, w+4, ... of XSLOTS
+        // 16-byte slots; slot -> (row, plane, kk, quad slot) -> pixel + channel
+        // quad.  U (chunked layout [Cinp/8][16][Cout][8]) goes straight to
+        // registers: wave w loads its own points 4w..4w+3, each one contiguous
+        // kilobyte, lane (li, g) the quad g of output channel li -- the MFMA B
+        // operand for four k-steps.
+        unsigned xv[CF::KX];
+        unsigned xq = 0;
+#pragma unroll
+        for (int k = 0; k < CF::KX; ++k) {
+            const int sl = (wave + 4 * k) * 64 + lane;
+            const int qslot = sl & 1;
+            const int pk = sl >> 1;                     // (row*2 + plane)*TCP + kk
+            const int rp = pk / TCP, kk = pk - rp * TCP;
+            const int row = rp >> 1, plane = rp & 1;
+            const int q = qslot ^ ((kk >> CF::SWZ) & 1);
+            const int ih = 2 * ty0 - 1 + row, iw = 2 * tx0 - 1 + 2 * kk + plane;
+            const bool ok = sl < CF::XSLOTS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            xv[k] = ok ? (unsigned)((ih * W + iw) * Cin + 4 * q) * 4u : kOOB;
+            xq |= (unsigned)q << k;
+        }
+        const unsigned uv = cob + li < Cout ? (unsigned)((cob + li) * 8 + 4 * g) * 4u : kOOB;
+        const __amdgpu_buffer_rsrc_t xres =
+            __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, H * W * Cin * 4, 0x00020000);
+        // chunk c0 + j goes to X buffer j % 3
+        auto ld_u = [&](int j, f4* ub) {               // U(j): this wave's 4 points
+            const unsigned cbase = (unsigned)(c0 + j) * 16u * upt;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ub[k] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(ures, uv, cbase + (unsigned)(4 * wave + k) * upt, 0));
+        };
+        // X(j) into base: blocks WAVE, WAVE+4, ... (a compile-time count per wave,
+        // all lanes active, so the compiler's wait counts are exact)
+        auto dma_x = [&](auto wavec, int j, float* base) {
+            constexpr int WAVE = decltype(wavec)::value;
+            const int ci = 8 * (c0 + j);
+#pragma unroll
+            for (int k = 0; k < CF::KX; ++k) {
+                if (WAVE + 4 * k >= CF::XBLK) continue;
+                unsigned v = xv[k];
+                if (ragged && ci + 8 > Cin && ci + 4 * (int)((xq >> k) & 1) >= Cin) v = kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + (WAVE + 4 * k) * 256), 16,
+                                                         v, ci * 4, 0, 0);
             }
-            // Workgroup barrier ordering LDS only: __syncthreads() would also wait
-            // for the X loads still in flight.  This wave's LDS reads have
-            // completed (lgkmcnt(0)); the memory clobber keeps the compiler from
-            // moving LDS accesses across it.
+        };
+
+        const int m = c1 - c0;                          // chunks of this range (even)
+        f16v acc[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+
+        auto run = [&](auto rowc) {
+            constexpr int ROW = decltype(rowc)::value;
+            using RW = W23Row<TC, ROW>;
+            constexpr int NXW = CF::template nxw<ROW>();   // X blocks this wave issues per chunk
+
+            // ---- prologue: U(0), X(0), X(1), X(2) in this order; wait for U(0),
+            // X(0).  Loads past the range repeat a chunk of it into a buffer no
+            // one reads, so every step issues the same loads.
+            f4 uA[4], uB[4];
+            ld_u(0, uA);
+            dma_x(rowc, 0, smem);
+            dma_x(rowc, m > 1 ? 1 : 0, smem + CF::XFL);
+            dma_x(rowc, m > 2 ? 2 : 0, smem + 2 * CF::XFL);
+            wait_vmcnt(2 * NXW);
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            const float* X = smem + xb * CF::XFL;
-            const float* Ub = smem + CF::UOFF + (ch & 1) * CF::UFL;
-            float* nu = smem + CF::UOFF + ((ch + 1) & 1) * CF::UFL;   // U(ch+1)
-            const int xb2 = xb == 0 ? 2 : xb - 1;                     // (ch + 2) % 3
-            float* nx = smem + xb2 * CF::XFL;                          // X(ch+2)
-            const bool du = ch + 1 < nch, dx = ch + 2 < nch;
-            f4 bf[4];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) bf[a] = *(const f4*)&Ub[uoff + (4 * ROW + a) * 256];
-            f4 t[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int o = xoff[j >> 1][j & 1];
-                f4 dA = *(const f4*)&X[o + RW::A * 2 * TCP * 8];
-                f4 dB = *(const f4*)&X[o + RW::B * 2 * TCP * 8];
-                t[j] = RW::PLUS ? dA + dB : dA - dB;
-            }
-            f4 dh[4];
-            dh[0] = t[0] - t[2];
-            dh[1] = t[1] + t[2];
-            dh[2] = t[2] - t[1];
-            dh[3] = t[3] - t[1];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-#pragma unroll
-                for (int s2 = 0; s2 < 4; ++s2) {
-                    acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(dh[a][s2], bf[a][s2], acc[a], 0, 0, 0);
-                    const int item = a * 4 + s2;             // U(ch+1) first, then X(ch+2)
-                    if (item < 4) {
-                        if (du) dma_u(item, (ch + 1) * 8, nu);
-                    } else if (item < 4 + CF::KX) {
-                        if (dx) dma_x(item - 4, (ch + 2) * 8, nx);
-                    }
-                }
-            }
-            xb = xb == 2 ? 0 : xb + 1;
-        }
-    };
-    switch (wave) {
-        case 0: run(std::integral_constant<int, 0>{}); break;
-        case 1: run(std::integral_constant<int, 1>{}); break;
-        case 2: run(std::integral_constant<int, 2>{}); break;
-        default: run(std::integral_constant<int, 3>{}); break;
-    }
 
-    // ---- epilogue.  Lane l, register r <-> MFMA row (tile) 8*(r/4)+4*(l/32)+r%4,
-    // column (channel) l%32.  S layout [row 4][c 2][tile 32][SST floats].
-    __syncthreads();                     // staging buffers are free
-    {
-        float* p = smem + (wave * 2) * 32 * CF::SST + (4 * g) * CF::SST + li;
+            // row ROW of BT d for the lane's 4 patch columns (LDS reads), then BT
+            // along the columns: dh[j] = (BT d BT^T)[ROW][j]
+            auto xread = [&](const float* X, f4* dA, f4* dB) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int tt = 8 * (r >> 2) + (r & 3);
-            float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
-            p[tt * CF::SST] = m0 + m1 + m2;                    // S_i[0]
-            p[(32 + tt) * CF::SST] = m1 - m2 + m3;             // S_i[1]
+                for (int j = 0; j < 4; ++j) {
+                    const int o = xoff[j >> 1][j & 1];
+                    dA[j] = *(const f4*)&X[o + RW::A * 2 * TCP * 8];
+                    dB[j] = *(const f4*)&X[o + RW::B * 2 * TCP * 8];
+                }
+            };
+            auto xform = [&](const f4* dA, const f4* dB, f4* dh) {
+                f4 tt[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) tt[j] = RW::PLUS ? dA[j] + dB[j] : dA[j] - dB[j];
+                dh[0] = tt[0] - tt[2];
+                dh[1] = tt[1] + tt[2];
+                dh[2] = tt[2] - tt[1];
+                dh[3] = tt[3] - tt[1];
+            };
+            auto mfma_pt = [&](int a, const f4& d, const f4& bb) {
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2)
+                    acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(d[s2], bb[s2], acc[a], 0, 0, 0);
+            };
+            f4 dh[4];
+            {
+                f4 dA[4], dB[4];
+                xread(smem, dA, dB);
+                xform(dA, dB, dh);
+            }
+            int xb = 0;                                // X buffer of chunk j: j % 3
+            // chunk j multiplies with bf = U(j) and loads U(j+1) into un
+            auto chunk = [&](int j, const f4* bf, f4* un) {
+                // this wave's U(j) and X(j+1) have landed; X(j+2) may stay in flight
+                wait_vmcnt(NXW);
+                ld_u(j + 1 < m ? j + 1 : j, un);
+                mfma_pt(0, dh[0], bf[0]);
+                mfma_pt(1, dh[1], bf[1]);
+                const int xb1 = xb == 2 ? 0 : xb + 1;  // buffer of X(j+1)
+                // LDS-only workgroup barrier: __syncthreads() would also wait for
+                // the DMA still in flight.  lgkmcnt(0): this wave's LDS reads are
+                // complete; the memory clobber keeps LDS accesses on their side.
+                // After it X(j+1) is visible and X(j)'s buffer is free.
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                dma_x(rowc, j + 3 < m ? j + 3 : j, smem + xb * CF::XFL);
+                // X(j+1) (after the last chunk: a buffer whose loads completed at
+                // the wait above, read before any wave reaches the epilogue,
+                // results unused) -- unconditional so the transform can
+                // interleave with the MFMAs
+                f4 dA[4], dB[4];
+                xread(smem + xb1 * CF::XFL, dA, dB);
+                __builtin_amdgcn_sched_barrier(0);      // the reads go out first
+                mfma_pt(2, dh[2], bf[2]);
+                mfma_pt(3, dh[3], bf[3]);
+                xform(dA, dB, dh);
+                // two MFMAs cover the LDS latency, then the transform's 32 VALU
+                // operations interleave with the remaining six
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+                for (int i = 0; i < 6; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+                xb = xb1;
+            };
+            for (int j = 0; j < m; j += 2) {           // two register sets for U, no copies
+                chunk(j, uA, uB);
+                chunk(j + 1, uB, uA);
+            }
+        };
+        switch (wave) {
+            case 0: run(std::integral_constant<int, 0>{}); break;
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            default: run(std::integral_constant<int, 3>{}); break;
         }
-    }
-    __syncthreads();
-    {
-        const int tile = tid >> 3, cq = tid & 7;
-        const int c = cob + 4 * cq;
-        const int tsr = tile / TC, tsx = tile % TC;
-        const int oh0 = 2 * (ty0 + tsr), ow0 = 2 * (tx0 + tsx);
+
+        // ---- epilogue.  Lane l, register r <-> MFMA row (tile) 8*(r/4)+4*(l/32)+r%4,
+        // column (channel) l%32.  S layout [row 4][c 2][tile 32][SST floats].
+        wait_vmcnt(0);                       // the last (repeated) X loads have landed
+        __syncthreads();                     // staging buffers are free
+        {
+            float* pp = smem + (wave * 2) * 32 * CF::SST + (4 * g) * CF::SST + li;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tt = 8 * (r >> 2) + (r & 3);
+                float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
+                pp[tt * CF::SST] = m0 + m1 + m2;                   // S_i[0]
+                pp[(32 + tt) * CF::SST] = m1 - m2 + m3;            // S_i[1]
+            }
+        }
+        __syncthreads();
         f4 S[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc)
-                S[i][cc] = *(const f4*)&smem[((i * 2 + cc) * 32 + tile) * CF::SST + 4 * cq];
-        f4 bq = {0.f, 0.f, 0.f, 0.f};
-        if (bias) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bq[e] = c + e < Cout ? bias[c + e] : 0.f;
-        }
-        if (c < Cout) {
+                S[i][cc] = *(const f4*)&smem[((i * 2 + cc) * 32 + etile) * CF::SST + ecq];
+        if (ec < Cout) {
+            const int tsr = etile / TC, tsx = etile % TC;
+            const int oh0 = 2 * (ty0 + tsr), ow0 = 2 * (tx0 + tsx);
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -935,16 +992,18 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
                     v = v + bq;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = act_apply(v[e], act);
-                    float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + c;
-                    if (c + 4 <= Cout && (Cout & 3) == 0) {
+                    float* dst = out + (((long long)n * H + oh) * W + ow) * Cout + ec;
+                    if (ec + 4 <= Cout && (Cout & 3) == 0) {
                         *(f4*)dst = v;
                     } else {
-                        for (int e = 0; e < 4 && c + e < Cout; ++e) dst[e] = v[e];
+                        for (int e = 0; e < 4 && ec + e < Cout; ++e) dst[e] = v[e];
                     }
                 }
             }
         }
-    }
+    };
+
+    unit(blockIdx.x, 0, nch);
 }
 
 template <int TC>
@@ -958,9 +1017,9 @@ bool launch_wino23u(const float* in, const float* U, const float* bias, float* o
                                   hipFuncAttributeMaxDynamicSharedMemorySize, CF::LDS);
     }
     const int rblocks = (tH + CF::R - 1) / CF::R;
-    dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
-    ACFUN_LAUNCH("k_wino23", k_wino23u<TC>, grid, dim3(256), CF::LDS, s, in, U, bias, out, H, W, Cin, Cinp,
-                       Cout, rblocks, act);
+    const int gx = (tW + TC - 1) / TC, gy = N * rblocks, gz = (Cout + 31) / 32;
+    ACFUN_LAUNCH("k_wino23", k_wino23u<TC>, dim3((unsigned)(gx * gy * gz)), dim3(256), CF::LDS, s, in,
+                 U, bias, out, H, W, Cin, Cinp, Cout, rblocks, act, gx, gy);
     return check_launch("k_wino23u");
 }
 
@@ -975,21 +1034,24 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     }
     Scratch U((size_t)16 * Cout * Cinp * sizeof(float), s);
     if (!U.p) return false;
-    ACFUN_LAUNCH("k_wino_filter_t", k_wino_filter_tt<2>, dim3((Cout + 15) / 16, Cinp / 16),
-                 dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
-    if (!check_launch("k_wino_filter_t")) return false;
     // 32-tile units (three workgroups per CU) when the image is wide enough to
     // fill them; buffer resources address one image and the filter with 32-bit
-    // byte offsets.
-    if ((long long)H * W * Cin * 4 < (1ll << 31) && 16ll * Cout * Cinp * 4 < (1ll << 31) &&
-        (long long)N * ((tH + 1) / 2) < 65536) {
+    // byte offsets.  They read the chunked filter layout.
+    const bool unit32 = (long long)H * W * Cin * 4 < (1ll << 31) &&
+                        16ll * Cout * Cinp * 4 < (1ll << 31) && (long long)N * ((tH + 1) / 2) < 65536 &&
+                        tW >= 6;
+    if (unit32) {
+        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, true>), dim3((Cout + 15) / 16, Cinp / 16),
+                     dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
+        if (!check_launch("k_wino_filter_t")) return false;
         if (tW >= 12)
             return launch_wino23u<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
                                       act, s);
-        if (tW >= 6)
-            return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
-                                     act, s);
+        return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
     }
+    ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, false>), dim3((Cout + 15) / 16, Cinp / 16),
+                 dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
+    if (!check_launch("k_wino_filter_t")) return false;
     // Block: TC tile columns x R tile rows of one image, R*TC <= 128 slots and
     // two LDS buffers (padded X region + 16*32*16 filter floats) within 160 KB.
     auto buf_floats = [](int R, int TC) {
@@ -1013,7 +1075,8 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     static bool attr = false;
     if (!attr) {
         attr = true;
-        hipFuncSetAttribute((const void*)k_wino23, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute((const void*)k_wino23, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024);
     }
     int rblocks = (tH + R - 1) / R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));

@@ -324,20 +324,42 @@ def test_config3b_full_exact(gpu, rng):
     assert_bitexact(got, oracle.conv2d_int8(x, wq, ws, b, 3, 3, 128, 1, 1, 1), "cfg3b")
 
 
+def _check_images(got, x, w, b, Cout, tol, step=4):
+    """Every image against the f64 direct convolution, a few images at a time
+    (images are independent)."""
+    for n in range(0, x.shape[0], step):
+        want = oracle.conv2d_f64(np.ascontiguousarray(x[n:n + step]), w, b, 3, 3, Cout, 1, 1, 1, 1)
+        assert rel_err(got[n:n + step], want) < tol, (n, rel_err(got[n:n + step], want))
+
+
 @pytest.mark.parametrize("N,HW,tol", [(32, 56, WINO_TOL), (8, 112, WINO_TOL)])
 def test_config2_full(gpu, rng, N, HW, tol):
-    """fp32 3x3 conv + bias + ReLU at config 2a (F(2,3)) / 2b (F(4,3)) size; the
-    first and last image are checked against the f64 direct convolution
-    (images are independent)."""
+    """fp32 3x3 conv + bias + ReLU at config 2a (F(2,3)) / 2b (F(4,3)) size,
+    every image checked."""
     C = 64
     x = rng.uniform(0, 1, (N, HW, HW, C)).astype(np.float32)
     w = (rng.standard_normal((9 * C, C)) * np.sqrt(2 / (9 * C))).astype(np.float32)
     b = (rng.standard_normal(C) * 0.01).astype(np.float32)
     got = np.zeros((N, HW, HW, C), np.float32)
     gpu.acfun_conv2d_relu(P(x), N, HW, HW, C, P(w), P(b), 3, 3, C, 1, 1, P(got))
-    for n in (0, N - 1):
-        want = oracle.conv2d_f64(np.ascontiguousarray(x[n:n + 1]), w, b, 3, 3, C, 1, 1, 1, 1)
-        assert rel_err(got[n:n + 1], want) < tol
+    _check_images(got, x, w, b, C, tol)
+
+
+# F(2,3) 32-tile units at batch sizes around config 2a, including a ragged
+# 20 -> 40 conv (4 chunks, partial output-channel block); every image is
+# checked and a second run must repeat the first bit for bit.
+@pytest.mark.parametrize("N,Cin,Cout", [(15, 64, 64), (32, 20, 40), (26, 64, 64)])
+def test_wino23_batches(gpu, rng, N, Cin, Cout):
+    HW = 56
+    x = rng.uniform(0, 1, (N, HW, HW, Cin)).astype(np.float32)
+    w = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2 / (9 * Cin))).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
+    got = np.full((N, HW, HW, Cout), np.nan, np.float32)
+    gpu.acfun_conv2d_relu(P(x), N, HW, HW, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(got))
+    _check_images(got, x, w, b, Cout, WINO_TOL)
+    again = np.full_like(got, np.nan)
+    gpu.acfun_conv2d_relu(P(x), N, HW, HW, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(again))
+    assert_bitexact(again, got, "repeat run")
 
 
 def test_config4a_full_exact(gpu, rng):
