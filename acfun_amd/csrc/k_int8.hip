@@ -4,7 +4,7 @@
 // The reference (src/conv_int8.cpp:63-148) quantizes activations to u8 with
 // zero point 128 and multiplies u8 x s8 into i32.  Here the activation byte is
 // stored as s8 = u8 - 128 (an exact bijection; a padded tap, u8 128, becomes
-// s8 0), so the products run on v_mfma_i32_16x16x64_i8 (s8 x s8 -> i32) and
+// s8 0), so the products run on s8 x s8 -> i32 MFMA and
 //     acc_u = sum(u8 * w) = acc_s + 128 * Sw[j],   Sw[j] = sum_k w[k][j]
 // recovers the reference's accumulator exactly (wrapping i32 both sides).
 //
@@ -18,9 +18,20 @@
 //              the zero-point correction of :204,226-229 cancels the 128 offset), so a
 //              direct s8 implicit GEMM reproduces it bit for bit.
 //
-// Scales never visit the host: absmax -> params -> quantize -> GEMM are
-// queued back to back, the per-tensor scale living in a small device block.
+// Kernels.  The convolution routes (acfun_conv2d_int8 and its direct/Winograd
+// entries) run k_i8mm: an LDS-DMA staged implicit GEMM on
+// v_mfma_i32_32x32x32_i8 whose epilogue forms the per-channel factors from
+// the device scalars.  Scales never visit the host: absmax (in the same launch
+// as the per-call weight preparation) -> quantize (which reduces the absmax
+// partials into the scalars) -> k_i8mm are queued back to back.  The u8-input
+// GEMM entries (acfun_gemm_int8*, acfun_conv1x1_int8) and operands too large
+// for k_i8mm's 32-bit offsets run k_igemm_i8 (register-staged,
+// v_mfma_i32_16x16x64_i8).
 #include "rt.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace acfun {
 namespace {
@@ -218,6 +229,380 @@ __global__ __launch_bounds__(256) void k_igemm_i8(I8P p) {
     }
 }
 
+// ---------------------------------------------------------------- k_i8mm
+// int8 implicit GEMM for the convolution routes: LDS-DMA staging, int8 MFMA,
+// and warp specialization between compute and store waves.
+//
+// Workgroup = 512 threads, persistent.  Waves 0-3 (compute) own a BM x BN
+// output tile as 2 x 2 waves of FM x FN v_mfma_i32_32x32x32_i8 blocks (FM =
+// BM/64, FN = BN/64).  K (k' = tap*Cinp + ic) is consumed in chunks of 128
+// bytes; a stage holds A: BM rows x 8 quads of 16 bytes and B: BN rows x 8
+// quads, quad q of row r at slot r*8 + (q ^ swz(r)), swz(r) = (r ^ (r >> 3)) & 7,
+// so 8 and 16 consecutive rows read at one quad fall on distinct banks.  Both
+// are filled by buffer_load_dwordx4 ... lds: a wave instruction fills 64
+// consecutive slots (8 rows); lane l the 16 bytes of row 8I + l/8, slot l%8.
+// A's 16 bytes are 16 channels of one input pixel at one tap (NHWC s8,
+// channels padded to Cinp, a multiple of 16); a tap outside the image, a row
+// past M or a k past K reads zeros through an out-of-range offset -- s8 0 is
+// the reference's padding value u8 128.  NST stages: chunk c+NST-1 is issued
+// while chunk c is multiplied, across tile boundaries.  In k-step s (32 k)
+// lane half h reads quad 2s+h of its A and B rows with one ds_read_b128 each.
+// At a tile's last chunk the compute waves write the raw i32 accumulators
+// into one of two LDS output tiles and go on with the next tile.
+//
+// Waves 4-7 (store) drain the previous tile from LDS during the current
+// tile's chunks: they form the reference's epilogue per element, add the
+// fused residual, apply the activation and store 16-byte runs of a row.  The
+// two groups meet only at the one barrier per chunk, and the compute waves
+// issue no stores, so their waits on the DMA counter never wait for stores.
+//
+// The workgroups' tiles are cut into 8 contiguous runs, one per XCD
+// (workgroup id mod 8), so the BN-blocks of one pixel block share an L2.
+// A-operand addressing: AM_C128 when Cinp is a multiple of 128 (a chunk lies
+// in one tap: tap, offset and bounds test are per chunk and wave-uniform),
+// AM_C64 when Cinp = 64 (two taps per chunk), AM_GEN otherwise.
+struct I8M {
+    const int8_t* A;     // s8 NHWC [N*H*W][Cinp]
+    const int8_t* Bt;    // [N][ldb], ldb a multiple of 128, zero beyond taps*Cinp
+    int M, N, K, ldb;    // K = taps * Cinp
+    int H, W, Cinp, KW, stride, pad, OH, OW;
+    unsigned a_bytes, b_bytes;
+    int epi, act;
+    const int* Sw;       // EPI_GEMM: column sums of the weights
+    const float* ws;     // per-channel weight scales (with scal: factors made here)
+    const float* bias;   // nullable
+    const float* scal;   // device scalars [0] inv_s [1] sa [2] zero flag (nullable)
+    const float* alpha;  // explicit per-channel factors (nullable: made from scal, ws)
+    const float* beta;
+    const float* res;    // residual added before the activation (nullable)
+    float* Cf;
+    int ldc, ldr;
+    int vec;             // Cf (and res) rows allow 16-byte stores/loads
+    int gm, gn;          // grid in tiles
+};
+
+enum { AM_GEN = 0, AM_C128 = 1, AM_C64 = 2 };
+
+__device__ __forceinline__ int i8swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// floor(a / b) for 0 <= a < 2^24, b >= 1 via a float reciprocal, corrected.
+__device__ __forceinline__ int udiv_small(int a, int b, float rb) {
+    int q = (int)((float)a * rb);
+    q -= (q * b > a);
+    q += ((q + 1) * b <= a);
+    return q;
+}
+
+constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+constexpr size_t i8mm_lds(int BM, int BN, int NST) { return (size_t)NST * (BM + BN) * 128; }
+
+template <int BM, int BN, int NST, int AM>
+__global__ __launch_bounds__(256) void k_i8mm(I8M p) {
+    constexpr int FM = BM / 64, FN = BN / 64;
+    constexpr int SA = BM * 128, STG = (BM + BN) * 128;
+    constexpr int AIT = BM / 32, BIT = BN / 32;      // DMA instructions per wave per chunk
+    constexpr int ITEMS = AIT + BIT;
+    constexpr int AHEAD = NST - 1;
+    constexpr unsigned kOOB = 0x80000000u;
+    typedef __attribute__((address_space(3))) void lds_void;
+    typedef int i16v __attribute__((ext_vector_type(16)));
+    extern __shared__ __attribute__((aligned(16))) int8_t sm8[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nch = (p.K + 127) >> 7;
+
+    // ---- tiles of this workgroup: t0, t0 + tstr, ... (cnt of them)
+    const int total = p.gm * p.gn, G = gridDim.x, b = blockIdx.x;
+    int t0, tstr, cnt;
+    if ((G & 7) == 0) {
+        const int x = b & 7, i = b >> 3, gx = G >> 3;
+        const int sx = (int)(((long long)x * total) >> 3);
+        const int ex = (int)(((long long)(x + 1) * total) >> 3);
+        t0 = sx + i;
+        tstr = gx;
+        cnt = ex > t0 ? (ex - t0 + gx - 1) / gx : 0;
+    } else {
+        t0 = b;
+        tstr = G;
+        cnt = b < total ? (total - b + G - 1) / G : 0;
+    }
+    const int nit = cnt * nch;
+
+    // =============================== compute waves
+    const int wm = wave >> 1, wn = wave & 1;
+    const __amdgpu_buffer_rsrc_t ares =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.A, (short)0, (int)p.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.Bt, (short)0, (int)p.b_bytes, 0x00020000);
+
+    // ---- DMA rows of this lane: row 8*(wave + 4t) + lane/8 of the A and B
+    // stages, quad slot lane%8 holding data quad aq/bq
+    const int sl = lane & 7, rl = lane >> 3;
+    int aq[AIT], bk[BIT];
+#pragma unroll
+    for (int t = 0; t < AIT; ++t) aq[t] = sl ^ i8swz(8 * (wave + 4 * t) + rl);
+#pragma unroll
+    for (int t = 0; t < BIT; ++t) bk[t] = 16 * (sl ^ i8swz(8 * (wave + 4 * t) + rl));
+    // issue-side per-tile state
+    int abase[AIT], amask[AIT];          // fast modes: byte offset at tap 0, in-bounds taps
+    int apix[AIT], aih[AIT], aiw[AIT];   // AM_GEN
+    unsigned bv[BIT];
+    auto setup = [&](int k) {
+        const int L = t0 + k * tstr;
+        const int tm = L / p.gn, tn = L - tm * p.gn;
+#pragma unroll
+        for (int t = 0; t < AIT; ++t) {
+            const int m = tm * BM + 8 * (wave + 4 * t) + rl;
+            int pix = 0, ih0 = -(1 << 28), iw0 = 0;
+            if (m < p.M) {
+                const int hw = p.OH * p.OW;
+                const int n = m / hw, rem = m - n * hw;
+                const int oh = rem / p.OW, ow = rem - oh * p.OW;
+                pix = n * p.H * p.W;
+                ih0 = oh * p.stride - p.pad;
+                iw0 = ow * p.stride - p.pad;
+            }
+            if (AM == AM_GEN) {
+                apix[t] = pix;
+                aih[t] = ih0;
+                aiw[t] = iw0;
+            } else {
+                const int q16 = AM == AM_C64 ? 16 * (aq[t] & 3) : 16 * aq[t];
+                abase[t] = m < p.M ? (pix + ih0 * p.W + iw0) * p.Cinp + q16 : 0;
+                // bit kh*8 + kw: tap (kh, kw) inside the image (KH, KW <= 8)
+                unsigned rm = 0, cm = 0;
+                for (int d = 0; d < 8; ++d) {
+                    rm |= ((unsigned)(ih0 + d) < (unsigned)p.H) ? (1u << d) : 0u;
+                    cm |= ((unsigned)(iw0 + d) < (unsigned)p.W) ? (1u << d) : 0u;
+                }
+                unsigned mk = 0;
+                for (int d = 0; d < 4; ++d) mk |= (rm >> d & 1u) ? (cm << (8 * d)) : 0u;
+                amask[t] = (int)mk;       // taps with kh < 4 (fast modes need KH <= 4)
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < BIT; ++t) {
+            const int n = tn * BN + 8 * (wave + 4 * t) + rl;
+            bv[t] = n < p.N ? (unsigned)(n * p.ldb + bk[t]) : kOOB;
+        }
+    };
+    // issue-side per-chunk state (wave-uniform): fast modes track the tap of
+    // the chunk's first quad (kh, kw) and its channel offset ic0
+    int ikh = 0, ikw = 0, iic = 0;
+    const float rcinp = 1.0f / (float)p.Cinp, rkw = 1.0f / (float)p.KW;
+    const int taps = p.K / p.Cinp;
+    auto tap_off = [&](int kh, int kw) { return (kh * p.W + kw) * p.Cinp; };
+    auto issue = [&](int t, int c, int8_t* st) {      // DMA item t of chunk c into stage st
+        if (t < AIT) {
+            unsigned v = kOOB;
+            if (AM == AM_GEN) {
+                const int k = (c << 7) + 16 * aq[t];
+                if (k < p.K) {
+                    const int tap = udiv_small(k, p.Cinp, rcinp);
+                    const int ic = k - tap * p.Cinp;
+                    const int kh = udiv_small(tap, p.KW, rkw);
+                    const int kw = tap - kh * p.KW;
+                    const int ih = aih[t] + kh, iw = aiw[t] + kw;
+                    if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
+                        v = (unsigned)((apix[t] + ih * p.W + iw) * p.Cinp + ic);
+                }
+            } else if (AM == AM_C128) {
+                const bool ok = (amask[t] >> (ikh * 8 + ikw)) & 1;
+                v = ok ? (unsigned)(abase[t] + tap_off(ikh, ikw) + iic) : kOOB;
+            } else {
+                // two taps per chunk: quads 0-3 at (ikh, ikw), quads 4-7 at the next tap
+                int kh = ikh, kw = ikw + 1;
+                if (kw == p.KW) { kw = 0; ++kh; }
+                const bool second = aq[t] >= 4;
+                const bool inK = !second || (2 * c + 1 < taps);
+                const int th = second ? kh : ikh, tw = second ? kw : ikw;
+                const bool ok = inK && ((amask[t] >> (th * 8 + tw)) & 1);
+                v = ok ? (unsigned)(abase[t] + tap_off(th, tw)) : kOOB;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ares, (lds_void*)(st + (wave + 4 * t) * 1024), 16, v, 0, 0, 0);
+        } else {
+            const int tt = t - AIT;
+            // (a local, not the captured array element, as the builtin's operand:
+            // with the latter clang drops the kernel's host-side stub)
+            const unsigned v = bv[tt] + (unsigned)(c << 7);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                bres, (lds_void*)(st + SA + (wave + 4 * tt) * 1024), 16, v, 0, 0, 0);
+        }
+    };
+    auto advance = [&]() {                             // the issue cursor's next chunk
+        if (AM == AM_C128) {
+            iic += 128;
+            if (iic == p.Cinp) { iic = 0; if (++ikw == p.KW) { ikw = 0; ++ikh; } }
+        } else if (AM == AM_C64) {
+            ikw += 2;
+            while (ikw >= p.KW) { ikw -= p.KW; ++ikh; }
+        }
+    };
+
+    // ---- LDS read offsets (bytes within a stage) of this lane, per k-step
+    const int r32 = lane & 31, hq = lane >> 5;
+    int rda[4][FM], rdb[4][FN];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * (BM / 2) + 32 * i + r32;
+            rda[s][i] = r * 128 + 16 * ((2 * s + hq) ^ i8swz(r));
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int r = wn * (BN / 2) + 32 * j + r32;
+            rdb[s][j] = SA + r * 128 + 16 * ((2 * s + hq) ^ i8swz(r));
+        }
+    }
+    i16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    // ---- prologue: the first AHEAD chunks of the item stream (tile, chunk)
+    int ik = 0, ic = 0;                         // issue cursor
+    if (nit > 0) setup(0);
+#pragma unroll
+    for (int a = 0; a < AHEAD; ++a) {
+        if (a < nit) {
+#pragma unroll
+            for (int t = 0; t < ITEMS; ++t) issue(t, ic, sm8 + a * STG);
+            advance();
+            if (++ic == nch) {
+                ic = 0;
+                ikh = ikw = iic = 0;
+                if (++ik < cnt) setup(ik);
+            }
+        }
+    }
+
+    const bool zero = p.scal && p.scal[2] != 0.0f;
+    const float sa = p.scal ? p.scal[1] : 0.0f;
+    int st = 0, ck = 0, cc = 0;                 // compute cursor
+    bool stored = false;                        // stores issued since the last full wait
+    float pv0[FN], pv1[FN];                     // epilogue inputs of the current tile
+    int pv2[FN];
+    for (int g = 0; g < nit; ++g) {
+        // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
+        // chunks issued after it may stay in flight; once stores are pending
+        // the counter no longer orders them and everything is waited for.
+        const int later = nit - 1 - g < AHEAD - 1 ? nit - 1 - g : AHEAD - 1;
+        if (stored || later <= 0) __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+        else if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * ITEMS));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
+        stored = false;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int L = t0 + ck * tstr;
+        const int tm = L / p.gn, tn = L - tm * p.gn;
+        const int m0 = tm * BM, n0 = tn * BN;
+        if (cc == 0) {                          // the tile's epilogue inputs, a chunk early
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int n = n0 + wn * (BN / 2) + 32 * j + r32;
+                const int nn = n < p.N ? n : p.N - 1;
+                pv0[j] = p.alpha ? p.alpha[nn] : p.ws[nn];
+                pv1[j] = (p.epi == EPI_GEMM && p.alpha) ? p.beta[nn] : (p.bias ? p.bias[nn] : 0.0f);
+                pv2[j] = p.epi == EPI_GEMM ? p.Sw[nn] : 0;
+            }
+        }
+        const int8_t* S = sm8 + st * STG;
+        const int sta = st == 0 ? NST - 1 : st - 1;   // (g + AHEAD) % NST
+        int8_t* NA = sm8 + sta * STG;
+        const bool more = g + AHEAD < nit;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            i4 fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[i] = *(const i4*)(S + rda[s][i]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) fb[j] = *(const i4*)(S + rdb[s][j]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            if (more) {
+#pragma unroll
+                for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, ic, NA);
+            }
+        }
+        if (more) {
+            advance();
+            if (++ic == nch) {
+                ic = 0;
+                ikh = ikw = iic = 0;
+                if (++ik < cnt) setup(ik);
+            }
+        }
+        st = st == NST - 1 ? 0 : st + 1;
+        if (++cc < nch) continue;
+        // ---- epilogue of tile ck: lane l, register e of block (i, j) <->
+        //      row m0 + wm*BM/2 + 32i + 8(e/4) + 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32
+        if (nch == 1) {                          // parameters were loaded in this iteration
+            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+        }
+        const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+        const bool gemm = p.epi == EPI_GEMM;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + wn * (BN / 2) + 32 * j + r32;
+            float al, be;
+            int corr = 0;
+            if (gemm) {
+                corr = 128 * pv2[j];
+                if (p.alpha) {
+                    al = pv0[j];
+                    be = pv1[j];
+                } else {   // src/conv_int8.cpp:100-107: alpha = sa*ws; beta = b - (alpha*128)*Sw
+                    al = __fmul_rn(sa, pv0[j]);
+                    be = __fsub_rn(pv1[j], __fmul_rn(__fmul_rn(al, 128.0f), (float)pv2[j]));
+                }
+            } else {       // src/winograd_int8.cpp:155: (s_in*0.25)*ws, then fma with the bias
+                al = p.alpha ? pv0[j] : __fmul_rn(__fmul_rn(sa, 0.25f), pv0[j]);
+                be = pv1[j];
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                float rv[16];
+                if (p.res) {   // residual of the fused Add, all 16 loads in flight at once
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (e >> 2) + 4 * hq + (e & 3);
+                        rv[e] = (full || (m < p.M && n < p.N)) ? p.res[(long long)m * p.ldr + n] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (e >> 2) + 4 * hq + (e & 3);
+                    const int a = acc[i][j][e];
+                    acc[i][j][e] = 0;
+                    // GEMM routes: fl(fl(acc_u * alpha) + beta); Winograd route:
+                    // fmaf(4*acc_s, alpha_w, bias), with (float)(4a) = 4*(float)a exactly.
+                    // An all-zero input gives 0 without the bias (src/conv_int8.cpp:78).
+                    const float u = gemm
+                        ? __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr), al), be)
+                        : fmaf(4.0f * (float)a, al, be);
+                    float v = zero ? 0.0f : u;
+                    if (p.res) v = __fadd_rn(v, rv[e]);
+                    v = act_apply(v, p.act);
+                    if (full || (m < p.M && n < p.N)) p.Cf[(long long)m * p.ldc + n] = v;
+                }
+            }
+        }
+        stored = true;
+        cc = 0;
+        ++ck;
+    }
+}
+
 // ---------------------------------------------------------------- helpers
 
 // max|x| into *bits (as the bit pattern of a non-negative float).  NaN never
@@ -252,6 +637,111 @@ __global__ void k_absmax(const float* __restrict__ x, size_t n, unsigned* __rest
         for (int k = 1; k < (int)(blockDim.x >> 6); ++k) m = red[k] > m ? red[k] : m;
         atomicMax(bits, __float_as_uint(m));
     }
+}
+
+// Block blk of nblk: max|x| over its grid-stride share into part[blk] (same
+// NaN rule as k_absmax).  Each lane keeps four independent 16-byte loads in
+// flight per iteration.
+__device__ void absmax_block(const float* __restrict__ x, size_t n, float* __restrict__ part,
+                             int blk, int nblk) {
+    float m = 0.0f;
+    const size_t nth = (size_t)nblk * 256;
+    const size_t i0 = (size_t)blk * 256 + threadIdx.x;
+    auto upd = [&](float v) { float a = fabsf(v); m = a > m ? a : m; };
+    if ((((uintptr_t)x) & 15u) == 0) {
+        const float4* x4 = (const float4*)x;
+        const size_t n4 = n / 4;
+        size_t i = i0;
+        for (; i + 3 * nth < n4; i += 4 * nth) {
+            float4 v0 = x4[i], v1 = x4[i + nth], v2 = x4[i + 2 * nth], v3 = x4[i + 3 * nth];
+            upd(v0.x); upd(v0.y); upd(v0.z); upd(v0.w);
+            upd(v1.x); upd(v1.y); upd(v1.z); upd(v1.w);
+            upd(v2.x); upd(v2.y); upd(v2.z); upd(v2.w);
+            upd(v3.x); upd(v3.y); upd(v3.z); upd(v3.w);
+        }
+        for (; i < n4; i += nth) { float4 v = x4[i]; upd(v.x); upd(v.y); upd(v.z); upd(v.w); }
+        for (size_t k = n4 * 4 + i0; k < n; k += nth) upd(x[k]);
+    } else {
+        for (size_t k = i0; k < n; k += nth) upd(x[k]);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k) m = red[k] > m ? red[k] : m;
+        part[blk] = m;
+    }
+}
+
+// Activation quantization into s8 = u8 - 128 (k_quant_act's rules), 16
+// channels of one pixel per lane and one 16-byte store.  Every block first
+// reduces the absmax partials to the tensor's max|x| and forms inv_s =
+// 127/max (src/conv_int8.cpp:78-81); block 0 also writes the device scalars
+// scal = {inv_s, sa = max/127, zero flag, max}.
+__global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, long long pix,
+                                                 int Cin, int Cinp, int8_t* __restrict__ q,
+                                                 const float* __restrict__ part, int nparts,
+                                                 float* __restrict__ scal, int mode, int cvec) {
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += 256) { float a = part[i]; m = a > m ? a : m; }
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float maxa = red[0];
+    for (int k = 1; k < 4; ++k) maxa = red[k] > maxa ? red[k] : maxa;
+    const bool zero = maxa < 1e-12f;
+    const float inv_s = 127.0f / maxa;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        scal[0] = inv_s;
+        scal[1] = maxa / 127.0f;
+        scal[2] = zero ? 1.0f : 0.0f;
+        scal[3] = maxa;
+    }
+    const int groups = Cinp >> 4;
+    const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (g >= pix * groups) return;
+    const long long pp = g / groups;
+    const int c0 = (int)(g - pp * groups) * 16;
+    const float* src = x + pp * Cin + c0;
+    float v[16];
+    if (c0 + 16 <= Cin && (((uintptr_t)src) & 15u) == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float4 f = ((const float4*)src)[k];
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = c0 + k < Cin ? src[k] : 0.0f;
+    }
+    unsigned w[4] = {0u, 0u, 0u, 0u};
+    if (!zero) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int c = c0 + k;
+            int out = 0;
+            if (c < Cin) {
+                const float t = __fmul_rn(v[k], inv_s);
+                int r;
+                if (mode == 0) r = (int)rintf(t);
+                else if (c < cvec) r = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
+                else r = (int)roundf(t);
+                int u = r + 128;
+                u = u < 0 ? 0 : (u > 255 ? 255 : u);
+                out = u - 128;
+            }
+            w[k >> 2] |= ((unsigned)out & 0xffu) << (8 * (k & 3));
+        }
+    }
+    *(i4*)(q + pp * Cinp + c0) = i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
 
 __global__ void k_fill_u32(unsigned* p, int n, unsigned v) {
@@ -346,11 +836,8 @@ __global__ void k_u8_to_s8(const uint8_t* __restrict__ x, long long pix, int Cin
 // and for k' >= taps*Cinp), and Sw[n] = sum_k wq[k][n] (exact i32).  One
 // 256-thread block per output channel n: the row is written contiguously and
 // summed in the same pass.
-__global__ __launch_bounds__(256) void k_prep_weights(const int8_t* __restrict__ wq, int taps,
-                                                      int Cin, int Cinp, int N,
-                                                      int8_t* __restrict__ Bt, int ldb,
-                                                      int* __restrict__ Sw) {
-    const int n = blockIdx.x;
+__device__ void prep_row(const int8_t* __restrict__ wq, int taps, int Cin, int Cinp, int N,
+                         int8_t* __restrict__ Bt, int ldb, int* __restrict__ Sw, int n) {
     int sum = 0;
     for (int kp = threadIdx.x; kp < ldb; kp += 256) {
         int tap = kp / Cinp, ic = kp - tap * Cinp;
@@ -365,6 +852,30 @@ __global__ __launch_bounds__(256) void k_prep_weights(const int8_t* __restrict__
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
     __syncthreads();
     if (threadIdx.x == 0) Sw[n] = red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void k_prep_weights(const int8_t* __restrict__ wq, int taps,
+                                                      int Cin, int Cinp, int N,
+                                                      int8_t* __restrict__ Bt, int ldb,
+                                                      int* __restrict__ Sw) {
+    prep_row(wq, taps, Cin, Cinp, N, Bt, ldb, Sw, blockIdx.x);
+}
+
+__global__ __launch_bounds__(256) void k_absmax_part(const float* __restrict__ x, size_t n,
+                                                     float* __restrict__ part) {
+    absmax_block(x, n, part, blockIdx.x, gridDim.x);
+}
+
+// The activation absmax (blocks < nb) and, in the same launch, the per-call
+// weight preparation (one block per output channel after them).
+__global__ __launch_bounds__(256) void k_absmax_prep(const float* __restrict__ x, size_t n,
+                                                     float* __restrict__ part, int nb,
+                                                     const int8_t* __restrict__ wq, int taps,
+                                                     int Cin, int Cinp, int N,
+                                                     int8_t* __restrict__ Bt, int ldb,
+                                                     int* __restrict__ Sw) {
+    if ((int)blockIdx.x < nb) absmax_block(x, n, part, blockIdx.x, nb);
+    else prep_row(wq, taps, Cin, Cinp, N, Bt, ldb, Sw, blockIdx.x - nb);
 }
 
 // acfun_quantize_weights (src/conv_int8.cpp:24-37): one lane per column.
@@ -427,16 +938,118 @@ bool launch_i8(const I8P& p, bool conv, bool va, hipStream_t s) {
     return launch_i8_v<false, false>(p, bm, bn, s);
 }
 
+// k_i8mm tile choice.  ACFUN_I8_TILE="BMxBNxNST" overrides the tile and
+// ACFUN_I8_GRID=<workgroups per CU> caps the grid (persistent workgroups);
+// both exist for tile sweeps.
+struct I8Tile { int bm, bn, nst, per_cu; };
+I8Tile pick_i8mm_tile(int M, int N, int K) {
+    static int forced = -1;
+    static I8Tile ft{64, 64, 3, 0};
+    static int grid_cap = 0;
+    if (forced < 0) {
+        forced = 0;
+        if (const char* e = getenv("ACFUN_I8_TILE")) {
+            int a, b, c;
+            if (sscanf(e, "%dx%dx%d", &a, &b, &c) == 3 && (a == 64 || a == 128) &&
+                (b == 64 || b == 128) && c >= 2 && c <= 4) {
+                ft = I8Tile{a, b, c, 0};
+                forced = 1;
+            }
+        }
+        if (const char* e = getenv("ACFUN_I8_GRID")) grid_cap = atoi(e);
+    }
+    I8Tile t;
+    if (forced == 1) {
+        t = ft;
+    } else {
+        // Measured on configs 3a/3b: 64 x 64 tiles (five workgroups per CU) and
+        // one tile per workgroup beat larger and persistent tiles.
+        (void)M; (void)N;
+        t = I8Tile{64, 64, (K + 127) / 128 > 2 ? 3 : 2, 0};
+    }
+    t.per_cu = grid_cap;
+    return t;
+}
+
+// Whether k_i8mm's 32-bit buffer offsets cover the operands.
+bool i8mm_fits(long long a_bytes, long long n, int ldb) {
+    return a_bytes < 0x7fffffffll && n * ldb < 0x7fffffffll;
+}
+
+template <int BM, int BN, int NST, int AM>
+bool launch_i8mm_t(I8M& p, int cap, hipStream_t s) {
+    constexpr size_t lds = i8mm_lds(BM, BN, NST);
+    static_assert(lds <= 160 * 1024, "k_i8mm LDS");
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_i8mm<BM, BN, NST, AM>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    }
+    p.gm = (p.M + BM - 1) / BM;
+    p.gn = (p.N + BN - 1) / BN;
+    // one tile per workgroup, or (cap > 0) at most cap persistent workgroups per
+    // CU, a multiple of 8 (the per-XCD runs)
+    const long long total = (long long)p.gm * p.gn;
+    long long gsz = total;
+    if (cap > 0) {
+        gsz = std::min(total, (long long)cap * num_cus());
+        if (gsz >= 8) gsz &= ~7ll;
+    }
+    dim3 grid((unsigned)gsz);
+    ACFUN_LAUNCH("k_igemm_i8", (k_i8mm<BM, BN, NST, AM>), grid, dim3(256), lds, s, p);
+    return check_launch("k_i8mm");
+}
+
+template <int AM>
+bool launch_i8mm_am(I8M& p, const I8Tile& t, hipStream_t s) {
+#define ACFUN_I8MM(BM, BN, NST) \
+    if (t.bm == BM && t.bn == BN && t.nst == NST) return launch_i8mm_t<BM, BN, NST, AM>(p, t.per_cu, s);
+    ACFUN_I8MM(128, 128, 2) ACFUN_I8MM(128, 128, 3) ACFUN_I8MM(128, 128, 4)
+    ACFUN_I8MM(64, 128, 2) ACFUN_I8MM(64, 128, 3) ACFUN_I8MM(64, 128, 4)
+    ACFUN_I8MM(128, 64, 2) ACFUN_I8MM(128, 64, 3) ACFUN_I8MM(128, 64, 4)
+    ACFUN_I8MM(64, 64, 2) ACFUN_I8MM(64, 64, 3) ACFUN_I8MM(64, 64, 4)
+#undef ACFUN_I8MM
+    set_error("k_i8mm: no tile %dx%dx%d", t.bm, t.bn, t.nst);
+    return false;
+}
+
+bool launch_i8mm(I8M& p, hipStream_t s) {
+    if (p.M <= 0 || p.N <= 0) return true;
+    const I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
+    auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    p.vec = al16(p.Cf) && p.ldc % 4 == 0 && (!p.res || (al16(p.res) && p.ldr % 4 == 0));
+    const int KH = p.K / p.Cinp / p.KW;
+    const bool small = p.KW <= 8 && KH <= 4;    // the fast modes' tap bitmask: 4 rows x 8 columns
+    if (small && p.Cinp % 128 == 0) return launch_i8mm_am<AM_C128>(p, t, s);
+    if (small && p.Cinp == 64) return launch_i8mm_am<AM_C64>(p, t, s);
+    return launch_i8mm_am<AM_GEN>(p, t, s);
+}
+
+// Fills the convolution part of k_i8mm's arguments.
+void i8mm_conv(I8M& p, const int8_t* q, const ConvShape& g, int Cinp, const int8_t* bt, int ldb,
+               int Cout) {
+    p.A = q; p.Bt = bt; p.M = g.N * g.OH * g.OW; p.N = Cout; p.K = g.KH * g.KW * Cinp;
+    p.ldb = ldb; p.H = g.H; p.W = g.W; p.Cinp = Cinp; p.KW = g.KW; p.stride = g.stride;
+    p.pad = g.pad; p.OH = g.OH; p.OW = g.OW;
+    p.a_bytes = (unsigned)((long long)g.N * g.H * g.W * Cinp);
+    p.b_bytes = (unsigned)((long long)Cout * ldb);
+    p.ldc = Cout;
+}
+
 // Prepared weights: Bt [N][ldb] and Sw [N] in pooled device memory.
 struct PrepW {
     Scratch bt, sw;
     int ldb = 0;
 };
-bool prep_weights(const int8_t* wq, int taps, int Cin, int Cinp, int N, hipStream_t s, PrepW& w) {
-    w.ldb = rup(taps * Cinp, 16);
+bool alloc_weights(int taps, int Cinp, int N, hipStream_t s, PrepW& w) {
+    w.ldb = rup(taps * Cinp, 128);
     w.bt = Scratch((size_t)N * w.ldb, s);
     w.sw = Scratch((size_t)N * sizeof(int), s);
-    if (!w.bt.p || !w.sw.p) return false;
+    return w.bt.p && w.sw.p;
+}
+bool prep_weights(const int8_t* wq, int taps, int Cin, int Cinp, int N, hipStream_t s, PrepW& w) {
+    if (!alloc_weights(taps, Cinp, N, s, w)) return false;
     hipLaunchKernelGGL(k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N,
                        w.bt.as<int8_t>(), w.ldb, w.sw.as<int>());
     return check_launch("k_prep_weights");
@@ -487,6 +1100,13 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
     if (!check_launch("k_u8_to_s8")) return false;
     PrepW w;
     if (!prep_weights(wq, g.KH * g.KW, g.Cin, Cinp, Cout, s, w)) return false;
+    if (i8mm_fits(pix * Cinp, Cout, w.ldb)) {
+        I8M p{};
+        i8mm_conv(p, q.as<int8_t>(), g, Cinp, w.bt.as<int8_t>(), w.ldb, Cout);
+        p.epi = EPI_GEMM; p.act = act; p.Sw = w.sw.as<int>(); p.alpha = alpha; p.beta = beta;
+        p.Cf = out;
+        return launch_i8mm(p, s);
+    }
     I8P p{};
     p.A = q.as<int8_t>(); p.Bt = w.bt.as<int8_t>(); p.M = g.N * g.OH * g.OW; p.N = Cout;
     p.K = g.KH * g.KW * Cinp; p.ldb = w.ldb;
@@ -505,6 +1125,50 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     int Cinp = rup(g.Cin, 16);
     long long pix = (long long)g.N * g.H * g.W;
     size_t inN = (size_t)pix * g.Cin;
+    PrepW w;
+    const int8_t* bt;
+    const int* sw;
+    int ldb;
+    const bool prepared = pre && pre->bt && pre->taps == g.KH * g.KW && pre->Cin == g.Cin &&
+                          pre->N == Cout;
+    if (prepared) {
+        bt = pre->bt; sw = pre->sw; ldb = pre->ldb;
+    } else {
+        if (!alloc_weights(g.KH * g.KW, Cinp, Cout, s, w)) return false;
+        bt = w.bt.as<int8_t>(); sw = w.sw.as<int>(); ldb = w.ldb;
+    }
+    if (i8mm_fits(pix * Cinp, Cout, ldb)) {
+        // absmax partials -> quantize (reduces them, writes the scalars) -> k_i8mm,
+        // whose epilogue forms the per-channel factors from the scalars
+        constexpr int kParts = 512;
+        Scratch par((size_t)(8 + kParts) * sizeof(float), s);
+        Scratch q((size_t)pix * Cinp, s);
+        if (!par.p || !q.p) return false;
+        float* scal = par.as<float>();
+        float* part = scal + 8;
+        long long n4 = (long long)(inN / 4);
+        int nb = (int)((n4 + 1023) / 1024);
+        nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
+        hipLaunchKernelGGL(k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
+                           inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, w.bt.as<int8_t>(),
+                           ldb, w.sw.as<int>());
+        if (!check_launch("k_absmax_prep")) return false;
+        const long long groups = pix * (Cinp / 16);
+        hipLaunchKernelGGL(k_quant16, g1(groups), dim3(256), 0, s, in, pix, g.Cin, Cinp,
+                           q.as<int8_t>(), part, nb, scal, wino ? 2 : 0, g.Cin & ~15);
+        if (!check_launch("k_quant16")) return false;
+        I8M p{};
+        i8mm_conv(p, q.as<int8_t>(), g, Cinp, bt, ldb, Cout);
+        p.act = act; p.scal = scal; p.ws = ws; p.bias = bias; p.Cf = out;
+        if (wino) p.epi = EPI_WINO;
+        else { p.epi = EPI_GEMM; p.Sw = sw; }
+        return launch_i8mm(p, s);
+    }
+    if (!prepared) {
+        hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
+                           Cinp, Cout, w.bt.as<int8_t>(), ldb, w.sw.as<int>());
+        if (!check_launch("k_prep_weights")) return false;
+    }
     // device block: [0..3] scalars+maxbits, then alpha, beta, alpha_w
     Scratch par((size_t)(8 + 3 * Cout) * sizeof(float), s);
     Scratch q((size_t)pix * Cinp, s);
@@ -514,16 +1178,6 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     float* alpha = scal + 8;
     float* beta = alpha + Cout;
     float* alpha_w = beta + Cout;
-    PrepW w;
-    const int8_t* bt;
-    const int* sw;
-    int ldb;
-    if (pre && pre->bt && pre->taps == g.KH * g.KW && pre->Cin == g.Cin && pre->N == Cout) {
-        bt = pre->bt; sw = pre->sw; ldb = pre->ldb;
-    } else {
-        if (!prep_weights(wq, g.KH * g.KW, g.Cin, Cinp, Cout, s, w)) return false;
-        bt = w.bt.as<int8_t>(); sw = w.sw.as<int>(); ldb = w.ldb;
-    }
     hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, s, bits, 1, 0u);
     if (!check_launch("k_fill_u32")) return false;
     int nb = (int)((inN / 4 + 255) / 256);
@@ -565,6 +1219,13 @@ bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8
     if (!check_launch("k_alpha_w")) return false;
     PrepW w;
     if (!prep_weights(wq, 9, Cin, Cinp, Cout, s, w)) return false;
+    if (i8mm_fits(pix * Cinp, Cout, w.ldb)) {
+        ConvShape g{N, H, W, Cin, 3, 3, 1, 1, H, W};
+        I8M p{};
+        i8mm_conv(p, q.as<int8_t>(), g, Cinp, w.bt.as<int8_t>(), w.ldb, Cout);
+        p.epi = EPI_WINO; p.act = act; p.alpha = aw.as<float>(); p.bias = bias; p.Cf = out;
+        return launch_i8mm(p, s);
+    }
     I8P p{};
     p.A = q.as<int8_t>(); p.Bt = w.bt.as<int8_t>(); p.M = N * H * W; p.N = Cout;
     p.K = 9 * Cinp; p.ldb = w.ldb;
@@ -576,7 +1237,7 @@ bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8
 bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStream_t s) {
     i8_release(w);
     int Cinp = rup(Cin, 16);
-    w.ldb = rup(taps * Cinp, 16);
+    w.ldb = rup(taps * Cinp, 128);
     if (!check(hipMalloc((void**)&w.bt, (size_t)N * w.ldb), "hipMalloc(int8 weights)") ||
         !check(hipMalloc((void**)&w.sw, (size_t)N * sizeof(int)), "hipMalloc(int8 sums)")) {
         i8_release(w);
