@@ -59,7 +59,7 @@ bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float
     if (KH == 3 && KW == 3 && stride == 1 && pad == 1 && H >= 3 && W >= 3 && Cin >= 4 &&
         Cout >= 4) {  // :169-176
         int tile = (H >= 112 && W >= 112 && Cin >= 64 && Cout >= 64) ? 4 : 2;
-        return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
+        return winograd_route_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
     }
     int OH = (H + 2 * pad - KH) / stride + 1;  // :178-194
     int OW = (W + 2 * pad - KW) / stride + 1;

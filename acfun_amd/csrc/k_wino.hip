@@ -1113,4 +1113,14 @@ bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const
     return run_wino23(in, N, H, W, Cin, w, bias, Cout, out, act, s);
 }
 
+bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
+                        const float* bias, int Cout, float* out, int act, hipStream_t s) {
+    // Measured on MI355X at BASELINE config 2(b) (8 x 112^2 x 64 -> 64): the
+    // F(2,3) unit kernel (k_wino23u) takes about half the time of k_wino_fused<4>,
+    // so the F(4,3) route runs it whenever its staging conditions hold.
+    const bool unit23 = Cin % 4 == 0 && ((uintptr_t)in & 15u) == 0 && (W + 1) / 2 >= 6;
+    if (tile == 4 && unit23) tile = 2;
+    return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
+}
+
 }  // namespace acfun

@@ -137,6 +137,12 @@ bool round_bf16(const float* in, float* out, size_t n, hipStream_t s);
 // Winograd 3x3/s1/p1 (tile = 2 for F(2,3), 4 for F(4,3)).
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
                   const float* bias, int Cout, float* out, int act, hipStream_t s);
+// The conv2d route's Winograd step: the route names the tile the reference
+// would use; both tiles compute the direct convolution exactly over the
+// rationals, so the faster kernel for the shape runs (within the Winograd
+// tolerance of the reference either way).
+bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
+                        const float* bias, int Cout, float* out, int act, hipStream_t s);
 
 // Bandwidth kernels.
 bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, const float* bias,
