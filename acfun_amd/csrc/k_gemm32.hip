@@ -32,14 +32,21 @@ typedef __attribute__((address_space(3))) void lds_void32;
 constexpr int G32_BM = 64, G32_BN = 64, G32_KC = 64;
 constexpr int G32_STAGE = 2 * 1024 * 4;           // floats per stage: A + B, 1024 quads each
 
-template <int NST>
+// Implicit-GEMM convolution geometry (CONV mode): A is the NHWC input
+// [n][H][W][Cin], row m of the GEMM the output pixel (n, oh, ow), k = tap*Cin + ic.
+struct G32Conv {
+    int H, W, Cin, KW, stride, pad, OH, OW;
+    unsigned bytes;    // N*H*W*Cin*4, below 2^31
+};
+
+template <int NST, bool CONV>
 __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 float* __restrict__ C,
                                                 const float* __restrict__ bias,
                                                 const float* __restrict__ res, int M, int N,
                                                 int K, int lda, int ldb, int ldc, int ldr,
-                                                int act) {
+                                                int act, G32Conv cv) {
     constexpr unsigned kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -50,16 +57,46 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 
     // ---- DMA descriptors.  Wave w issues A blocks and B blocks w + 4t
     // (t = 0..3); lane l of block b covers slot 64b + l = row*16 + quad slot.
-    const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(A + (long long)m0 * lda), (short)0,
-        (int)((long long)(M - m0) * lda * 4 < 0x7fffffff ? (long long)(M - m0) * lda * 4 : 0x7fffffff),
-        0x00020000);
+    const __amdgpu_buffer_rsrc_t ares = CONV
+        ? __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)cv.bytes, 0x00020000)
+        : __builtin_amdgcn_make_buffer_rsrc(
+              (void*)(A + (long long)m0 * lda), (short)0,
+              (int)((long long)(M - m0) * lda * 4 < 0x7fffffff ? (long long)(M - m0) * lda * 4 : 0x7fffffff),
+              0x00020000);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)B, (short)0, (int)((long long)K * ldb * 4), 0x00020000);
     const int arow = 4 * wave + (lane >> 4);               // + 16t
     const int aq = (lane & 15) ^ (arow & 15);              // same for every t
     const unsigned av = (unsigned)(arow * lda + 4 * aq) * 4u;
     const unsigned astep = 16u * lda * 4u;                 // 16 rows per t
+    // CONV: per row t, the byte offset of channel quad aq of tap (0, 0) and the
+    // in-image taps as bits kh*8 + kw (KH, KW <= 8)
+    int cbase[4];
+    unsigned long long cmask[4];
+    if (CONV) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = m0 + arow + 16 * t;
+            cbase[t] = 0;
+            cmask[t] = 0;
+            if (m < M) {
+                const int hw = cv.OH * cv.OW;
+                const int n = m / hw, rem = m - n * hw;
+                const int oh = rem / cv.OW, ow = rem - oh * cv.OW;
+                const int ih0 = oh * cv.stride - cv.pad, iw0 = ow * cv.stride - cv.pad;
+                cbase[t] = ((n * cv.H + ih0) * cv.W + iw0) * cv.Cin * 4 + 16 * aq;
+                unsigned rm = 0, cm = 0;
+                for (int d = 0; d < 8; ++d) {
+                    rm |= ((unsigned)(ih0 + d) < (unsigned)cv.H) ? (1u << d) : 0u;
+                    cm |= ((unsigned)(iw0 + d) < (unsigned)cv.W) ? (1u << d) : 0u;
+                }
+                unsigned long long mk = 0;
+                for (int d = 0; d < 8; ++d)
+                    if ((rm >> d) & 1u) mk |= (unsigned long long)cm << (8 * d);
+                cmask[t] = mk;
+            }
+        }
+    }
     const int brow = 4 * wave + (lane >> 4);               // k row within the chunk, + 16t
     int bq[2];
     bool bok[2];
@@ -78,8 +115,17 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     auto issue = [&](int t, int c, float* st) {            // item t of chunk c into stage st
         const int k0 = c * G32_KC;
         if (t < 4) {
-            unsigned v = av + (unsigned)k0 * 4u + (unsigned)t * astep;
-            if (kragged && k0 + 4 * aq >= K) v = kOOB;
+            unsigned v;
+            if (CONV) {
+                // a 64-channel chunk lies in one tap (Cin % 64 == 0): wave-uniform
+                const int tap = k0 / cv.Cin, ic0 = k0 - tap * cv.Cin;
+                const int kh = tap / cv.KW, kw = tap - kh * cv.KW;
+                const bool ok = (cmask[t] >> (kh * 8 + kw)) & 1ull;
+                v = ok ? (unsigned)(cbase[t] + ((kh * cv.W + kw) * cv.Cin + ic0) * 4) : kOOB;
+            } else {
+                v = av + (unsigned)k0 * 4u + (unsigned)t * astep;
+                if (kragged && k0 + 4 * aq >= K) v = kOOB;
+            }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wave + 4 * t) * 256),
                                                      16, v, 0, 0, 0);
         } else {
@@ -166,15 +212,18 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 
 }  // namespace
 
-bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
-                int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr) {
+namespace {
+template <bool CONV>
+bool launch_gemm32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+                   int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
+                   const G32Conv& cv) {
     if (M <= 0 || N <= 0) return true;
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm32<3>,
+        (void)hipFuncSetAttribute((const void*)k_gemm32<3, CONV>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 3 * G32_STAGE * 4);
-        (void)hipFuncSetAttribute((const void*)k_gemm32<2>,
+        (void)hipFuncSetAttribute((const void*)k_gemm32<2, CONV>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G32_STAGE * 4);
     }
     dim3 grid((unsigned)((N + G32_BN - 1) / G32_BN), (unsigned)((M + G32_BM - 1) / G32_BM));
@@ -187,12 +236,35 @@ bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, in
     const int stages = deep ? 3 : (nch < 2 ? 1 : 2);
     const size_t lds = (size_t)stages * G32_STAGE * 4;
     if (deep)
-        ACFUN_LAUNCH("k_gemm_f32", k_gemm32<3>, grid, dim3(256), lds, s, A, B, C, bias, res, M, N, K,
-                     lda, ldb, ldc, ldr, act);
+        ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<3, CONV>), grid, dim3(256), lds, s, A, B, C, bias, res, M,
+                     N, K, lda, ldb, ldc, ldr, act, cv);
     else
-        ACFUN_LAUNCH("k_gemm_f32", k_gemm32<2>, grid, dim3(256), lds, s, A, B, C, bias, res, M, N, K,
-                     lda, ldb, ldc, ldr, act);
+        ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<2, CONV>), grid, dim3(256), lds, s, A, B, C, bias, res, M,
+                     N, K, lda, ldb, ldc, ldr, act, cv);
     return check_launch("k_gemm32");
+}
+}  // namespace
+
+bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+                int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr) {
+    return launch_gemm32<false>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, G32Conv{});
+}
+
+bool conv32_ok(const ConvShape& g, int Cout, const float* in, const float* w) {
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    const long long M = (long long)g.N * g.OH * g.OW;
+    const long long K = (long long)g.KH * g.KW * g.Cin;
+    return g.Cin % 64 == 0 && g.KH <= 8 && g.KW <= 8 && Cout % 4 == 0 && al(in) && al(w) &&
+           (long long)g.N * g.H * g.W * g.Cin * 4 < 0x7fffffffll && K * Cout * 4 < 0x7fffffffll &&
+           M < (1ll << 31) && (Cout + 63) / 64 < 65536 * 32 && (M + 63) / 64 < 65536;
+}
+
+bool conv32_f32(const ConvShape& g, const float* in, const float* w, const float* bias, int Cout,
+                float* out, int act, hipStream_t s, const float* res, int ldr) {
+    G32Conv cv{g.H, g.W, g.Cin, g.KW, g.stride, g.pad, g.OH, g.OW,
+               (unsigned)((long long)g.N * g.H * g.W * g.Cin * 4)};
+    const int M = g.N * g.OH * g.OW, K = g.KH * g.KW * g.Cin;
+    return launch_gemm32<true>(M, Cout, K, in, g.Cin, w, Cout, out, Cout, bias, act, s, res, ldr, cv);
 }
 
 bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int ldb) {

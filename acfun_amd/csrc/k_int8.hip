@@ -1118,7 +1118,7 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
 
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
-                     const I8Weights* pre) {
+                     const I8Weights* pre, const float* res) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
                       g.W >= 3 && g.Cin >= 4 && Cout >= 4;
@@ -1160,9 +1160,14 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
         I8M p{};
         i8mm_conv(p, q.as<int8_t>(), g, Cinp, bt, ldb, Cout);
         p.act = act; p.scal = scal; p.ws = ws; p.bias = bias; p.Cf = out;
+        p.res = res; p.ldr = Cout;
         if (wino) p.epi = EPI_WINO;
         else { p.epi = EPI_GEMM; p.Sw = sw; }
         return launch_i8mm(p, s);
+    }
+    if (res) {
+        set_error("conv2d_int8: a fused residual needs operands within 32-bit offsets");
+        return false;
     }
     if (!prepared) {
         hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,

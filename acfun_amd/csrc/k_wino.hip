@@ -1120,6 +1120,11 @@ bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin,
     // so the F(4,3) route runs it whenever its staging conditions hold.
     const bool unit23 = Cin % 4 == 0 && ((uintptr_t)in & 15u) == 0 && (W + 1) / 2 >= 6;
     if (tile == 4 && unit23) tile = 2;
+    // Images too narrow for the unit kernel (ResNet's 7 x 7 stage): the
+    // implicit GEMM on the LDS-DMA engine, about 3x faster there than k_wino23
+    // (which pads 7 x 7 to 8 x 8 tiles and fills few workgroups).
+    ConvShape g{N, H, W, Cin, 3, 3, 1, 1, H, W};
+    if (!unit23 && conv32_ok(g, Cout, in, w)) return conv32_f32(g, in, w, bias, Cout, out, act, s);
     return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
 }
 

@@ -368,12 +368,21 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
     // Execution plan: the same arithmetic in fewer passes.
     //  * A ReLU layer that alone consumes a dense conv's output runs in the
     //    conv's epilogue with the layer's own rule (act 2: v < 0 -> 0).
-    //  * An Add that alone consumes the output of a 1x1/s1/p0 fp32 conv runs in
-    //    the GEMM epilogue: v = (acc + bias) + residual, then its ReLU -- the
-    //    same roundings as the separate Add.
+    //  * An Add that alone consumes the output of a 1x1 conv runs in the conv's
+    //    epilogue: v = (conv + bias) + residual, then its ReLU -- the same
+    //    roundings as the separate Add.  fp32: the GEMM engine (any stride when
+    //    Cin is a multiple of 64); int8 models: k_i8mm.
     //  * An Input layer aliases the tensor it names (no copy).
     // A fused or aliasing layer owns no buffer; its tensor is alias[i] (-1 =
     // the model input), kept alive as long as the alias is used.
+    auto in_of = [&](int i) { return i > 0 ? out[i - 1] : Dims{m->inH, m->inW, m->inC}; };
+    auto fusable_add = [&](const AcfunModel* mm, int i, int Cout, int Cin) {
+        const Layer& F = mm->layers[i];
+        if (F.type != 1 || F.p[0] != 1 || F.p[1] != 1 || Cout % 4 != 0) return false;
+        if (mm->int8 && F.wq) return true;
+        if (F.p[3] == 1 && F.p[4] == 0) return Cin % 4 == 0;
+        return Cin % 64 == 0;
+    };
     std::vector<int> alias(L, -2), act_of(L, -1), res_of(L, -3);
     for (int i = 0; i + 1 < L; ++i) {
         const Layer& F = m->layers[i];
@@ -383,9 +392,7 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
             act_of[i] = 2;                           // the separate layer's ReLU rule
             alias[i + 1] = i;
             ++i;
-        } else if (G.type == 8 && F.type == 1 && !(m->int8 && F.wq) && F.p[0] == 1 && F.p[1] == 1 &&
-                   F.p[3] == 1 && F.p[4] == 0 && G.from != i && out[i].C % 4 == 0 && i > 0 &&
-                   m->layers[i - 1].type != 10 && (out[i - 1].C % 4) == 0) {
+        } else if (G.type == 8 && G.from != i && fusable_add(m, i, out[i].C, in_of(i).C)) {
             res_of[i] = G.from;
             act_of[i] = G.p[1] ? 2 : 0;              // k_add_relu's rule: v < 0 -> 0
             alias[i + 1] = i;
@@ -440,16 +447,19 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                 int groups = F.type == 7 ? F.p[5] : 1;
                 const int act = act_of[i] >= 0 ? act_of[i] : F.act;
                 const long long M = (long long)N * in.H * in.W;
-                if (res_of[i] != -3 && M < (1ll << 31) &&
-                    gemm32_ok((int)M, o.C, in.C, x, in.C, F.w, o.C)) {
-                    ok = gemm32_f32((int)M, o.C, in.C, x, in.C, F.w, o.C, y, o.C, F.b, act, s,
-                                    tensor_of(res_of[i]), o.C);
-                } else if (res_of[i] != -3) {
+                const float* res = res_of[i] != -3 ? tensor_of(res_of[i]) : nullptr;
+                ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
+                if (m->int8 && F.type == 1 && F.wq) {
+                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res);
+                } else if (res && F.p[3] == 1 && F.p[4] == 0 && M < (1ll << 31) &&
+                           gemm32_ok((int)M, o.C, in.C, x, in.C, F.w, o.C)) {
+                    ok = gemm32_f32((int)M, o.C, in.C, x, in.C, F.w, o.C, y, o.C, F.b, act, s, res,
+                                    o.C);
+                } else if (res && conv32_ok(g, o.C, x, F.w)) {
+                    ok = conv32_f32(g, x, F.w, F.b, o.C, y, act, s, res, o.C);
+                } else if (res) {
                     set_error("model: residual fusion precondition failed at layer %d", i);
                     return 0;
-                } else if (m->int8 && F.type == 1 && F.wq) {
-                    ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
-                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8);
                 } else {
                     ok = conv2d_route_f32(x, N, in.H, in.W, in.C, F.w, F.b, F.p[0], F.p[1], o.C,
                                           F.p[3], F.p[4], groups > 1 ? groups : 1, y, act, s);

@@ -124,6 +124,11 @@ bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int
 bool gemm32_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
                 int ldc, const float* bias, int act, hipStream_t s, const float* res = nullptr,
                 int ldr = 0);
+// The same engine as an implicit-GEMM convolution (im2col never materialized)
+// when Cin is a multiple of 64 and KH, KW <= 8 (conv32_ok).
+bool conv32_ok(const ConvShape& g, int Cout, const float* in, const float* w);
+bool conv32_f32(const ConvShape& g, const float* in, const float* w, const float* bias, int Cout,
+                float* out, int act, hipStream_t s, const float* res = nullptr, int ldr = 0);
 bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
               int ldc, const float* bias, int act, hipStream_t s);
 bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const float* bias,
@@ -186,9 +191,11 @@ struct I8Weights {
 };
 bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStream_t s);
 void i8_release(I8Weights& w);
+// res (nullable): a residual [pixels][Cout] added before the activation (a
+// model's Add fused into the conv; the same two roundings as a separate Add).
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
-                     const I8Weights* pre = nullptr);
+                     const I8Weights* pre = nullptr, const float* res = nullptr);
 // The int8 Winograd-route entry with caller-supplied scales.
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,
                        const float* ws, const float* bias, int Cout, float s_in, float inv_s,

@@ -85,6 +85,13 @@ CONV_CASES = [
     (1, 112, 112, 64, 3, 3, 64, 1, 1, 1, 5, WINO_TOL),   # F(4,3)
     (1, 113, 115, 64, 3, 3, 72, 1, 1, 1, 5, WINO_TOL),   # F(4,3), ragged tiles
     (2, 10, 10, 256, 3, 3, 256, 1, 1, 2, 3, GEMM_TOL),   # grouped, Cin_per=128 > 64 -> split
+    # Cin a multiple of 64: the implicit GEMM on the LDS-DMA engine (conv32)
+    (2, 15, 15, 64, 1, 1, 40, 2, 0, 1, 4, GEMM_TOL),     # 1x1/2 projection
+    (2, 16, 17, 64, 3, 3, 64, 2, 1, 1, 7, GEMM_TOL),     # 3x3/2
+    (1, 9, 9, 128, 3, 3, 36, 2, 1, 1, 7, GEMM_TOL),      # 3x3/2, ragged M and Cout
+    (1, 12, 11, 64, 5, 5, 32, 1, 2, 1, 7, GEMM_TOL),     # 5x5 pad 2
+    (1, 10, 10, 128, 3, 3, 68, 1, 0, 1, 7, GEMM_TOL),    # 3x3 pad 0, two 64-channel chunks per tap
+    (3, 7, 7, 128, 3, 3, 64, 1, 1, 1, 6, WINO_TOL),      # F(2,3) route on a 7x7 image
 ]
 
 
