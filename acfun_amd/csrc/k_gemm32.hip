@@ -22,6 +22,8 @@
 // contiguous bytes per half-wave row.
 #include "rt.hpp"
 
+#include <cstdlib>
+
 namespace acfun {
 namespace {
 
@@ -29,8 +31,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4g __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void32;
 
-constexpr int G32_BM = 64, G32_BN = 64, G32_KC = 64;
-constexpr int G32_STAGE = 2 * 1024 * 4;           // floats per stage: A + B, 1024 quads each
+constexpr int G32_KC = 64;
 
 // Implicit-GEMM convolution geometry (CONV mode): A is the NHWC input
 // [n][H][W][Cin], row m of the GEMM the output pixel (n, oh, ow), k = tap*Cin + ic.
@@ -39,7 +40,10 @@ struct G32Conv {
     unsigned bytes;    // N*H*W*Cin*4, below 2^31
 };
 
-template <int NST, bool CONV>
+constexpr int g32_stage(int BM, int BN) { return BM * G32_KC + G32_KC * BN; }   // floats
+constexpr int g32_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+template <int BM, int BN, int NST, bool CONV>
 __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 float* __restrict__ C,
@@ -48,15 +52,22 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
                                                 int K, int lda, int ldb, int ldc, int ldr,
                                                 int act, G32Conv cv) {
     constexpr unsigned kOOB = 0x80000000u;
+    constexpr int FM = BM / 64, FN = BN / 64;          // 32 x 32 blocks per wave
+    constexpr int STAGE = g32_stage(BM, BN);
+    constexpr int SB = BM * G32_KC;                     // B's offset in a stage (floats)
+    constexpr int AIT = BM / 16, BIT = BN / 16;         // DMA instructions per wave per chunk
+    constexpr int ITEMS = AIT + BIT;
+    constexpr int BQ = BN / 4;                          // quads per B row
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * G32_BM, n0 = blockIdx.x * G32_BN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nch = (K + G32_KC - 1) / G32_KC;
 
-    // ---- DMA descriptors.  Wave w issues A blocks and B blocks w + 4t
-    // (t = 0..3); lane l of block b covers slot 64b + l = row*16 + quad slot.
+    // ---- DMA descriptors.  A: wave w issues instructions w + 4t (t < AIT),
+    // each 4 rows x 16 quads; lane l -> row 4(w + 4t) + l/16, quad slot l%16.
+    // B: instructions w + 4t (t < BIT), each 64 slots of k rows of BQ quads.
     const __amdgpu_buffer_rsrc_t ares = CONV
         ? __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)cv.bytes, 0x00020000)
         : __builtin_amdgcn_make_buffer_rsrc(
@@ -71,11 +82,11 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     const unsigned astep = 16u * lda * 4u;                 // 16 rows per t
     // CONV: per row t, the byte offset of channel quad aq of tap (0, 0) and the
     // in-image taps as bits kh*8 + kw (KH, KW <= 8)
-    int cbase[4];
-    unsigned long long cmask[4];
+    int cbase[AIT];
+    unsigned long long cmask[AIT];
     if (CONV) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < AIT; ++t) {
             const int m = m0 + arow + 16 * t;
             cbase[t] = 0;
             cmask[t] = 0;
@@ -97,24 +108,23 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
             }
         }
     }
-    const int brow = 4 * wave + (lane >> 4);               // k row within the chunk, + 16t
-    int bq[2];
-    bool bok[2];
-    unsigned bv[2];
+    bool bok[BIT];
+    unsigned bv[BIT];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {                        // t < 2: k < 32; t >= 2: k >= 32
-        bq[hh] = (lane & 15) ^ (hh << 3);
-        bok[hh] = n0 + 4 * bq[hh] < N;
-        bv[hh] = (unsigned)(brow * ldb + n0 + 4 * bq[hh]) * 4u;
+    for (int t = 0; t < BIT; ++t) {
+        const int slot = 64 * (wave + 4 * t) + lane;
+        const int krow = slot / BQ;
+        const int q = (slot % BQ) ^ ((krow & 32) >> 2);    // quad q of k row r at slot q ^ 8[r >= 32]
+        bok[t] = n0 + 4 * q < N;
+        bv[t] = (unsigned)(krow * ldb + n0 + 4 * q) * 4u;
     }
-    const unsigned bstep = 16u * ldb * 4u;
     const bool kragged = (K & (G32_KC - 1)) != 0;
 
     // Every variable part of an address is in the per-lane offset (which the
     // buffer range check covers); the scalar offset stays 0.
     auto issue = [&](int t, int c, float* st) {            // item t of chunk c into stage st
         const int k0 = c * G32_KC;
-        if (t < 4) {
+        if (t < AIT) {
             unsigned v;
             if (CONV) {
                 // a 64-channel chunk lies in one tap (Cin % 64 == 0): wave-uniform
@@ -129,82 +139,128 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wave + 4 * t) * 256),
                                                      16, v, 0, 0, 0);
         } else {
-            const int tt = t - 4, hh = tt >> 1;
-            unsigned v = bok[hh] ? bv[hh] + (unsigned)k0 * ldb * 4u + (unsigned)tt * bstep : kOOB;
+            const int tt = t - AIT;
+            const unsigned v = bok[tt] ? bv[tt] + (unsigned)k0 * ldb * 4u : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                bres, (lds_void32*)(st + 4096 + (wave + 4 * tt) * 256), 16, v, 0, 0, 0);
+                bres, (lds_void32*)(st + SB + (wave + 4 * tt) * 256), 16, v, 0, 0, 0);
         }
     };
 
-    // ---- per-lane read offsets within a stage (floats)
+    // ---- per-lane read offsets within a stage (floats).  MFMA k assignment:
+    // in k-step s of a chunk, lane half h carries k = 32h + s for both operands.
     const int r = lane & 31, h = lane >> 5;
-    const int rowA = 32 * wm + r;
-    int aoff[8];
+    int aoff[FM][8], boff[FN];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) aoff[j] = (rowA * 16 + ((8 * h + j) ^ (rowA & 15))) * 4;
-    const int col = 32 * wn + r;
-    const int boff = 4096 + ((32 * h) * 16 + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
-
-    f16v acc;
+    for (int i = 0; i < FM; ++i) {
+        const int rowA = (BM / 2) * wm + 32 * i + r;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-
-    // Bias and residual of this lane's 16 outputs, loaded first (loads complete
-    // in issue order) so their latency hides behind chunk 0's.
-    const int n = n0 + col;
-    float bn = 0.f, rv[16];
-    if (n < N && bias) bn = bias[n];
+        for (int j = 0; j < 8; ++j) aoff[i][j] = (rowA * 16 + ((8 * h + j) ^ (rowA & 15))) * 4;
+    }
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
-        rv[e] = (res && n < N && m < M) ? res[(long long)m * ldr + n] : 0.f;
+    for (int j = 0; j < FN; ++j) {
+        const int col = (BN / 2) * wn + 32 * j + r;
+        boff[j] = SB + ((32 * h) * BQ + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
     }
 
-    // NST = 3: chunk c+2 is issued while chunk c is multiplied; NST = 2 (two
-    // workgroups per CU): chunk c+1.  NST stages hold min(NST, nch) chunks.
+    f16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    // Bias of this lane's columns, loaded first (loads complete in issue order)
+    // so its latency hides behind chunk 0's.
+    float bn[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = n0 + (BN / 2) * wn + 32 * j + r;
+        bn[j] = (bias && n < N) ? bias[n] : 0.f;
+    }
+    // With one 32 x 32 block per wave the residual is loaded up front as well.
+    constexpr bool PRE = FM * FN == 1;
+    float rv0[16];
+    if (PRE) {
+        const int n = n0 + (BN / 2) * wn + r;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = m0 + (BM / 2) * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+            rv0[e] = (res && n < N && m < M) ? res[(long long)m * ldr + n] : 0.f;
+        }
+    }
+
+    // NST = 3: chunk c+2 is issued while chunk c is multiplied; NST = 2: c+1.
     constexpr int AHEAD = NST - 1;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) issue(t, 0, sm);
+    for (int t = 0; t < ITEMS; ++t) issue(t, 0, sm);
     if (AHEAD == 2 && nch > 1) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) issue(t, 1, sm + G32_STAGE);
+        for (int t = 0; t < ITEMS; ++t) issue(t, 1, sm + STAGE);
     }
 
     int st = 0;
     for (int c = 0; c < nch; ++c) {
-        // outstanding in issue order: ..., chunk c, [chunk c+1] (8 items each)
-        if (AHEAD == 2 && c + 1 < nch) __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8)
-        else __builtin_amdgcn_s_waitcnt(0x0F70);                             // vmcnt(0)
+        // outstanding in issue order: ..., chunk c, [chunk c+1] (ITEMS each)
+        if (AHEAD == 2 && c + 1 < nch) __builtin_amdgcn_s_waitcnt(g32_vmcnt(ITEMS));
+        else __builtin_amdgcn_s_waitcnt(g32_vmcnt(0));
         // LDS-only workgroup barrier: this wave's LDS reads are complete;
         // the loads of later chunks stay in flight.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const float* S = sm + st * G32_STAGE;
+        const float* S = sm + st * STAGE;
         const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
-        float* NA = sm + sta * G32_STAGE;
+        float* NA = sm + sta * STAGE;
         const bool more = c + AHEAD < nch;
-        f4g a[8];
+        f4g a[FM][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = *(const f4g*)&S[aoff[j]];
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[i][j] = *(const f4g*)&S[aoff[i][j]];
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
-            const float b = S[boff + s * 64];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b, acc, 0, 0, 0);
-            if ((s & 3) == 3 && more) issue(s >> 2, c + AHEAD, NA);
+            float b[FN];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = S[boff[j] + s * BN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j], acc[i][j],
+                                                                     0, 0, 0);
+            if (more) {
+#pragma unroll
+                for (int t = s * ITEMS / 32; t < (s + 1) * ITEMS / 32; ++t) issue(t, c + AHEAD, NA);
+            }
         }
         st = AHEAD == 2 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
     }
 
-    // ---- epilogue: lane l, register e <-> row 8*(e/4) + 4*(l/32) + e%4, column l%32
-    if (n < N) {
+    // ---- epilogue: lane l, register e of block (i, j) <->
+    //      row m0 + BM/2*wm + 32i + 8*(e/4) + 4*(l/32) + e%4, column n0 + BN/2*wn + 32j + l%32
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int m = m0 + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (m < M) {
-                float v = acc[e];
-                if (bias) v = v + bn;
-                if (res) v = v + rv[e];                   // fused residual Add
-                v = act_apply(v, act);
-                C[(long long)m * ldc + n] = v;
+    for (int j = 0; j < FN; ++j) {
+        const int n = n0 + (BN / 2) * wn + 32 * j + r;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            float rv[16];
+            if (res && !PRE) {                            // all 16 loads in flight at once
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                    rv[e] = m < M ? res[(long long)m * ldr + n] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (m < M) {
+                    float v = acc[i][j][e];
+                    if (bias) v = v + bn[j];
+                    if (res) v = v + (PRE ? rv0[e] : rv[e]);   // fused residual Add
+                    v = act_apply(v, act);
+                    C[(long long)m * ldc + n] = v;
+                }
             }
         }
     }
@@ -213,35 +269,67 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 }  // namespace
 
 namespace {
+struct G32Tile { int bm, bn, nst; };
+
+// Tile choice.  Measured on MI355X (config 1 and the ResNet-50 batch-64
+// layers): 64 x 64 tiles, two or three workgroups per CU, beat the 128-row
+// tiles at every K, since one workgroup per CU leaves the DMA latency and the
+// epilogue exposed.  ACFUN_G32_KMIN=<K> enables the larger tiles from that K
+// (sweeps).  Three stages when the 64 x 64 grid is a single wave of workgroups.
+G32Tile pick_g32(int M, int N, int K) {
+    const long long cus = num_cus();
+    const int nch = (K + G32_KC - 1) / G32_KC;
+    auto tiles = [&](int bm, int bn) {
+        return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    };
+    // ACFUN_G32_KMIN: the K from which the larger tiles are used (sweeps)
+    static int kmin = -1;
+    if (kmin < 0) {
+        const char* e = getenv("ACFUN_G32_KMIN");
+        kmin = e ? atoi(e) : 0x7fffffff;
+    }
+    if (K >= kmin && N > 64 && tiles(128, 128) >= cus) return G32Tile{128, 128, 2};
+    if (K >= kmin && tiles(128, 64) >= cus) return G32Tile{128, 64, nch > 2 ? 3 : 2};
+    const bool deep = nch > 2 && tiles(64, 64) < 2 * cus;
+    return G32Tile{64, 64, deep ? 3 : 2};
+}
+
+template <int BM, int BN, int NST, bool CONV>
+bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
+                int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
+                const G32Conv& cv) {
+    const int nch = (K + G32_KC - 1) / G32_KC;
+    // LDS holds only the stages that can be in use
+    const int stages = nch < NST ? (nch < 1 ? 1 : nch) : NST;
+    const size_t lds = (size_t)stages * g32_stage(BM, BN) * 4;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  NST * g32_stage(BM, BN) * 4);
+    }
+    dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+    ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<BM, BN, NST, CONV>), grid, dim3(256), lds, s, A, B, C, bias,
+                 res, M, N, K, lda, ldb, ldc, ldr, act, cv);
+    return check_launch("k_gemm32");
+}
+
 template <bool CONV>
 bool launch_gemm32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
                    int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
                    const G32Conv& cv) {
     if (M <= 0 || N <= 0) return true;
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm32<3, CONV>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 3 * G32_STAGE * 4);
-        (void)hipFuncSetAttribute((const void*)k_gemm32<2, CONV>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 2 * G32_STAGE * 4);
-    }
-    dim3 grid((unsigned)((N + G32_BN - 1) / G32_BN), (unsigned)((M + G32_BM - 1) / G32_BM));
-    const int nch = (K + G32_KC - 1) / G32_KC;
-    const long long tiles = (long long)grid.x * grid.y;
-    // Three stages (one workgroup per CU) only pay when the grid is a single
-    // wave of workgroups; otherwise two stages let two workgroups share a CU.
-    // LDS holds only the stages that can be in use.
-    const bool deep = nch > 2 && tiles < 2ll * num_cus();
-    const int stages = deep ? 3 : (nch < 2 ? 1 : 2);
-    const size_t lds = (size_t)stages * G32_STAGE * 4;
-    if (deep)
-        ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<3, CONV>), grid, dim3(256), lds, s, A, B, C, bias, res, M,
-                     N, K, lda, ldb, ldc, ldr, act, cv);
-    else
-        ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<2, CONV>), grid, dim3(256), lds, s, A, B, C, bias, res, M,
-                     N, K, lda, ldb, ldc, ldr, act, cv);
-    return check_launch("k_gemm32");
+    const G32Tile t = pick_g32(M, N, K);
+    if (t.bm == 128 && t.bn == 128)
+        return launch_g32<128, 128, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    if (t.bm == 128 && t.nst == 3)
+        return launch_g32<128, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    if (t.bm == 128)
+        return launch_g32<128, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    if (t.nst == 3)
+        return launch_g32<64, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    return launch_g32<64, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
 }
 }  // namespace
 
