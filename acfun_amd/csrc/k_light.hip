@@ -18,6 +18,7 @@ namespace acfun {
 namespace {
 
 __device__ __forceinline__ float vmax(float a, float b) { return a > b ? a : b; }  // max_ps
+typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Depthwise conv: weights [C][KH][KW]; act==1 -> ReLU (max_ps semantics).
 __global__ void k_dwconv(const float* __restrict__ in, int N, int H, int W, int C,
@@ -286,6 +287,128 @@ __global__ void k_gconv(const float* __restrict__ in, int N, int H, int W, int C
     out[idx] = s;
 }
 
+// k_gconv for Cin_p and Cout_p multiples of 4 with the all-FMA rule
+// (Cout_p >= 8): a lane owns one output pixel x 4 consecutive output channels
+// of one group.  Per in-range tap it loads the group's Cin_p input channels
+// as 16-byte quads and, per input channel, the 4 weights as one quad; each
+// output keeps the reference's order (bias, then taps kh-major, then input
+// channels, one fmaf each).  Lanes run channel-quad fastest, so a wave's
+// stores cover whole output pixels.
+__global__ __launch_bounds__(256) void k_gconv4(const float* __restrict__ in, int N, int H, int W,
+                                                int Cin, const float* __restrict__ w,
+                                                const float* __restrict__ bias, int KH, int KW,
+                                                int Cout, int stride, int pad, int groups, int OH,
+                                                int OW, float* __restrict__ out, int act,
+                                                int vec_end) {
+    const int cq = Cout >> 2;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)N * OH * OW * cq;
+    if (idx >= total) return;
+    const int q = (int)(idx % cq);
+    long long p = idx / cq;
+    const int ow = (int)(p % OW);
+    p /= OW;
+    const int oh = (int)(p % OH);
+    const int n = (int)(p / OH);
+    const int Cin_p = Cin / groups, Cout_p = Cout / groups;
+    const int co = 4 * q;
+    const int g = co / Cout_p, oc = co - g * Cout_p;
+    const float* wg = w + (long long)g * Cout_p * KH * KW * Cin_p + oc;
+    f4 s = {0.f, 0.f, 0.f, 0.f};
+    if (bias) s = *(const f4*)(bias + co);
+    for (int kh = 0; kh < KH; ++kh) {
+        const int ih = oh * stride - pad + kh;
+        if (ih < 0 || ih >= H) continue;
+        for (int kw = 0; kw < KW; ++kw) {
+            const int iw = ow * stride - pad + kw;
+            if (iw < 0 || iw >= W) continue;
+            const float* px = in + (((long long)n * H + ih) * W + iw) * Cin + (long long)g * Cin_p;
+            const float* wp = wg + (long long)((kh * KW + kw) * Cin_p) * Cout_p;
+            for (int i4 = 0; i4 < Cin_p; i4 += 4) {
+                const f4 x = *(const f4*)(px + i4);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const f4 wv = *(const f4*)(wp + (long long)(i4 + u) * Cout_p);
+                    s.x = fmaf(x[u], wv.x, s.x);
+                    s.y = fmaf(x[u], wv.y, s.y);
+                    s.z = fmaf(x[u], wv.z, s.z);
+                    s.w = fmaf(x[u], wv.w, s.w);
+                }
+            }
+        }
+    }
+    if (act == 1) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (oc + u < vec_end) s[u] = vmax(s[u], 0.0f);
+            else if (s[u] < 0.0f) s[u] = 0.0f;
+        }
+    }
+    *(f4*)(out + (((long long)n * OH + oh) * OW + ow) * Cout + co) = s;
+}
+
+// k_gconv4 for 3x3 kernels and Cin_p = 4*CINQ: every load of the lane (the
+// in-image taps' input quads and all weight quads) is issued before the first
+// fmaf, so the lane waits for memory once instead of once per tap.  Taps
+// outside the image are skipped (not multiplied by zero), as in the reference.
+template <int CINQ>
+__global__ __launch_bounds__(256) void k_gconv4_3x3(const float* __restrict__ in, int N, int H,
+                                                    int W, int Cin, const float* __restrict__ w,
+                                                    const float* __restrict__ bias, int Cout,
+                                                    int stride, int pad, int groups, int OH, int OW,
+                                                    float* __restrict__ out, int act, int vec_end) {
+    constexpr int CP = 4 * CINQ;
+    const int cq = Cout >> 2;
+    // 32-bit index math (the launcher checks N*OH*OW*Cout/4 < 2^31)
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= N * OH * OW * cq) return;
+    const int q = idx % cq;
+    int p = idx / cq;
+    const int ow = p % OW;
+    p /= OW;
+    const int oh = p % OH;
+    const int n = p / OH;
+    const int Cout_p = Cout / groups;
+    const int co = 4 * q;
+    const int g = co / Cout_p, oc = co - g * Cout_p;
+    const float* wg = w + (long long)g * Cout_p * 9 * CP + oc;
+    const float* img = in + (long long)n * H * W * Cin + (long long)g * CP;
+    f4 x[9][CINQ], wv[9][CP];
+    bool ok[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        const int ih = oh * stride - pad + t / 3, iw = ow * stride - pad + t % 3;
+        ok[t] = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+        const float* px = img + ((long long)(ok[t] ? ih : 0) * W + (ok[t] ? iw : 0)) * Cin;
+#pragma unroll
+        for (int c = 0; c < CINQ; ++c) x[t][c] = *(const f4*)(px + 4 * c);
+#pragma unroll
+        for (int i = 0; i < CP; ++i) wv[t][i] = *(const f4*)(wg + (long long)(t * CP + i) * Cout_p);
+    }
+    f4 s = {0.f, 0.f, 0.f, 0.f};
+    if (bias) s = *(const f4*)(bias + co);
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        if (!ok[t]) continue;
+#pragma unroll
+        for (int i = 0; i < CP; ++i) {
+            const float xi = x[t][i >> 2][i & 3];
+            s.x = fmaf(xi, wv[t][i].x, s.x);
+            s.y = fmaf(xi, wv[t][i].y, s.y);
+            s.z = fmaf(xi, wv[t][i].z, s.z);
+            s.w = fmaf(xi, wv[t][i].w, s.w);
+        }
+    }
+    if (act == 1) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (oc + u < vec_end) s[u] = vmax(s[u], 0.0f);
+            else if (s[u] < 0.0f) s[u] = 0.0f;
+        }
+    }
+    *(f4*)(out + (((long long)n * OH + oh) * OW + ow) * Cout + co) = s;
+}
+
 // MaxPool: channels below vec_end use max_ps semantics, the rest the scalar
 // compare of src/layers.cpp:221-246 (they differ only for NaN / signed zero).
 __global__ void k_maxpool(const float* __restrict__ in, int N, int H, int W, int C, int pool,
@@ -461,6 +584,24 @@ bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, co
     // >=8 -> AVX2 kernel (vector part + contracted scalar tail), else scalar.
     int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
     int fma_all = Cout_p >= 8 ? 1 : 0;
+    const int Cin_p = Cin / groups;
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    if (fma_all && Cin_p % 4 == 0 && Cout_p % 4 == 0 && al(in) && al(w) && al(out) &&
+        (!bias || al(bias))) {
+        const long long total4 = (long long)N * OH * OW * (Cout / 4);
+        if (KH == 3 && KW == 3 && (Cin_p == 4 || Cin_p == 8) && total4 < (1ll << 31)) {
+            if (Cin_p == 4)
+                ACFUN_LAUNCH("k_gconv", k_gconv4_3x3<1>, grid1d(total4), dim3(256), 0, s, in, N, H, W, Cin,
+                             w, bias, Cout, stride, pad, groups, OH, OW, out, act, vec_end);
+            else
+                ACFUN_LAUNCH("k_gconv", k_gconv4_3x3<2>, grid1d(total4), dim3(256), 0, s, in, N, H, W, Cin,
+                             w, bias, Cout, stride, pad, groups, OH, OW, out, act, vec_end);
+            return check_launch("k_gconv4_3x3");
+        }
+        ACFUN_LAUNCH("k_gconv", k_gconv4, grid1d(total4), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH,
+                     KW, Cout, stride, pad, groups, OH, OW, out, act, vec_end);
+        return check_launch("k_gconv4");
+    }
     long long total = (long long)N * OH * OW * Cout;
     ACFUN_LAUNCH("k_gconv", k_gconv, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w, bias, KH, KW,
                        Cout, stride, pad, groups, OH, OW, out, act, vec_end, fma_all);

@@ -156,14 +156,16 @@ def test_depthwise_exact(gpu, rng, N, H, W, C, K, st, pd, act):
 @pytest.mark.parametrize("Cin,Cout,g", [(24, 48, 6), (12, 24, 3), (32, 48, 4), (12, 36, 3),
                                         (48, 96, 2), (6, 12, 3), (16, 128, 4)])
 @pytest.mark.parametrize("act", [0, 1])
-def test_grouped_exact(gpu, rng, Cin, Cout, g, act):
+@pytest.mark.parametrize("st", [1, 2])
+def test_grouped_exact(gpu, rng, Cin, Cout, g, act, st):
     N, H, W = 2, 9, 10
     x = rng.standard_normal((N, H, W, Cin)).astype(np.float32)
     w = (rng.standard_normal((g, 9 * (Cin // g), Cout // g)) * 0.3).astype(np.float32)
     b = rng.standard_normal(Cout).astype(np.float32)
-    got = np.zeros((N, H, W, Cout), np.float32)
-    gpu.acfun_conv2d_g(P(x), N, H, W, Cin, P(w), P(b), 3, 3, Cout, 1, 1, g, P(got), act)
-    assert_bitexact(got, oracle.conv2d_grouped(x, w, b, 3, 3, Cout, 1, 1, g, act), "grouped")
+    OH, OW = oracle.out_hw(H, W, 3, 3, st, 1)
+    got = np.zeros((N, OH, OW, Cout), np.float32)
+    gpu.acfun_conv2d_g(P(x), N, H, W, Cin, P(w), P(b), 3, 3, Cout, st, 1, g, P(got), act)
+    assert_bitexact(got, oracle.conv2d_grouped(x, w, b, 3, 3, Cout, st, 1, g, act), "grouped")
 
 
 @pytest.mark.parametrize("C", [5, 12, 16, 20, 96])
