@@ -62,7 +62,19 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // Tile order: the 1-D grid is cut into 8 contiguous runs, one per XCD
+    // (workgroup id mod 8), and within a run tiles go in groups of 4 tile rows,
+    // column-major inside a group -- so the workgroups one XCD runs at a time
+    // cover a compact patch and their A rows and B columns share its L2.
+    const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM, total = gm * gn;
+    int L = blockIdx.x;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    constexpr int GRP = 4;
+    const int grp = L / (GRP * gn), gbase = grp * GRP;
+    const int rows = gm - gbase < GRP ? gm - gbase : GRP;
+    const int r_in = L - grp * GRP * gn;
+    const int tm = gbase + r_in % rows, tn = r_in / rows;
+    const int m0 = tm * BM, n0 = tn * BN;
     const int nch = (K + G32_KC - 1) / G32_KC;
 
     // ---- DMA descriptors.  A: wave w issues instructions w + 4t (t < AIT),
@@ -199,40 +211,79 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
         for (int t = 0; t < ITEMS; ++t) issue(t, 1, sm + STAGE);
     }
 
-    int st = 0;
-    for (int c = 0; c < nch; ++c) {
+    // Software pipeline per chunk c (operands in registers):
+    //   MFMAs of k-steps 0..27 (the DMA of chunk c+AHEAD issued between them);
+    //   the last four k-steps' operands set aside;
+    //   wait for chunk c+1's DMA, LDS-only barrier, LDS reads of all of chunk
+    //   c+1's operands;
+    //   MFMAs of k-steps 28..31 of chunk c, which cover the barrier and the
+    //   LDS latency of the reads.
+    // The barrier before chunk c+1's reads also orders every wave's reads of
+    // chunk c-1's stage before the DMA of chunk c+AHEAD overwrites it.
+    constexpr int DEFER = 4;
+    f4g a[FM][8];
+    float bb[FN][32];
+    auto wait_chunk = [&](int c) {            // chunk c's DMA has landed (everyone's)
         // outstanding in issue order: ..., chunk c, [chunk c+1] (ITEMS each)
         if (AHEAD == 2 && c + 1 < nch) __builtin_amdgcn_s_waitcnt(g32_vmcnt(ITEMS));
         else __builtin_amdgcn_s_waitcnt(g32_vmcnt(0));
-        // LDS-only workgroup barrier: this wave's LDS reads are complete;
-        // the loads of later chunks stay in flight.
+        // LDS-only workgroup barrier: this wave's LDS reads are complete; the
+        // loads of later chunks stay in flight.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const float* S = sm + st * STAGE;
-        const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
-        float* NA = sm + sta * STAGE;
-        const bool more = c + AHEAD < nch;
-        f4g a[FM][8];
+    };
+    auto read_chunk = [&](const float* S) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j) a[i][j] = *(const f4g*)&S[aoff[i][j]];
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            float b[FN];
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int j = 0; j < FN; ++j) b[j] = S[boff[j] + s * BN];
+            for (int s = 0; s < 32; ++s) bb[j][s] = S[boff[j] + s * BN];
+    };
+    if (nch > 0) {
+        wait_chunk(0);
+        read_chunk(sm);
+    }
+    int st = 0;
+    for (int c = 0; c < nch; ++c) {
+        const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
+        float* NA = sm + sta * STAGE;
+        const bool more = c + AHEAD < nch;
+#pragma unroll
+        for (int s = 0; s < 32 - DEFER; ++s) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j], acc[i][j],
-                                                                     0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], bb[j][s],
+                                                                     acc[i][j], 0, 0, 0);
             if (more) {
 #pragma unroll
-                for (int t = s * ITEMS / 32; t < (s + 1) * ITEMS / 32; ++t) issue(t, c + AHEAD, NA);
+                for (int t = s * ITEMS / (32 - DEFER); t < (s + 1) * ITEMS / (32 - DEFER); ++t)
+                    issue(t, c + AHEAD, NA);
             }
         }
+        f4g al[FM];
+        float bl[FN][DEFER];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) al[i] = a[i][7];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int u = 0; u < DEFER; ++u) bl[j][u] = bb[j][32 - DEFER + u];
         st = AHEAD == 2 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
+        if (c + 1 < nch) {
+            wait_chunk(c + 1);
+            read_chunk(sm + st * STAGE);
+        }
+#pragma unroll
+        for (int u = 0; u < DEFER; ++u)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(al[i][u], bl[j][u], acc[i][j], 0, 0, 0);
     }
 
     // ---- epilogue: lane l, register e of block (i, j) <->
@@ -309,7 +360,7 @@ bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, in
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   NST * g32_stage(BM, BN) * 4);
     }
-    dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+    dim3 grid((unsigned)(((N + BN - 1) / BN) * ((M + BM - 1) / BM)));
     ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<BM, BN, NST, CONV>), grid, dim3(256), lds, s, A, B, C, bias,
                  res, M, N, K, lda, ldb, ldc, ldr, act, cv);
     return check_launch("k_gemm32");
@@ -344,7 +395,7 @@ bool conv32_ok(const ConvShape& g, int Cout, const float* in, const float* w) {
     const long long K = (long long)g.KH * g.KW * g.Cin;
     return g.Cin % 64 == 0 && g.KH <= 8 && g.KW <= 8 && Cout % 4 == 0 && al(in) && al(w) &&
            (long long)g.N * g.H * g.W * g.Cin * 4 < 0x7fffffffll && K * Cout * 4 < 0x7fffffffll &&
-           M < (1ll << 31) && (Cout + 63) / 64 < 65536 * 32 && (M + 63) / 64 < 65536;
+           M < (1ll << 31) && (long long)((Cout + 63) / 64) * ((M + 63) / 64) < 0x7fffffffll;
 }
 
 bool conv32_f32(const ConvShape& g, const float* in, const float* w, const float* bias, int Cout,
@@ -359,8 +410,8 @@ bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int
     auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
     return K > 0 && K % 4 == 0 && N % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && al(A) && al(B) &&
            (long long)K * ldb * 4 < 0x7fffffffll && (long long)(M + 64) * lda * 4 < (1ll << 40) &&
-           (long long)lda * 16 * 4 < 0x7fffffffll && (N + 63) / 64 < 65536 * 32 &&
-           (M + 63) / 64 < 65536;
+           (long long)lda * 16 * 4 < 0x7fffffffll &&
+           (long long)((N + 63) / 64) * ((M + 63) / 64) < 0x7fffffffll;
 }
 
 }  // namespace acfun
