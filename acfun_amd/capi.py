@@ -63,6 +63,7 @@ SIGNATURES = {
     "acfun_last_error": (_s, []),
     "acfun_sync": (_i, []),
     "acfun_dev_gemm_epi": (_i, [_i, _i, _i, _p, _p, _p, _p, _i, _p]),
+    "acfun_dev_gemm_bf16": (_i, [_i, _i, _i, _p, _p, _p, _p]),
     "acfun_dev_conv2d": (_i, [_p, _i, _i, _i, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "acfun_dev_conv2d_int8": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i,
                                    _p]),

@@ -162,12 +162,7 @@ void acfun_gemm_bf16(int M, int N, int K, const float* A, const float* B, float*
         auto dB = (const float*)hc.in(B, F((long long)K * N));
         auto dC = (float*)hc.out(C, F((long long)M * N));
         if (hc.failed()) return false;
-        Scratch a16(F((long long)M * K), hc.stream()), b16(F((long long)K * N), hc.stream());
-        if ((M * (long long)K && !a16.p) || (K * (long long)N && !b16.p)) return false;
-        return round_bf16(dA, a16.as<float>(), (size_t)M * K, hc.stream()) &&
-               round_bf16(dB, b16.as<float>(), (size_t)K * N, hc.stream()) &&
-               gemm_f32(M, N, K, a16.as<float>(), K, b16.as<float>(), N, dC, N, nullptr, 0,
-                        hc.stream());
+        return gemm_bf16_dev(M, N, K, dA, dB, dC, hc.stream());
     });
 }
 
@@ -461,6 +456,13 @@ int acfun_dev_gemm_epi(int M, int N, int K, const float* A, const float* B, floa
     if (!ensure_device()) return -1;
     if (M <= 0 || N <= 0 || K < 0) return 0;
     return gemm_f32(M, N, K, A, K, B, N, C, N, bias, act, resolve(stream)) ? 0 : -1;
+}
+
+int acfun_dev_gemm_bf16(int M, int N, int K, const float* A, const float* B, float* C,
+                        void* stream) {
+    if (!ensure_device()) return -1;
+    if (M <= 0 || N <= 0 || K < 0) return 0;
+    return gemm_bf16_dev(M, N, K, A, B, C, resolve(stream)) ? 0 : -1;
 }
 
 int acfun_dev_conv2d(const float* input, int N, int H, int W, int Cin, const float* weight,

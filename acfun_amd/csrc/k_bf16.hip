@@ -1,0 +1,210 @@
+// k_bf16.hip -- acfun_gemm_bf16 on bf16 MFMA.
+//
+// Replaces the reference's AVX-512 BF16 path (src/gemm_bf16_avx512.cpp): A and
+// B are rounded to bf16 (round to nearest even on bit 16, :37-44) and the
+// products accumulate in fp32.  Products of two bf16 values are exact in fp32,
+// so the result differs from the reference only by the fp32 accumulation
+// order.
+//
+// Two packing kernels write the rounded operands k-contiguous -- A as
+// [M][Kp], B transposed as [N][Kp], Kp = K rounded up to 64, zeros beyond K --
+// and k_bf16mm multiplies them on v_mfma_f32_32x32x16_bf16.  Its staging is
+// the int8 kernel's: 64 x 64 tiles, 2 x 2 waves, K in chunks of 128 bytes
+// (64 bf16) DMA'd into LDS by buffer_load_dwordx4 ... lds, quad q of row r at
+// slot r*8 + (q ^ swz(r)), three stages.  In k-step s lane half h reads quad
+// 2s+h of its A row and its B row: eight bf16 each, the MFMA's 16 k per step.
+#include "rt.hpp"
+
+namespace acfun {
+namespace {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// fp32 -> bf16 bits: round to nearest even on bit 16 for finite values, NaN kept quiet.
+__device__ __forceinline__ unsigned bf16_bits(float f) {
+    unsigned u = __float_as_uint(f);
+    if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
+    else if (u & 0x007fffffu) u |= 0x00400000u;
+    return u >> 16;
+}
+
+// One lane: 8 consecutive k of one row of A -> one 16-byte store.
+__global__ __launch_bounds__(256) void k_pack_a_bf16(const float* __restrict__ A, int M, int K,
+                                                     int lda, unsigned short* __restrict__ Ab,
+                                                     int Kp) {
+    const int kq = Kp >> 3;
+    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (long long)M * kq) return;
+    const int m = (int)(t / kq), k0 = (int)(t - (long long)m * kq) * 8;
+    const float* src = A + (long long)m * lda + k0;
+    unsigned w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int k = k0 + 2 * p;
+        const unsigned lo = k < K ? bf16_bits(src[2 * p]) : 0u;
+        const unsigned hi = k + 1 < K ? bf16_bits(src[2 * p + 1]) : 0u;
+        w[p] = lo | (hi << 16);
+    }
+    *(i4v*)(Ab + (long long)m * Kp + k0) = i4v{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// One lane: column n, 8 consecutive k of B -> one 16-byte store into Bt[n][k0..].
+// Lanes run n fastest, so each of the 8 loads is a coalesced row segment.
+__global__ __launch_bounds__(256) void k_pack_bt_bf16(const float* __restrict__ B, int K, int N,
+                                                      int ldb, unsigned short* __restrict__ Bt,
+                                                      int Kp) {
+    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (long long)N * (Kp >> 3)) return;
+    const int kb = (int)(t / N), n = (int)(t - (long long)kb * N);
+    const int k0 = kb * 8;
+    unsigned w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int k = k0 + 2 * p;
+        const unsigned lo = k < K ? bf16_bits(B[(long long)k * ldb + n]) : 0u;
+        const unsigned hi = k + 1 < K ? bf16_bits(B[(long long)(k + 1) * ldb + n]) : 0u;
+        w[p] = lo | (hi << 16);
+    }
+    *(i4v*)(Bt + (long long)n * Kp + k0) = i4v{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+__device__ __forceinline__ int bswz(int r) { return (r ^ (r >> 3)) & 7; }
+
+constexpr int BF_BM = 64, BF_BN = 64, BF_NST = 3;
+constexpr int BF_SA = BF_BM * 128, BF_STG = (BF_BM + BF_BN) * 128;
+
+__global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict__ Ab,
+                                                const unsigned short* __restrict__ Bt,
+                                                float* __restrict__ C, int M, int N, int Kp,
+                                                int ldc, unsigned a_bytes, unsigned b_bytes) {
+    constexpr int AIT = BF_BM / 32, BIT = BF_BN / 32, ITEMS = AIT + BIT;
+    constexpr int AHEAD = BF_NST - 1;
+    constexpr unsigned kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smb[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    // XCD-contiguous tile order (workgroup id mod 8 = XCD)
+    const int gn = (N + BF_BN - 1) / BF_BN, total = gn * ((M + BF_BM - 1) / BF_BM);
+    int L = blockIdx.x;
+    if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+    const int m0 = (L / gn) * BF_BM, n0 = (L % gn) * BF_BN;
+    const int nch = Kp >> 6;
+    const __amdgpu_buffer_rsrc_t ares =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, (int)a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Bt, (short)0, (int)b_bytes, 0x00020000);
+    // DMA rows of this lane: row 8*(wave + 4t) + lane/8, quad slot lane%8
+    const int sl = lane & 7, rl = lane >> 3;
+    unsigned av[AIT], bv[BIT];
+#pragma unroll
+    for (int t = 0; t < AIT; ++t) {
+        const int row = 8 * (wave + 4 * t) + rl, q = sl ^ bswz(row);
+        av[t] = m0 + row < M ? (unsigned)((m0 + row) * Kp * 2 + 16 * q) : kOOB;
+    }
+#pragma unroll
+    for (int t = 0; t < BIT; ++t) {
+        const int row = 8 * (wave + 4 * t) + rl, q = sl ^ bswz(row);
+        bv[t] = n0 + row < N ? (unsigned)((n0 + row) * Kp * 2 + 16 * q) : kOOB;
+    }
+    auto issue = [&](int t, int c, char* st) {
+        if (t < AIT) {
+            const unsigned v = av[t] + (unsigned)(c << 7);   // kOOB + k stays out of range
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(st + (wave + 4 * t) * 1024), 16,
+                                                     v, 0, 0, 0);
+        } else {
+            const int tt = t - AIT;
+            const unsigned v = bv[tt] + (unsigned)(c << 7);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(st + BF_SA + (wave + 4 * tt) * 1024),
+                                                     16, v, 0, 0, 0);
+        }
+    };
+    // LDS read offsets (bytes within a stage) per k-step
+    const int r32 = lane & 31, hq = lane >> 5;
+    const int ra = wm * 32 + r32, rb = wn * 32 + r32;
+    int rda[4], rdb[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        rda[s] = ra * 128 + 16 * ((2 * s + hq) ^ bswz(ra));
+        rdb[s] = BF_SA + rb * 128 + 16 * ((2 * s + hq) ^ bswz(rb));
+    }
+    f16v acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+#pragma unroll
+    for (int a = 0; a < AHEAD; ++a)
+        if (a < nch) {
+#pragma unroll
+            for (int t = 0; t < ITEMS; ++t) issue(t, a, smb + a * BF_STG);
+        }
+    int st = 0;
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt((ITEMS & 15) | 0x0F70);   // vmcnt(ITEMS)
+        else __builtin_amdgcn_s_waitcnt(0x0F70);                               // vmcnt(0)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const char* S = smb + st * BF_STG;
+        char* NA = smb + (st == 0 ? BF_NST - 1 : st - 1) * BF_STG;
+        const bool more = c + AHEAD < nch;
+        i4v fa[4], fb[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            fa[s] = *(const i4v*)(S + rda[s]);
+            fb[s] = *(const i4v*)(S + rdb[s]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, fa[s]),
+                                                          __builtin_bit_cast(bf8, fb[s]), acc, 0, 0, 0);
+            if (more) {
+#pragma unroll
+                for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, c + AHEAD, NA);
+            }
+        }
+        st = st == BF_NST - 1 ? 0 : st + 1;
+    }
+    // epilogue: lane l, register e <-> row m0 + 32wm + 8(e/4) + 4(l/32) + e%4, column n0 + 32wn + l%32
+    const int n = n0 + wn * 32 + r32;
+    if (n >= N) return;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * 32 + 8 * (e >> 2) + 4 * hq + (e & 3);
+        if (m < M) C[(long long)m * ldc + n] = acc[e];
+    }
+}
+
+}  // namespace
+
+bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C, hipStream_t s) {
+    if (M <= 0 || N <= 0) return true;
+    const int Kp = K <= 0 ? 64 : (K + 63) / 64 * 64;
+    if ((long long)M * Kp * 2 >= 0x7fffffffll || (long long)N * Kp * 2 >= 0x7fffffffll) {
+        set_error("acfun_gemm_bf16: operands beyond 2 GB");
+        return false;
+    }
+    Scratch ab((size_t)M * Kp * 2, s), bt((size_t)N * Kp * 2, s);
+    if (!ab.p || !bt.p) return false;
+    const long long na = (long long)M * (Kp / 8), nb = (long long)N * (Kp / 8);
+    hipLaunchKernelGGL(k_pack_a_bf16, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, A, M, K, K,
+                       ab.as<unsigned short>(), Kp);
+    if (!check_launch("k_pack_a_bf16")) return false;
+    hipLaunchKernelGGL(k_pack_bt_bf16, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, B, K, N, N,
+                       bt.as<unsigned short>(), Kp);
+    if (!check_launch("k_pack_bt_bf16")) return false;
+    static bool attr = false;
+    constexpr int lds = BF_NST * BF_STG;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_bf16mm, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    }
+    const long long tiles = (long long)((M + BF_BM - 1) / BF_BM) * ((N + BF_BN - 1) / BF_BN);
+    ACFUN_LAUNCH("k_bf16mm", k_bf16mm, dim3((unsigned)tiles), dim3(256), lds, s, ab.as<unsigned short>(),
+                 bt.as<unsigned short>(), C, M, N, Kp, N, (unsigned)((long long)M * Kp * 2),
+                 (unsigned)((long long)N * Kp * 2));
+    return check_launch("k_bf16mm");
+}
+
+}  // namespace acfun

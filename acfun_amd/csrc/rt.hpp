@@ -138,6 +138,8 @@ bool gemm_f32_batched(int batch, int M, int N, int K, const float* A, long long 
                       const float* B, long long sB, int ldb, float* C, long long sC, int ldc,
                       hipStream_t s);
 bool round_bf16(const float* in, float* out, size_t n, hipStream_t s);
+// acfun_gemm_bf16 on bf16 MFMA (k_bf16.hip): C = bf16(A) * bf16(B), fp32 accumulation.
+bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C, hipStream_t s);
 
 // Winograd 3x3/s1/p1 (tile = 2 for F(2,3), 4 for F(4,3)).
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,

@@ -206,6 +206,17 @@ def main():
                                      "frac_fp32_peak": round(f / PEAK_FP32, 4),
                                      "kernel_ms": {"k_gemm_f32": k}}
 
+        # acfun_gemm_bf16 at 1024^3 on device pointers (bf16 MFMA; not a BASELINE config)
+        sb = lambda: check(lib.acfun_dev_gemm_bf16(M, M, M, A.data_ptr(), Bm.data_ptr(),
+                                                   Cm.data_ptr(), sp))
+        t = T.run(sb, steps, 5)
+        k = T.kernel_ms(lib, sb, steps, "k_bf16mm")
+        f = 2.0 * M ** 3 / (t * 1e-3)
+        configs["gemm_bf16_1024"] = {"ms": round(t, 5), "TFLOPS": round(f / 1e12, 3),
+                                     "frac_bf16_peak": round(f / 2.5e15, 4),
+                                     "kernel_ms": {"k_bf16mm": k},
+                                     "note": "step = two bf16 packing passes + k_bf16mm"}
+
         # 2b: F(4,3), N=8, 112x112
         x2 = cuda(rng.uniform(0, 1, (8, 112, 112, 64)).astype(np.float32))
         y2 = torch.empty((8, 112, 112, 64), device=dev)

@@ -176,6 +176,10 @@ int acfun_sync(void);
  * Return 0 on success, -1 on a shape or launch error (see acfun_last_error()). */
 int acfun_dev_gemm_epi(int M, int N, int K, const float* A, const float* B, float* C,
                        const float* bias, int act, void* stream);
+/* acfun_gemm_bf16 on device pointers (bf16 MFMA; operands rounded as the reference's
+ * gemm_bf16_avx512.cpp:37-44). */
+int acfun_dev_gemm_bf16(int M, int N, int K, const float* A, const float* B, float* C,
+                        void* stream);
 int acfun_dev_conv2d(const float* input, int N, int H, int W, int Cin,
                      const float* weight, const float* bias, int KH, int KW, int Cout,
                      int stride, int pad, int groups, float* output, int act, void* stream);

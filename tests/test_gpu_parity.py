@@ -40,8 +40,9 @@ def test_gemm_f32(gpu, rng, M, N, K, epi):
     assert rel_err(got, want) < GEMM_TOL, rel_err(got, want)
 
 
-def test_gemm_bf16(gpu, rng):
-    M, N, K = 200, 96, 300
+@pytest.mark.parametrize("M,N,K", [(200, 96, 300), (64, 64, 64), (1, 1, 1), (130, 70, 7),
+                                   (1024, 1024, 1024), (33, 40, 0)])
+def test_gemm_bf16(gpu, rng, M, N, K):
     A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
     got = np.zeros((M, N), np.float32)
@@ -51,6 +52,9 @@ def test_gemm_bf16(gpu, rng):
         u = a.view(np.uint32).astype(np.uint64)
         u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
         return u.astype(np.uint32).view(np.float32)
+    if K == 0:
+        assert not got.any()
+        return
     want = oracle.gemm_f64(bf16(A), bf16(B))
     assert rel_err(got, want) < 1e-5
 
