@@ -835,30 +835,36 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
         const unsigned uv = cob + li < Cout ? (unsigned)((cob + li) * 8 + 4 * g) * 4u : kOOB;
         const __amdgpu_buffer_rsrc_t xres =
             __builtin_amdgcn_make_buffer_rsrc((void*)img, (short)0, H * W * Cin * 4, 0x00020000);
-        // chunk c0 + j goes to X buffer j % 3
+        const int m = c1 - c0;                          // chunks of this range (even)
+        // chunk c0 + j goes to X buffer j % 3.  A chunk index j >= m (the
+        // pipeline's loads past the range) reads out of range: the loads are
+        // still issued, so every step issues the same instructions and wait
+        // counts, but they return zeros without touching memory.
         auto ld_u = [&](int j, f4* ub) {               // U(j): this wave's 4 points
-            const unsigned cbase = (unsigned)(c0 + j) * 16u * upt;
+            const bool live = j < m;
+            const unsigned cbase = (unsigned)(c0 + (live ? j : 0)) * 16u * upt;
+            const unsigned v = live ? uv : kOOB;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 ub[k] = __builtin_bit_cast(
-                    f4, __builtin_amdgcn_raw_buffer_load_b128(ures, uv, cbase + (unsigned)(4 * wave + k) * upt, 0));
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(ures, v, cbase + (unsigned)(4 * wave + k) * upt, 0));
         };
         // X(j) into base: blocks WAVE, WAVE+4, ... (a compile-time count per wave,
         // all lanes active, so the compiler's wait counts are exact)
         auto dma_x = [&](auto wavec, int j, float* base) {
             constexpr int WAVE = decltype(wavec)::value;
-            const int ci = 8 * (c0 + j);
+            const bool live = j < m;
+            const int ci = 8 * (c0 + (live ? j : 0));
 #pragma unroll
             for (int k = 0; k < CF::KX; ++k) {
                 if (WAVE + 4 * k >= CF::XBLK) continue;
-                unsigned v = xv[k];
+                unsigned v = live ? xv[k] : kOOB;
                 if (ragged && ci + 8 > Cin && ci + 4 * (int)((xq >> k) & 1) >= Cin) v = kOOB;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + (WAVE + 4 * k) * 256), 16,
                                                          v, ci * 4, 0, 0);
             }
         };
 
-        const int m = c1 - c0;                          // chunks of this range (even)
         f16v acc[4];
 #pragma unroll
         for (int a = 0; a < 4; ++a)
@@ -871,13 +877,12 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
             constexpr int NXW = CF::template nxw<ROW>();   // X blocks this wave issues per chunk
 
             // ---- prologue: U(0), X(0), X(1), X(2) in this order; wait for U(0),
-            // X(0).  Loads past the range repeat a chunk of it into a buffer no
-            // one reads, so every step issues the same loads.
+            // X(0).  Loads past the range fill a buffer no one reads with zeros.
             f4 uA[4], uB[4];
             ld_u(0, uA);
             dma_x(rowc, 0, smem);
-            dma_x(rowc, m > 1 ? 1 : 0, smem + CF::XFL);
-            dma_x(rowc, m > 2 ? 2 : 0, smem + 2 * CF::XFL);
+            dma_x(rowc, 1, smem + CF::XFL);
+            dma_x(rowc, 2, smem + 2 * CF::XFL);
             wait_vmcnt(2 * NXW);
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -916,7 +921,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
             auto chunk = [&](int j, const f4* bf, f4* un) {
                 // this wave's U(j) and X(j+1) have landed; X(j+2) may stay in flight
                 wait_vmcnt(NXW);
-                ld_u(j + 1 < m ? j + 1 : j, un);
+                ld_u(j + 1, un);
                 mfma_pt(0, dh[0], bf[0]);
                 mfma_pt(1, dh[1], bf[1]);
                 const int xb1 = xb == 2 ? 0 : xb + 1;  // buffer of X(j+1)
@@ -925,10 +930,10 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
                 // complete; the memory clobber keeps LDS accesses on their side.
                 // After it X(j+1) is visible and X(j)'s buffer is free.
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                dma_x(rowc, j + 3 < m ? j + 3 : j, smem + xb * CF::XFL);
-                // X(j+1) (after the last chunk: a buffer whose loads completed at
-                // the wait above, read before any wave reaches the epilogue,
-                // results unused) -- unconditional so the transform can
+                dma_x(rowc, j + 3, smem + xb * CF::XFL);
+                // X(j+1) (after the last chunk: a buffer whose out-of-range loads
+                // completed at the wait above, read before any wave reaches the
+                // epilogue, results unused) -- unconditional so the transform can
                 // interleave with the MFMAs
                 f4 dA[4], dB[4];
                 xread(smem + xb1 * CF::XFL, dA, dB);
@@ -960,7 +965,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23u(
 
         // ---- epilogue.  Lane l, register r <-> MFMA row (tile) 8*(r/4)+4*(l/32)+r%4,
         // column (channel) l%32.  S layout [row 4][c 2][tile 32][SST floats].
-        wait_vmcnt(0);                       // the last (repeated) X loads have landed
+        wait_vmcnt(0);                       // the last (out-of-range) X loads have landed
         __syncthreads();                     // staging buffers are free
         {
             float* pp = smem + (wave * 2) * 32 * CF::SST + (4 * g) * CF::SST + li;
@@ -1023,6 +1028,339 @@ bool launch_wino23u(const float* in, const float* U, const float* bias, float* o
     return check_launch("k_wino23u");
 }
 
+// F(2,3), persistent form of k_wino23u: each workgroup runs a list of
+// 32-tile x 32-channel units back to back, and the chunk pipeline runs on
+// across unit boundaries -- the loads of the next unit's first chunks are
+// issued during the current unit's last ones, so a unit costs no load
+// latency up front and no drain at the end.
+//
+// Unit u (channel block fastest, then column block, then image x row block)
+// is assigned by XCD: XCD x = blockIdx.x % 8 owns the contiguous unit range
+// [x*U/8, (x+1)*U/8) and its workgroups take it round robin, so the two
+// channel blocks of a spatial block and neighbouring row blocks (which share
+// two halo rows) are read while still in that XCD's L2.
+//
+// The per-chunk body is k_wino23u's (same LDS layouts, operands and MFMA
+// order).  The epilogue runs in two rounds of 16 KB (output column cc of the
+// 2x2 tiles): each wave stores its row sums S_i[cc] (the AT column reduction
+// of its transform row) in LDS, and after a barrier every thread forms
+// Y[0][cc] = S0 + S1 + S2 and Y[1][cc] = S1 - S2 + S3 for one tile and 4
+// channels, adds the bias (staged in LDS at the start), applies the
+// activation and stores two 16-byte quads.
+//
+// Wait counts.  Chunk J issues U(J+1) at its start and X(J+3) after its
+// barrier (the next unit's chunks once J+1, J+3 pass the unit's end), and
+// waits for U(J), X(J+1) with X(J+2) left in flight, as in k_wino23u.  The
+// epilogue after a unit's last chunk J makes the wait of chunk J+1 (X(J+3)
+// left in flight) before its stores, so that chunk skips it.  Stores then
+// sit between loads in the vmcnt queue: a later wait that leaves n loads in
+// flight still proves every older load landed, because loads complete in
+// issue order (a store may complete at any time; it only makes the wait
+// longer).  The stores are inline asm, so the compiler's own wait insertion
+// sees only loads, whose counts are exact, instead of falling back to
+// vmcnt(0) for mixed loads and stores.
+template <int TC, int ACT>
+__global__ __launch_bounds__(256, 3) void k_wino23p(
+    const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
+    float* __restrict__ out, int H, int W, int Cin, int Cinp, int Cout, int rblocks, int gx, int gz,
+    int nunits, int in_bytes) {
+    using CF = W23Cfg<TC>;
+    constexpr int R = CF::R, TCP = CF::TCP;
+    constexpr unsigned kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* const epi = smem + 3 * CF::XFL;             // [S_i 4][tile 32][SST floats]
+    float* const bsm = epi + 4 * 32 * CF::SST;         // bias, Cout floats (padded to 4)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // = transform row
+    const int li = lane & 31, g = lane >> 5;
+    const int m = Cinp / 8;                            // chunks per unit (even, >= 4)
+
+    // this workgroup's units: rs + i0, rs + i0 + nwx, ... < re
+    const int nwx = (int)(gridDim.x / 8);
+    const int xcd = (int)(blockIdx.x % 8), i0 = (int)(blockIdx.x / 8);
+    const int rs = (int)((long long)xcd * nunits / 8), re = (int)((long long)(xcd + 1) * nunits / 8);
+    const int nu = rs + i0 < re ? (re - rs - i0 + nwx - 1) / nwx : 0;
+    if (nu == 0) return;                               // uniform per workgroup
+
+    for (int c = tid; c < (Cout + 3) / 4 * 4; c += 256) bsm[c] = bias && c < Cout ? bias[c] : 0.f;
+    const int etile = tid >> 3, ecq = 4 * (tid & 7);   // epilogue: one tile x 4 channels
+    const bool Cout4 = (Cout & 3) == 0;
+
+    const unsigned upt = 32u * Cout;                   // bytes per point of one chunk
+    const __amdgpu_buffer_rsrc_t ures =
+        __builtin_amdgcn_make_buffer_rsrc((void*)U, (short)0, (int)(16u * upt * (Cinp >> 3)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)in, (short)0, in_bytes, 0x00020000);
+    const bool ragged = (Cin & 7) != 0;
+    // per-lane LDS read offsets (floats, X buffer 0)
+    const int sr = li / TC, stx = li % TC;
+    int xoff[2][2];                                    // [kk = stx + jj][plane]
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int kk = stx + jj;
+        const int qs = g ^ ((kk >> CF::SWZ) & 1);
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) xoff[jj][pl] = (((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
+    }
+    // X DMA slots of this lane: block k holds slot (wave + 4k)*64 + lane ->
+    // staged pixel (row, col) and channel quad q; ~0u past the staged region
+    unsigned xl[CF::KX];
+#pragma unroll
+    for (int k = 0; k < CF::KX; ++k) {
+        const int sl = (wave + 4 * k) * 64 + lane;
+        const int pk = sl >> 1;                        // (row*2 + plane)*TCP + kk
+        const int rp = pk / TCP, kk = pk - rp * TCP;
+        const int q = (sl & 1) ^ ((kk >> CF::SWZ) & 1);
+        xl[k] = sl < CF::XSLOTS ? (unsigned)((rp >> 1) | ((2 * kk + (rp & 1)) << 8) | (q << 16)) : ~0u;
+    }
+
+    struct UnitP { int n, ty0, tx0, cob; };
+    auto decode = [&](int k) {                         // k-th unit of this workgroup
+        const int u = rs + i0 + k * nwx;
+        const int bz = u % gz, sp = u / gz;
+        const int bx = sp % gx, by = sp / gx;
+        const int n = by / rblocks;
+        return UnitP{n, (by - n * rblocks) * R, bx * TC, bz * 32};
+    };
+    // U(j) of unit P: this wave's 4 points; out of range (zeros, no memory
+    // access) when !live
+    auto ld_u = [&](const UnitP& P, bool live, int j, f4* ub) {
+        const unsigned cbase = (unsigned)(live ? j : 0) * 16u * upt;
+        const unsigned v = live && P.cob + li < Cout ? (unsigned)((P.cob + li) * 8 + 4 * g) * 4u : kOOB;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            ub[k] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(ures, v, cbase + (unsigned)(4 * wave + k) * upt, 0));
+    };
+    // X(j) of unit P into base: blocks WAVE, WAVE+4, ...
+    auto dma_x = [&](auto wavec, const UnitP& P, bool live, int j, float* base) {
+        constexpr int WAVE = decltype(wavec)::value;
+        const int ci = 8 * (live ? j : 0);
+#pragma unroll
+        for (int k = 0; k < CF::KX; ++k) {
+            if (WAVE + 4 * k >= CF::XBLK) continue;
+            const unsigned c = xl[k];
+            const int ih = 2 * P.ty0 - 1 + (int)(c & 255), iw = 2 * P.tx0 - 1 + (int)((c >> 8) & 255);
+            const int q = (int)((c >> 16) & 1);
+            const bool ok = live && c != ~0u && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W &&
+                            !(ragged && ci + 4 * q >= Cin);
+            const unsigned v = ok ? (unsigned)(((P.n * H + ih) * W + iw) * Cin + 4 * q) * 4u : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + (WAVE + 4 * k) * 256), 16, v,
+                                                     ci * 4, 0, 0);
+        }
+    };
+
+    f16v acc[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+
+    auto run = [&](auto rowc) {
+        constexpr int ROW = decltype(rowc)::value;
+        using RW = W23Row<TC, ROW>;
+        constexpr int NXW = CF::template nxw<ROW>();   // X blocks this wave issues per chunk
+
+        UnitP cur = decode(0), nxt = decode(nu > 1 ? 1 : 0);
+        bool nlive = nu > 1;
+
+        // ---- prologue: U(0), X(0), X(1), X(2) of the first unit; wait for
+        // U(0), X(0) (and the bias staging, by the barrier's lgkmcnt)
+        f4 uA[4], uB[4];
+        ld_u(cur, true, 0, uA);
+        dma_x(rowc, cur, true, 0, smem);
+        dma_x(rowc, cur, true, 1, smem + CF::XFL);
+        dma_x(rowc, cur, true, 2, smem + 2 * CF::XFL);
+        wait_vmcnt(2 * NXW);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+        auto xread = [&](const float* X, f4* dA, f4* dB) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int o = xoff[j >> 1][j & 1];
+                dA[j] = *(const f4*)&X[o + RW::A * 2 * TCP * 8];
+                dB[j] = *(const f4*)&X[o + RW::B * 2 * TCP * 8];
+            }
+        };
+        auto xform = [&](const f4* dA, const f4* dB, f4* dh) {
+            f4 tt[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tt[j] = RW::PLUS ? dA[j] + dB[j] : dA[j] - dB[j];
+            dh[0] = tt[0] - tt[2];
+            dh[1] = tt[1] + tt[2];
+            dh[2] = tt[2] - tt[1];
+            dh[3] = tt[3] - tt[1];
+        };
+        auto mfma_pt = [&](int a, const f4& d, const f4& bb) {
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                acc[a] = __builtin_amdgcn_mfma_f32_32x32x2f32(d[s2], bb[s2], acc[a], 0, 0, 0);
+        };
+        f4 dh[4];
+        {
+            f4 dA[4], dB[4];
+            xread(smem, dA, dB);
+            xform(dA, dB, dh);
+        }
+        int xb = 0;                                    // X buffer of the current chunk
+        // chunk j of the current unit multiplies with bf and loads the next
+        // chunk's U into un
+        auto chunk = [&](int j, const f4* bf, f4* un, bool wait) {
+            if (wait) wait_vmcnt(NXW);                 // U(j), X(j+1) have landed
+            {
+                const bool in_cur = j + 1 < m;
+                ld_u(in_cur ? cur : nxt, in_cur || nlive, in_cur ? j + 1 : 0, un);
+            }
+            mfma_pt(0, dh[0], bf[0]);
+            mfma_pt(1, dh[1], bf[1]);
+            const int xb1 = xb == 2 ? 0 : xb + 1;
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            {                                          // X(j+3) into X(j)'s buffer
+                const bool in_cur = j + 3 < m;
+                dma_x(rowc, in_cur ? cur : nxt, in_cur || nlive, in_cur ? j + 3 : j + 3 - m,
+                      smem + xb * CF::XFL);
+            }
+            f4 dA[4], dB[4];
+            xread(smem + xb1 * CF::XFL, dA, dB);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_pt(2, dh[2], bf[2]);
+            mfma_pt(3, dh[3], bf[3]);
+            xform(dA, dB, dh);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            xb = xb1;
+        };
+
+        for (int k = 0; k < nu; ++k) {
+            // two register sets for U, no copies; the first chunk after an
+            // epilogue needs no wait (the epilogue's covers it)
+            for (int j = 0; j < m; j += 2) {
+                chunk(j, uA, uB, j != 0 || k == 0);
+                chunk(j + 1, uB, uA, true);
+            }
+            // ---- epilogue of unit cur.  After this wait only the X(J+3)
+            // loads of the last chunk J (the next unit's X(2)) are in flight:
+            // the next unit's U(0) and X(1), which its first chunk needs, have
+            // landed.  Two rounds (output column cc of each tile): every wave
+            // stores its row sum S_ROW[cc] in LDS, then every thread forms
+            // Y[0][cc] = S0 + S1 + S2 and Y[1][cc] = S1 - S2 + S3 for one tile
+            // and 4 channels and stores two 16-byte quads.
+            wait_vmcnt(NXW);
+            const int ec = cur.cob + ecq;
+            const f4 bq = *(const f4*)&bsm[ec < Cout ? ec : 0];
+            const int tsr = etile / TC, tsx = etile % TC;
+            const int oh0 = 2 * (cur.ty0 + tsr), ow0 = 2 * (cur.tx0 + tsx);
+            float* const orow = out + (((long long)cur.n * H + oh0) * W + ow0) * Cout + ec;
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                {
+                    float* pp = epi + (ROW * 32 + 4 * g) * CF::SST + li;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r];
+                        pp[(8 * (r >> 2) + (r & 3)) * CF::SST] = cc == 0 ? m0 + m1 + m2 : m1 - m2 + m3;
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                f4 S[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[i] = *(const f4*)&epi[(i * 32 + etile) * CF::SST + ecq];
+                // the round-1 writes must not overtake these reads
+                if (cc == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                if (ec < Cout && ow0 + cc < W) {
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        if (oh0 + r >= H) continue;
+                        f4 v = r == 0 ? S[0] + S[1] + S[2] : S[1] - S[2] + S[3];
+                        v = v + bq;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = act_apply(v[e], ACT);
+                        float* dst = orow + ((long long)r * W + cc) * Cout;
+                        if (Cout4) {
+                            // s_nop: a VALU write to the data registers of a store
+                            // of more than 8 bytes needs a wait state after it,
+                            // which the compiler cannot insert after inline asm
+                            asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(dst), "v"(v)
+                                         : "memory");
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (ec + e < Cout)
+                                    asm volatile("global_store_dword %0, %1, off" ::"v"(dst + e), "v"(v[e])
+                                                 : "memory");
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[a][e] = 0.f;
+            cur = nxt;
+            nlive = k + 2 < nu;
+            nxt = decode(nlive ? k + 2 : k + 1);
+        }
+        wait_vmcnt(0);                                 // out-of-range loads and stores done
+    };
+    switch (wave) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
+    }
+}
+
+template <int TC>
+size_t wino23p_lds(int Cout) {
+    return ((size_t)3 * W23Cfg<TC>::XFL + 4 * 32 * W23Cfg<TC>::SST + (size_t)(Cout + 3) / 4 * 4) *
+           sizeof(float);
+}
+
+// Persistent launch: 3 workgroups per CU (a multiple of 8 workgroups), each
+// running its share of the units.  False when the shape does not suit it
+// (fewer than 4 chunks per unit, the input past 2 GB or the LDS budget).
+template <int TC>
+bool launch_wino23p(const float* in, const float* U, const float* bias, float* out, int N, int H,
+                    int W, int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s,
+                    bool* launched) {
+    using CF = W23Cfg<TC>;
+    *launched = false;
+    const size_t lds = wino23p_lds<TC>(Cout);
+    const long long in_bytes = (long long)N * H * W * Cin * 4;
+    if (Cinp / 8 < 4 || in_bytes >= (1ll << 31) || lds * 3 > 160 * 1024) return true;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 0>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 / 3);
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 / 3);
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 / 3);
+    }
+    const int rblocks = (tH + CF::R - 1) / CF::R;
+    const long long gx = (tW + TC - 1) / TC, gy = (long long)N * rblocks, gz = (Cout + 31) / 32;
+    const long long nunits = gx * gy * gz;
+    if (nunits >= (1ll << 30)) return true;
+    const long long slots = 3ll * num_cus() / 8, need = (nunits + 7) / 8;
+    const unsigned grid = (unsigned)(8 * (slots < need ? slots : need));
+    if (act == 1)
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 1>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
+                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+    else if (act == 2)
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 2>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
+                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+    else
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 0>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
+                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+    *launched = true;
+    return check_launch("k_wino23p");
+}
+
 bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
                 int Cout, float* out, int act, hipStream_t s) {
     int tH = (H + 1) / 2, tW = (W + 1) / 2;
@@ -1044,9 +1382,15 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
         ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, true>), dim3((Cout + 15) / 16, Cinp / 16),
                      dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
         if (!check_launch("k_wino_filter_t")) return false;
-        if (tW >= 12)
+        bool launched = false;
+        if (tW >= 12) {
+            if (!launch_wino23p<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+                                    s, &launched))
+                return false;
+            if (launched) return true;
             return launch_wino23u<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
                                       act, s);
+        }
         return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
     }
     ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, false>), dim3((Cout + 15) / 16, Cinp / 16),

@@ -359,9 +359,12 @@ def test_config2_full(gpu, rng, N, HW, tol):
 
 
 # F(2,3) 32-tile units at batch sizes around config 2a, including a ragged
-# 20 -> 40 conv (4 chunks, partial output-channel block); every image is
-# checked and a second run must repeat the first bit for bit.
-@pytest.mark.parametrize("N,Cin,Cout", [(15, 64, 64), (32, 20, 40), (26, 64, 64)])
+# 20 -> 40 conv (4 chunks, partial output-channel block), 896 units of 16
+# chunks (more units than workgroups) and 252 units (fewer units than
+# workgroups, not a multiple of 8); every image is checked and a second run
+# must repeat the first bit for bit.
+@pytest.mark.parametrize("N,Cin,Cout", [(15, 64, 64), (32, 20, 40), (26, 64, 64), (4, 128, 256),
+                                        (3, 32, 96)])
 def test_wino23_batches(gpu, rng, N, Cin, Cout):
     HW = 56
     x = rng.uniform(0, 1, (N, HW, HW, Cin)).astype(np.float32)
