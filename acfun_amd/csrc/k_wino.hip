@@ -1041,8 +1041,11 @@ bool launch_wino23u(const float* in, const float* U, const float* bias, float* o
 // two halo rows) are read while still in that XCD's L2.
 //
 // The per-chunk body is k_wino23u's (same LDS layouts, operands and MFMA
-// order).  The epilogue runs in two rounds of 16 KB (output column cc of the
-// 2x2 tiles): each wave stores its row sums S_i[cc] (the AT column reduction
+// order).  A lane's X slot offsets relative to a unit's window origin are the
+// same for every unit; per unit only the window origin (a scalar) and the
+// lane's in-image bits change.  The epilogue runs in two rounds through a
+// 20 KB LDS area (output column cc of the 2x2 tiles): each wave stores its
+// row sums S_i[cc] (the AT column reduction
 // of its transform row) in LDS, and after a barrier every thread forms
 // Y[0][cc] = S0 + S1 + S2 and Y[1][cc] = S1 - S2 + S3 for one tile and 4
 // channels, adds the bias (staged in LDS at the start), applies the
@@ -1103,17 +1106,21 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
         for (int pl = 0; pl < 2; ++pl) xoff[jj][pl] = (((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
     }
     // X DMA slots of this lane: block k holds slot (wave + 4k)*64 + lane ->
-    // staged pixel (row, col) and channel quad q; ~0u past the staged region
-    unsigned xl[CF::KX];
+    // staged pixel (row, col) of the unit's window and channel quad q.
+    // xlo[k]: the slot's byte offset from the window origin (pixel (2 ty0 - 1,
+    // 2 tx0 - 1) of the unit's image), the same for every unit.
+    auto slot_q = [&](int k) {                         // channel quad of block k's slot
+        const int sl = (wave + 4 * k) * 64 + lane;
+        return (sl & 1) ^ ((((sl >> 1) % TCP) >> CF::SWZ) & 1);
+    };
+    unsigned xlo[CF::KX];
 #pragma unroll
     for (int k = 0; k < CF::KX; ++k) {
         const int sl = (wave + 4 * k) * 64 + lane;
         const int pk = sl >> 1;                        // (row*2 + plane)*TCP + kk
         const int rp = pk / TCP, kk = pk - rp * TCP;
-        const int q = (sl & 1) ^ ((kk >> CF::SWZ) & 1);
-        xl[k] = sl < CF::XSLOTS ? (unsigned)((rp >> 1) | ((2 * kk + (rp & 1)) << 8) | (q << 16)) : ~0u;
+        xlo[k] = (unsigned)((((rp >> 1) * W + 2 * kk + (rp & 1)) * Cin + 4 * slot_q(k)) * 4);
     }
-
     struct UnitP { int n, ty0, tx0, cob; };
     auto decode = [&](int k) {                         // k-th unit of this workgroup
         const int u = rs + i0 + k * nwx;
@@ -1122,6 +1129,23 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
         const int n = by / rblocks;
         return UnitP{n, (by - n * rblocks) * R, bx * TC, bz * 32};
     };
+    // in-image bits of the lane's slots for unit P: bit k (k < KX)
+    auto inimg = [&](const UnitP& P, bool live) {
+        unsigned b = 0;
+#pragma unroll
+        for (int k = 0; k < CF::KX; ++k) {
+            const int sl = (wave + 4 * k) * 64 + lane;
+            const int pk = sl >> 1;
+            const int rp = pk / TCP, kk = pk - rp * TCP;
+            const int ih = 2 * P.ty0 - 1 + (rp >> 1), iw = 2 * P.tx0 - 1 + 2 * kk + (rp & 1);
+            const bool ok = live && sl < CF::XSLOTS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            b |= (unsigned)ok << k;
+        }
+        return b;
+    };
+    // byte offset of unit P's window origin (negative at the image's top
+    // left; origin + xlo is in range wherever the in-image bit is set)
+    auto origin = [&](const UnitP& P) { return ((P.n * H + 2 * P.ty0 - 1) * W + 2 * P.tx0 - 1) * Cin * 4; };
     // U(j) of unit P: this wave's 4 points; out of range (zeros, no memory
     // access) when !live
     auto ld_u = [&](const UnitP& P, bool live, int j, f4* ub) {
@@ -1132,19 +1156,16 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
             ub[k] = __builtin_bit_cast(
                 f4, __builtin_amdgcn_raw_buffer_load_b128(ures, v, cbase + (unsigned)(4 * wave + k) * upt, 0));
     };
-    // X(j) of unit P into base: blocks WAVE, WAVE+4, ...
-    auto dma_x = [&](auto wavec, const UnitP& P, bool live, int j, float* base) {
+    // X(j) of the unit with window origin org and in-image bits ib into base:
+    // blocks WAVE, WAVE+4, ...
+    auto dma_x = [&](auto wavec, int org, unsigned ib, int j, float* base) {
         constexpr int WAVE = decltype(wavec)::value;
-        const int ci = 8 * (live ? j : 0);
+        const int ci = 8 * j;
 #pragma unroll
         for (int k = 0; k < CF::KX; ++k) {
             if (WAVE + 4 * k >= CF::XBLK) continue;
-            const unsigned c = xl[k];
-            const int ih = 2 * P.ty0 - 1 + (int)(c & 255), iw = 2 * P.tx0 - 1 + (int)((c >> 8) & 255);
-            const int q = (int)((c >> 16) & 1);
-            const bool ok = live && c != ~0u && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W &&
-                            !(ragged && ci + 4 * q >= Cin);
-            const unsigned v = ok ? (unsigned)(((P.n * H + ih) * W + iw) * Cin + 4 * q) * 4u : kOOB;
+            unsigned v = (ib >> k) & 1 ? (unsigned)org + xlo[k] : kOOB;
+            if (ragged && ci + 8 > Cin && ci + 4 * slot_q(k) >= Cin) v = kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + (WAVE + 4 * k) * 256), 16, v,
                                                      ci * 4, 0, 0);
         }
@@ -1163,14 +1184,16 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
 
         UnitP cur = decode(0), nxt = decode(nu > 1 ? 1 : 0);
         bool nlive = nu > 1;
+        // in-image bits of the current (bits 0..3) and next unit (bits 4..7)
+        unsigned ib = inimg(cur, true) | (inimg(nxt, nlive) << 4);
 
         // ---- prologue: U(0), X(0), X(1), X(2) of the first unit; wait for
         // U(0), X(0) (and the bias staging, by the barrier's lgkmcnt)
         f4 uA[4], uB[4];
         ld_u(cur, true, 0, uA);
-        dma_x(rowc, cur, true, 0, smem);
-        dma_x(rowc, cur, true, 1, smem + CF::XFL);
-        dma_x(rowc, cur, true, 2, smem + 2 * CF::XFL);
+        dma_x(rowc, origin(cur), ib, 0, smem);
+        dma_x(rowc, origin(cur), ib, 1, smem + CF::XFL);
+        dma_x(rowc, origin(cur), ib, 2, smem + 2 * CF::XFL);
         wait_vmcnt(2 * NXW);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -1217,7 +1240,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             {                                          // X(j+3) into X(j)'s buffer
                 const bool in_cur = j + 3 < m;
-                dma_x(rowc, in_cur ? cur : nxt, in_cur || nlive, in_cur ? j + 3 : j + 3 - m,
+                dma_x(rowc, origin(in_cur ? cur : nxt), in_cur ? ib : ib >> 4, in_cur ? j + 3 : j + 3 - m,
                       smem + xb * CF::XFL);
             }
             f4 dA[4], dB[4];
@@ -1303,6 +1326,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
             cur = nxt;
             nlive = k + 2 < nu;
             nxt = decode(nlive ? k + 2 : k + 1);
+            ib = (ib >> 4) | (inimg(nxt, nlive) << 4);
         }
         wait_vmcnt(0);                                 // out-of-range loads and stores done
     };
@@ -1390,6 +1414,14 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
             if (launched) return true;
             return launch_wino23u<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
                                       act, s);
+        }
+        // 8-wide units: the persistent kernel measured faster at 8 chunks per
+        // unit and slower at 32 (ResNet-50's 14 x 14 x 256 stage)
+        if (Cinp <= 64) {
+            if (!launch_wino23p<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s,
+                                   &launched))
+                return false;
+            if (launched) return true;
         }
         return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
     }

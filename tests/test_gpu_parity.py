@@ -378,6 +378,18 @@ def test_wino23_batches(gpu, rng, N, Cin, Cout):
     assert_bitexact(again, got, "repeat run")
 
 
+# 8-wide F(2,3) units (images 12 to 22 pixels wide): ResNet-50's 28 x 28 stage
+# (1024 units, more than the persistent grid) and a ragged 36 -> 72 conv.
+@pytest.mark.parametrize("N,HW,Cin,Cout", [(32, 28, 128, 128), (5, 22, 36, 72)])
+def test_wino23_narrow(gpu, rng, N, HW, Cin, Cout):
+    x = rng.uniform(0, 1, (N, HW, HW, Cin)).astype(np.float32)
+    w = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2 / (9 * Cin))).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
+    got = np.full((N, HW, HW, Cout), np.nan, np.float32)
+    gpu.acfun_conv2d_relu(P(x), N, HW, HW, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(got))
+    _check_images(got, x, w, b, Cout, WINO_TOL, step=8)
+
+
 def test_config4a_full_exact(gpu, rng):
     """Depthwise 3x3/2 (BN folded, ReLU) then 3x3/2 MaxPool at config 4a size."""
     N, H, C = 32, 112, 96
