@@ -156,7 +156,8 @@ void acfun_gemm(int M, int N, int K, const float* A, const float* B, float* C) {
 }
 
 void acfun_gemm_bf16(int M, int N, int K, const float* A, const float* B, float* C) {
-    if (M <= 0 || N <= 0 || K < 0) return;
+    // K <= 0 leaves C untouched (src/gemm_bf16_avx512.cpp:173)
+    if (M <= 0 || N <= 0 || K <= 0) return;
     host_call([&](HostCall& hc) {
         auto dA = (const float*)hc.in(A, F((long long)M * K));
         auto dB = (const float*)hc.in(B, F((long long)K * N));
@@ -461,7 +462,7 @@ int acfun_dev_gemm_epi(int M, int N, int K, const float* A, const float* B, floa
 int acfun_dev_gemm_bf16(int M, int N, int K, const float* A, const float* B, float* C,
                         void* stream) {
     if (!ensure_device()) return -1;
-    if (M <= 0 || N <= 0 || K < 0) return 0;
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
     return gemm_bf16_dev(M, N, K, A, B, C, resolve(stream)) ? 0 : -1;
 }
 

@@ -23,12 +23,13 @@ typedef int i4v __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// fp32 -> bf16 bits: round to nearest even on bit 16 for finite values, NaN kept quiet.
+// fp32 -> bf16 bits as the reference packs its operands
+// (src/gemm_bf16_avx512.cpp:37-44): add 0x7fff plus bit 16, keep the upper
+// half.  The 32-bit add wraps, so some NaNs become infinities or zero there
+// too.
 __device__ __forceinline__ unsigned bf16_bits(float f) {
-    unsigned u = __float_as_uint(f);
-    if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
-    else if (u & 0x007fffffu) u |= 0x00400000u;
-    return u >> 16;
+    const unsigned u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
 // One lane: 8 consecutive k of one row of A -> one 16-byte store.
@@ -176,11 +177,10 @@ __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict
     }
 }
 
-}  // namespace
-
-bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C, hipStream_t s) {
-    if (M <= 0 || N <= 0) return true;
-    const int Kp = K <= 0 ? 64 : (K + 63) / 64 * 64;
+// C[0:M, 0:N] (row stride ldb = ldc) = bf16(A[0:M, :]) x bf16(B[:, 0:N]) on bf16 MFMA
+bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, float* C,
+                 hipStream_t s) {
+    const int Kp = (K + 63) / 64 * 64;
     if ((long long)M * Kp * 2 >= 0x7fffffffll || (long long)N * Kp * 2 >= 0x7fffffffll) {
         set_error("acfun_gemm_bf16: operands beyond 2 GB");
         return false;
@@ -191,7 +191,7 @@ bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C
     hipLaunchKernelGGL(k_pack_a_bf16, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, A, M, K, K,
                        ab.as<unsigned short>(), Kp);
     if (!check_launch("k_pack_a_bf16")) return false;
-    hipLaunchKernelGGL(k_pack_bt_bf16, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, B, K, N, N,
+    hipLaunchKernelGGL(k_pack_bt_bf16, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, B, K, N, ldb,
                        bt.as<unsigned short>(), Kp);
     if (!check_launch("k_pack_bt_bf16")) return false;
     static bool attr = false;
@@ -202,9 +202,29 @@ bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C
     }
     const long long tiles = (long long)((M + BF_BM - 1) / BF_BM) * ((N + BF_BN - 1) / BF_BN);
     ACFUN_LAUNCH("k_bf16mm", k_bf16mm, dim3((unsigned)tiles), dim3(256), lds, s, ab.as<unsigned short>(),
-                 bt.as<unsigned short>(), C, M, N, Kp, N, (unsigned)((long long)M * Kp * 2),
+                 bt.as<unsigned short>(), C, M, N, Kp, ldb, (unsigned)((long long)M * Kp * 2),
                  (unsigned)((long long)N * Kp * 2));
     return check_launch("k_bf16mm");
+}
+
+}  // namespace
+
+// The reference's split (src/gemm_bf16_avx512.cpp:123-168): its 16 x 16
+// micro-tiles multiply bf16-rounded operands; the rows past the last multiple
+// of 16 of M and the columns past the last multiple of 16 of N (its 256 x 128
+// tiles are multiples of 16) take the scalar fp32 path on the unrounded
+// operands.  Here k_bf16mm covers the first region and the fp32 GEMM engine
+// the two strips.  K <= 0 leaves C untouched, as there (:173).
+bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C, hipStream_t s) {
+    if (M <= 0 || N <= 0 || K <= 0) return true;
+    const int M16 = M / 16 * 16, N16 = N / 16 * 16;
+    if (M16 < M && !gemm_f32(M - M16, N, K, A + (long long)M16 * K, K, B, N, C + (long long)M16 * N, N,
+                             nullptr, 0, s))
+        return false;
+    if (N16 < N && M16 > 0 && !gemm_f32(M16, N - N16, K, A, K, B + N16, N, C + N16, N, nullptr, 0, s))
+        return false;
+    if (M16 == 0 || N16 == 0) return true;
+    return bf16_region(M16, N16, N, K, A, B, C, s);
 }
 
 }  // namespace acfun

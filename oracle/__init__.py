@@ -41,6 +41,7 @@ def lib():
             "oracle_gemm": [_i, _i, _i, _f32p, _f32p, _f32p],
             "oracle_gemm_epi": [_i, _i, _i, _f32p, _f32p, _f32p, _vp, _i],
             "oracle_gemm_f64": [_i, _i, _i, _f32p, _f32p, _f64p],
+            "oracle_bf16_round": [_f32p, _f32p, _sz],
             "oracle_conv2d_route": [_i] * 10,
             "oracle_conv2d_f64": [_f32p, _i, _i, _i, _i, _f32p, _vp, _i, _i, _i, _i, _i, _i, _f64p, _i],
             "oracle_conv2d_dw": [_f32p, _i, _i, _i, _i, _f32p, _vp, _i, _i, _i, _i, _f32p, _i],
@@ -112,6 +113,30 @@ def gemm_f64(A, B):
     N = B.shape[1]
     Cm = np.empty((M, N), np.float64)
     lib().oracle_gemm_f64(M, N, K, A, B, Cm)
+    return Cm
+
+
+def bf16(x):
+    """x rounded to bf16 as acfun_gemm_bf16 rounds its operands, widened back to fp32."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().oracle_bf16_round(x.reshape(-1), y.reshape(-1), x.size)
+    return y
+
+
+def gemm_bf16_f64(A, B):
+    """acfun_gemm_bf16's arithmetic in f64 (src/gemm_bf16_avx512.cpp:123-168):
+    its 16 x 16 micro-tiles multiply bf16-rounded operands; rows past the last
+    multiple of 16 of M and columns past the last multiple of 16 of N (its
+    256 x 128 tiles are multiples of 16) take the scalar fp32 path
+    (acfun_gemm_ref_ld) on the unrounded operands."""
+    M, N = A.shape[0], B.shape[1]
+    Cm = gemm_f64(bf16(A), bf16(B))
+    M16, N16 = M // 16 * 16, N // 16 * 16
+    if M16 < M:
+        Cm[M16:] = gemm_f64(np.ascontiguousarray(A[M16:]), B)
+    if N16 < N and M16 > 0:
+        Cm[:M16, N16:] = gemm_f64(np.ascontiguousarray(A[:M16]), np.ascontiguousarray(B[:, N16:]))
     return Cm
 
 

@@ -80,6 +80,19 @@ EXPORT void oracle_gemm_f64(int M, int N, int K, const float* A, const float* B,
     }
 }
 
+/* fp32 -> bf16 as acfun_gemm_bf16 packs its operands (src/gemm_bf16_avx512.cpp:
+ * 37-44): add 0x7fff plus bit 16 to the fp32 bits (32-bit wrap-around, so
+ * some NaNs become infinities or zero, as there), keep the upper half.  y gets
+ * the bf16 value widened back to fp32. */
+EXPORT void oracle_bf16_round(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t u;
+        memcpy(&u, &x[i], 4);
+        u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+        memcpy(&y[i], &u, 4);
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* fp32 convolution                                                          */
 /* ------------------------------------------------------------------------ */

@@ -52,3 +52,19 @@ def int8_conv_inputs(rng, N, H, W, Cin, KH, KW, Cout, bias=True):
     ws = rng.uniform(0.005, 0.05, Cout).astype(np.float32)
     b = (rng.standard_normal(Cout) * 0.01).astype(np.float32) if bias else None
     return x, wq, ws, b
+
+
+def bf16_probe_values(rng):
+    """fp32 inputs for the bf16 rounding check: ties to even and to odd, values
+    that round up to the next binade or to infinity, signed zero, infinities,
+    NaNs whose 32-bit rounding add wraps (to zero) or lands on infinity, and
+    random normals.  No denormals: vdpbf16ps reads bf16 denormals as zero."""
+    bits = np.array([0x3F808000, 0x3F818000, 0x3F80C000, 0x3F7FFFFF, 0x7F7FFFFF, 0xFF7FFFFF,
+                     0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001,
+                     0xFFFFFFFF, 0xFF800001, 0x7FFFFFFF, 0x00800000, 0x3380FFFF], np.uint32)
+    rand = rng.standard_normal(495).astype(np.float32) * np.float32(1e3)
+    return np.concatenate([bits.view(np.float32), rand])
+
+
+def same_or_both_nan(a, b):
+    return bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))

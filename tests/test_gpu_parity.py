@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import P, assert_bitexact, int8_conv_inputs, rel_err, s8, u8
+from tests.helpers import (P, assert_bitexact, bf16_probe_values, int8_conv_inputs, rel_err, s8,
+                           same_or_both_nan, u8)
 
 pytestmark = pytest.mark.gpu
 
@@ -41,22 +42,29 @@ def test_gemm_f32(gpu, rng, M, N, K, epi):
 
 
 @pytest.mark.parametrize("M,N,K", [(200, 96, 300), (64, 64, 64), (1, 1, 1), (130, 70, 7),
-                                   (1024, 1024, 1024), (33, 40, 0)])
+                                   (1024, 1024, 1024), (33, 40, 0), (7, 300, 64), (290, 5, 33)])
 def test_gemm_bf16(gpu, rng, M, N, K):
+    """acfun_gemm_bf16 against the reference's arithmetic (oracle.gemm_bf16_f64:
+    bf16 operands in the 16-aligned region, fp32 in the ragged strips, each
+    pinned to the compiled reference); K = 0 leaves C untouched."""
     A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
-    got = np.zeros((M, N), np.float32)
+    got = np.full((M, N), 7.0, np.float32)
     gpu.acfun_gemm_bf16(M, N, K, P(A), P(B), P(got))
-
-    def bf16(a):   # round to nearest even on the upper 16 bits
-        u = a.view(np.uint32).astype(np.uint64)
-        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
-        return u.astype(np.uint32).view(np.float32)
     if K == 0:
-        assert not got.any()
+        assert np.all(got == 7.0)
         return
-    want = oracle.gemm_f64(bf16(A), bf16(B))
-    assert rel_err(got, want) < 1e-5
+    assert rel_err(got, oracle.gemm_bf16_f64(A, B)) < 1e-5
+
+
+def test_gemm_bf16_rounding_exact(gpu, rng):
+    """The operand rounding bit for bit (ties, overflow to infinity, NaNs whose
+    rounding add wraps): K = 1, B = 1, all in the bf16 region, so C = bf16(A)."""
+    A = bf16_probe_values(rng).reshape(-1, 1)
+    B = np.ones((1, 16), np.float32)
+    got = np.full((A.shape[0], 16), 7.0, np.float32)
+    gpu.acfun_gemm_bf16(A.shape[0], 16, 1, P(A), P(B), P(got))
+    assert same_or_both_nan(got, np.repeat(oracle.bf16(A), 16, axis=1))
 
 
 def test_fc_and_fc_relu(gpu, rng):

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import P, assert_bitexact, f32, int8_conv_inputs, rel_err, s8, u8
+from tests.helpers import (P, assert_bitexact, bf16_probe_values, f32, int8_conv_inputs, rel_err,
+                           s8, same_or_both_nan, u8)
 
 EPI_SHAPES = [(64, 64, 64), (100, 100, 100), (255, 255, 255), (127, 129, 63), (16, 16, 16),
               (1, 16, 255), (513, 17, 131), (4, 4, 4), (33, 65, 129), (1023, 4, 7), (7, 1023, 5)]
@@ -206,6 +207,41 @@ def test_softmax_close(ref, olib, rng):
     ref.acfun_softmax(P(x), 4, 1000, P(want))
     olib.oracle_softmax(x, 4, 1000, got)
     assert rel_err(got, want) < 1e-6
+
+
+def test_bf16_rounding_against_reference(ref, rng):
+    """oracle.bf16 against the reference's own operand rounding, read back
+    exactly: with K = 1, B = 1 and M, N multiples of 16 (all in its bf16
+    micro-tiles) the reference computes C = bf16(A) * 1
+    (src/gemm_bf16_avx512.cpp:37-44), and a product with 1 is exact."""
+    A = bf16_probe_values(rng).reshape(-1, 1)
+    assert A.shape[0] % 16 == 0
+    B = np.ones((1, 16), np.float32)
+    C = np.full((A.shape[0], 16), 7.0, np.float32)
+    ref.acfun_gemm_bf16(A.shape[0], 16, 1, P(A), P(B), P(C))
+    assert same_or_both_nan(C, np.repeat(oracle.bf16(A), 16, axis=1))
+
+
+@pytest.mark.parametrize("M,N,K", [(96, 80, 200), (100, 70, 129), (7, 300, 64), (290, 5, 33)])
+def test_gemm_bf16_against_reference(ref, rng, M, N, K):
+    """The reference's bf16 GEMM against oracle.gemm_bf16_f64 (bf16 region and
+    fp32 strips), each region discriminated from the other model, and K = 0
+    leaving C untouched (src/gemm_bf16_avx512.cpp:173)."""
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C = np.empty((M, N), np.float32)
+    ref.acfun_gemm_bf16(M, N, K, P(A), P(B), P(C))
+    want = oracle.gemm_bf16_f64(A, B)
+    assert rel_err(C, want) < 1e-5
+    M16, N16 = M // 16 * 16, N // 16 * 16
+    rounded, exact = oracle.gemm_f64(oracle.bf16(A), oracle.bf16(B)), oracle.gemm_f64(A, B)
+    if M16 and N16:
+        assert rel_err(C[:M16, :N16], exact[:M16, :N16]) > 1e-4
+    if M16 < M:
+        assert rel_err(C[M16:], rounded[M16:]) > 1e-4
+    C0 = np.full((M, N), 7.0, np.float32)
+    ref.acfun_gemm_bf16(M, N, 0, P(A), P(B), P(C0))
+    assert np.all(C0 == 7.0)
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 64, 64), (127, 129, 63), (256, 64, 1024), (1, 1000, 2048)])
