@@ -230,31 +230,28 @@ __global__ __launch_bounds__(256) void k_igemm_i8(I8P p) {
 }
 
 // ---------------------------------------------------------------- k_i8mm
-// int8 implicit GEMM for the convolution routes: LDS-DMA staging, int8 MFMA,
-// and warp specialization between compute and store waves.
+// int8 implicit GEMM for the convolution routes: LDS-DMA staging and int8
+// MFMA, persistent workgroups.
 //
-// Workgroup = 512 threads, persistent.  Waves 0-3 (compute) own a BM x BN
-// output tile as 2 x 2 waves of FM x FN v_mfma_i32_32x32x32_i8 blocks (FM =
-// BM/64, FN = BN/64).  K (k' = tap*Cinp + ic) is consumed in chunks of 128
-// bytes; a stage holds A: BM rows x 8 quads of 16 bytes and B: BN rows x 8
-// quads, quad q of row r at slot r*8 + (q ^ swz(r)), swz(r) = (r ^ (r >> 3)) & 7,
-// so 8 and 16 consecutive rows read at one quad fall on distinct banks.  Both
-// are filled by buffer_load_dwordx4 ... lds: a wave instruction fills 64
-// consecutive slots (8 rows); lane l the 16 bytes of row 8I + l/8, slot l%8.
-// A's 16 bytes are 16 channels of one input pixel at one tap (NHWC s8,
-// channels padded to Cinp, a multiple of 16); a tap outside the image, a row
-// past M or a k past K reads zeros through an out-of-range offset -- s8 0 is
-// the reference's padding value u8 128.  NST stages: chunk c+NST-1 is issued
-// while chunk c is multiplied, across tile boundaries.  In k-step s (32 k)
-// lane half h reads quad 2s+h of its A and B rows with one ds_read_b128 each.
-// At a tile's last chunk the compute waves write the raw i32 accumulators
-// into one of two LDS output tiles and go on with the next tile.
-//
-// Waves 4-7 (store) drain the previous tile from LDS during the current
-// tile's chunks: they form the reference's epilogue per element, add the
-// fused residual, apply the activation and store 16-byte runs of a row.  The
-// two groups meet only at the one barrier per chunk, and the compute waves
-// issue no stores, so their waits on the DMA counter never wait for stores.
+// Workgroup = 256 threads; its waves own a BM x BN output tile as 2 x 2 waves
+// of FM x FN v_mfma_i32_32x32x32_i8 blocks (FM = BM/64, FN = BN/64).  K (k' =
+// tap*Cinp + ic) is consumed in chunks of 128 bytes; a stage holds A: BM rows
+// x 8 quads of 16 bytes and B: BN rows x 8 quads, quad q of row r at slot
+// r*8 + (q ^ swz(r)), swz(r) = (r ^ (r >> 3)) & 7, so 8 and 16 consecutive
+// rows read at one quad fall on distinct banks.  Both are filled by
+// buffer_load_dwordx4 ... lds: a wave instruction fills 64 consecutive slots
+// (8 rows); lane l the 16 bytes of row 8I + l/8, slot l%8.  A's 16 bytes are
+// 16 channels of one input pixel at one tap (NHWC s8, channels padded to
+// Cinp, a multiple of 16); a tap outside the image, a row past M or a k past
+// K reads zeros through an out-of-range offset -- s8 0 is the reference's
+// padding value u8 128.  NST stages: chunk c+NST-1 is issued while chunk c is
+// multiplied, across tile boundaries (a workgroup runs its tiles back to
+// back).  In k-step s (32 k) lane half h reads quad 2s+h of its A and B rows
+// with one ds_read_b128 each.  At a tile's last chunk each lane forms the
+// reference's epilogue for its 16 x FM x FN accumulators, adds the fused
+// residual, applies the activation and stores dwords (inline asm, so the
+// compiler's wait insertion keeps exact counts for the loads; the waits stay
+// correct with stores queued, since loads complete in issue order).
 //
 // The workgroups' tiles are cut into 8 contiguous runs, one per XCD
 // (workgroup id mod 8), so the BN-blocks of one pixel block share an L2.
@@ -349,6 +346,20 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     int abase[AIT], amask[AIT];          // fast modes: byte offset at tap 0, in-bounds taps
     int apix[AIT], aih[AIT], aiw[AIT];   // AM_GEN
     unsigned bv[BIT];
+    // Per-tile pixel decode.  A 1x1 / stride 1 / pad 0 convolution's row m is
+    // input pixel m; otherwise m -> (image, oh, ow) by float-reciprocal
+    // division while m < 2^24 (exact after udiv_small's correction).
+    const bool gemm1 = p.K == p.Cinp && p.KW == 1 && p.stride == 1 && p.pad == 0 && p.OH == p.H &&
+                       p.OW == p.W;
+    const bool small_m = p.M < (1 << 24);
+    const int ohw = p.OH * p.OW;
+    const float rohw = 1.0f / (float)ohw, row_ = 1.0f / (float)p.OW;
+    // bits [lo, hi) of 8
+    auto span8 = [](int lo, int hi) -> unsigned {
+        lo = lo > 0 ? lo : 0;
+        hi = hi < 8 ? hi : 8;
+        return hi > lo ? (1u << hi) - (1u << lo) : 0u;
+    };
     auto setup = [&](int k) {
         const int L = t0 + k * tstr;
         const int tm = L / p.gn, tn = L - tm * p.gn;
@@ -357,12 +368,23 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
             const int m = tm * BM + 8 * (wave + 4 * t) + rl;
             int pix = 0, ih0 = -(1 << 28), iw0 = 0;
             if (m < p.M) {
-                const int hw = p.OH * p.OW;
-                const int n = m / hw, rem = m - n * hw;
-                const int oh = rem / p.OW, ow = rem - oh * p.OW;
-                pix = n * p.H * p.W;
-                ih0 = oh * p.stride - p.pad;
-                iw0 = ow * p.stride - p.pad;
+                if (gemm1) {
+                    pix = m;
+                    ih0 = iw0 = 0;
+                } else {
+                    int n, oh;
+                    if (small_m) {
+                        n = udiv_small(m, ohw, rohw);
+                        oh = udiv_small(m - n * ohw, p.OW, row_);
+                    } else {
+                        n = m / ohw;
+                        oh = (m - n * ohw) / p.OW;
+                    }
+                    const int ow = m - n * ohw - oh * p.OW;
+                    pix = n * p.H * p.W;
+                    ih0 = oh * p.stride - p.pad;
+                    iw0 = ow * p.stride - p.pad;
+                }
             }
             if (AM == AM_GEN) {
                 apix[t] = pix;
@@ -371,15 +393,13 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
             } else {
                 const int q16 = AM == AM_C64 ? 16 * (aq[t] & 3) : 16 * aq[t];
                 abase[t] = m < p.M ? (pix + ih0 * p.W + iw0) * p.Cinp + q16 : 0;
-                // bit kh*8 + kw: tap (kh, kw) inside the image (KH, KW <= 8)
-                unsigned rm = 0, cm = 0;
-                for (int d = 0; d < 8; ++d) {
-                    rm |= ((unsigned)(ih0 + d) < (unsigned)p.H) ? (1u << d) : 0u;
-                    cm |= ((unsigned)(iw0 + d) < (unsigned)p.W) ? (1u << d) : 0u;
-                }
-                unsigned mk = 0;
-                for (int d = 0; d < 4; ++d) mk |= (rm >> d & 1u) ? (cm << (8 * d)) : 0u;
-                amask[t] = (int)mk;       // taps with kh < 4 (fast modes need KH <= 4)
+                // bit kh*8 + kw: tap (kh, kw) inside the image (KW <= 8, kh < 4:
+                // the fast modes need KH <= 4).  Rows and columns in range form
+                // bit spans; the kh-th byte of the mask is the column span when
+                // row kh is in range.
+                const unsigned rm = span8(-ih0, p.H - ih0), cm = span8(-iw0, p.W - iw0);
+                const unsigned rs4 = (rm & 1u) | ((rm & 2u) << 7) | ((rm & 4u) << 14) | ((rm & 8u) << 21);
+                amask[t] = (int)(rs4 * cm);
             }
         }
 #pragma unroll
@@ -486,18 +506,20 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     const bool zero = p.scal && p.scal[2] != 0.0f;
     const float sa = p.scal ? p.scal[1] : 0.0f;
     int st = 0, ck = 0, cc = 0;                 // compute cursor
-    bool stored = false;                        // stores issued since the last full wait
     float pv0[FN], pv1[FN];                     // epilogue inputs of the current tile
     int pv2[FN];
     for (int g = 0; g < nit; ++g) {
         // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
-        // chunks issued after it may stay in flight; once stores are pending
-        // the counter no longer orders them and everything is waited for.
+        // chunks issued after it may stay in flight.  A previous tile's
+        // epilogue stores may sit in the counter's queue after some of those
+        // loads: a wait that leaves only the later chunks' loads outstanding
+        // still proves chunk g landed (a store completing early cannot stand
+        // in for an older load, since the loads complete in order).  The
+        // stores are inline asm, so the compiler's own waits see loads only.
         const int later = nit - 1 - g < AHEAD - 1 ? nit - 1 - g : AHEAD - 1;
-        if (stored || later <= 0) __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+        if (later <= 0) __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
         else if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * ITEMS));
         else __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
-        stored = false;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const int L = t0 + ck * tstr;
         const int tm = L / p.gn, tn = L - tm * p.gn;
@@ -551,53 +573,80 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         }
         const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
         const bool gemm = p.epi == EPI_GEMM;
+        const bool relu1 = p.act == 1, relu2 = p.act == 2;
+        float al[FN], be[FN];
+        int corr[FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int n = n0 + wn * (BN / 2) + 32 * j + r32;
-            float al, be;
-            int corr = 0;
+            corr[j] = 0;
             if (gemm) {
-                corr = 128 * pv2[j];
+                corr[j] = 128 * pv2[j];
                 if (p.alpha) {
-                    al = pv0[j];
-                    be = pv1[j];
+                    al[j] = pv0[j];
+                    be[j] = pv1[j];
                 } else {   // src/conv_int8.cpp:100-107: alpha = sa*ws; beta = b - (alpha*128)*Sw
-                    al = __fmul_rn(sa, pv0[j]);
-                    be = __fsub_rn(pv1[j], __fmul_rn(__fmul_rn(al, 128.0f), (float)pv2[j]));
+                    al[j] = __fmul_rn(sa, pv0[j]);
+                    be[j] = __fsub_rn(pv1[j], __fmul_rn(__fmul_rn(al[j], 128.0f), (float)pv2[j]));
                 }
             } else {       // src/winograd_int8.cpp:155: (s_in*0.25)*ws, then fma with the bias
-                al = p.alpha ? pv0[j] : __fmul_rn(__fmul_rn(sa, 0.25f), pv0[j]);
-                be = pv1[j];
-            }
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                float rv[16];
-                if (p.res) {   // residual of the fused Add, all 16 loads in flight at once
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (e >> 2) + 4 * hq + (e & 3);
-                        rv[e] = (full || (m < p.M && n < p.N)) ? p.res[(long long)m * p.ldr + n] : 0.0f;
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (e >> 2) + 4 * hq + (e & 3);
-                    const int a = acc[i][j][e];
-                    acc[i][j][e] = 0;
-                    // GEMM routes: fl(fl(acc_u * alpha) + beta); Winograd route:
-                    // fmaf(4*acc_s, alpha_w, bias), with (float)(4a) = 4*(float)a exactly.
-                    // An all-zero input gives 0 without the bias (src/conv_int8.cpp:78).
-                    const float u = gemm
-                        ? __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr), al), be)
-                        : fmaf(4.0f * (float)a, al, be);
-                    float v = zero ? 0.0f : u;
-                    if (p.res) v = __fadd_rn(v, rv[e]);
-                    v = act_apply(v, p.act);
-                    if (full || (m < p.M && n < p.N)) p.Cf[(long long)m * p.ldc + n] = v;
-                }
+                al[j] = p.alpha ? pv0[j] : __fmul_rn(__fmul_rn(sa, 0.25f), pv0[j]);
+                be[j] = pv1[j];
             }
         }
-        stored = true;
+        // Lane l, register e of block (i, j) <-> row m0 + wm*BM/2 + 32i + 8(e/4) +
+        // 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32.  The element loop is
+        // straight-line: both routes' formulas and both ReLU forms are computed
+        // and selected by wave-uniform flags; only whole-tile properties (in
+        // range, fused residual) pick one of four copies of the loop.
+        const int mb = m0 + wm * (BM / 2) + 4 * hq, nb = n0 + wn * (BN / 2) + r32;
+        float* const cl = p.Cf + (long long)mb * p.ldc + nb;      // this lane's first row
+        auto tile_out = [&](auto fullc, auto resc) {
+            constexpr bool FULL = decltype(fullc)::value, RES = decltype(resc)::value;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int n = nb + 32 * j;
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    float rv[16];
+                    if (RES) {     // residual of the fused Add, all 16 loads in flight at once
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3);
+                            rv[e] = (FULL || (m < p.M && n < p.N)) ? p.res[(long long)m * p.ldr + n] : 0.0f;
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3);
+                        const int a = acc[i][j][e];
+                        acc[i][j][e] = 0;
+                        // GEMM routes: fl(fl(acc_u * alpha) + beta); Winograd route:
+                        // fmaf(4*acc_s, alpha_w, bias), with (float)(4a) = 4*(float)a exactly.
+                        // An all-zero input gives 0 without the bias (src/conv_int8.cpp:78).
+                        const float ug =
+                            __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr[j]), al[j]), be[j]);
+                        const float uw = fmaf(4.0f * (float)a, al[j], be[j]);
+                        const float u = gemm ? ug : uw;
+                        float v = zero ? 0.0f : u;
+                        if (RES) v = __fadd_rn(v, rv[e]);
+                        v = act_select(v, relu1, relu2);
+                        if (FULL || (m < p.M && n < p.N)) {
+                            float* dst = cl + (32 * i + 8 * (e >> 2) + (e & 3)) * (long long)p.ldc + 32 * j;
+                            asm volatile("global_store_dword %0, %1, off" ::"v"(dst), "v"(v) : "memory");
+                        }
+                    }
+                }
+            }
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (full) {
+            if (p.res) tile_out(T_{}, T_{});
+            else tile_out(T_{}, F_{});
+        } else {
+            if (p.res) tile_out(F_{}, T_{});
+            else tile_out(F_{}, F_{});
+        }
         cc = 0;
         ++ck;
     }
@@ -939,13 +988,13 @@ bool launch_i8(const I8P& p, bool conv, bool va, hipStream_t s) {
 }
 
 // k_i8mm tile choice.  ACFUN_I8_TILE="BMxBNxNST" overrides the tile and
-// ACFUN_I8_GRID=<workgroups per CU> caps the grid (persistent workgroups);
-// both exist for tile sweeps.
+// ACFUN_I8_GRID=<workgroups per CU> the persistent grid (0: one tile per
+// workgroup); both exist for tile sweeps.
 struct I8Tile { int bm, bn, nst, per_cu; };
 I8Tile pick_i8mm_tile(int M, int N, int K) {
     static int forced = -1;
     static I8Tile ft{64, 64, 3, 0};
-    static int grid_cap = 0;
+    static int grid_cap = 3;
     if (forced < 0) {
         forced = 0;
         if (const char* e = getenv("ACFUN_I8_TILE")) {
@@ -962,8 +1011,12 @@ I8Tile pick_i8mm_tile(int M, int N, int K) {
     if (forced == 1) {
         t = ft;
     } else {
-        // Measured on configs 3a/3b: 64 x 64 tiles (five workgroups per CU) and
-        // one tile per workgroup beat larger and persistent tiles.
+        // Measured on configs 3a/3b and the ResNet-50 int8 model: 64 x 64 tiles
+        // in three persistent workgroups per CU (each runs its tiles back to
+        // back, the next tile's chunks loading during the current one's)
+        // beat larger tiles and one tile per workgroup: the short K loops
+        // leave a one-tile workgroup too little work to cover its launch,
+        // its first loads and its epilogue.
         (void)M; (void)N;
         t = I8Tile{64, 64, (K + 127) / 128 > 2 ? 3 : 2, 0};
     }

@@ -46,6 +46,15 @@ bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_
 __device__ __forceinline__ float act_apply(float v, int act) {
     return act == 1 ? (v > 0.f ? v : 0.f) : (act == 2 ? (v < 0.f ? 0.f : v) : v);
 }
+// The same for a runtime code in a loop over many elements: both ReLU forms
+// are computed and picked by the wave-uniform flags (relu1: code 1, relu2:
+// code 2), which compiles to selects instead of branches per element.
+__device__ __forceinline__ float act_select(float v, bool relu1, bool relu2) {
+    const float r1 = v > 0.f ? v : 0.f;
+    const float r2 = v < 0.f ? 0.f : v;
+    const float r = relu2 ? r2 : v;
+    return relu1 ? r1 : r;
+}
 
 // ----------------------------------------------------------------- device
 // Initializes the current device once (verifies it is gfx950, creates the
