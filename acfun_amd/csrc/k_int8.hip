@@ -276,7 +276,12 @@ struct I8M {
     int ldc, ldr;
     int vec;             // Cf (and res) rows allow 16-byte stores/loads
     int gm, gn;          // grid in tiles
+    float* amax;         // per-workgroup max|stored value| at [blockIdx.x] (nullable)
 };
+
+// Workgroups of k_i8mm when it reports the output's absmax: its consumer's
+// quantizer reduces this many per-workgroup partials (unused ones zero).
+constexpr int kAmaxParts = kI8AmaxParts;
 
 enum { AM_GEN = 0, AM_C128 = 1, AM_C64 = 2 };
 
@@ -508,6 +513,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     int st = 0, ck = 0, cc = 0;                 // compute cursor
     float pv0[FN], pv1[FN];                     // epilogue inputs of the current tile
     int pv2[FN];
+    float amx = 0.0f;                           // max|stored value| of this lane
     for (int g = 0; g < nit; ++g) {
         // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
         // chunks issued after it may stay in flight.  A previous tile's
@@ -633,6 +639,8 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                         if (FULL || (m < p.M && n < p.N)) {
                             float* dst = cl + (32 * i + 8 * (e >> 2) + (e & 3)) * (long long)p.ldc + 32 * j;
                             asm volatile("global_store_dword %0, %1, off" ::"v"(dst), "v"(v) : "memory");
+                            const float av = fabsf(v);
+                            amx = av > amx ? av : amx;             // NaN never wins
                         }
                     }
                 }
@@ -649,6 +657,22 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         }
         cc = 0;
         ++ck;
+    }
+    // this workgroup's max|v| of the output tensor, a partial of the next
+    // layer's absmax (the reference's max|x| of its input, src/conv_int8.cpp:77)
+    if (p.amax) {
+        __shared__ float wmax[4];
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(amx, off, 64);
+            amx = o > amx ? o : amx;
+        }
+        if (lane == 0) wmax[wave] = amx;
+        __syncthreads();
+        if (tid == 0) {
+            float mm = wmax[0];
+            for (int w = 1; w < 4; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
+            p.amax[blockIdx.x] = mm;
+        }
     }
 }
 
@@ -1049,6 +1073,7 @@ bool launch_i8mm_t(I8M& p, int cap, hipStream_t s) {
         gsz = std::min(total, (long long)cap * num_cus());
         if (gsz >= 8) gsz &= ~7ll;
     }
+    if (p.amax && gsz > kAmaxParts) gsz = kAmaxParts;     // one absmax partial per workgroup
     dim3 grid((unsigned)gsz);
     ACFUN_LAUNCH("k_igemm_i8", (k_i8mm<BM, BN, NST, AM>), grid, dim3(256), lds, s, p);
     return check_launch("k_i8mm");
@@ -1171,7 +1196,8 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
 
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
-                     const I8Weights* pre, const float* res) {
+                     const I8Weights* pre, const float* res, float* amax_out,
+                     const float* amax_in) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
                       g.W >= 3 && g.Cin >= 4 && Cout >= 4;
@@ -1200,24 +1226,32 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
         float* scal = par.as<float>();
         float* part = scal + 8;
         long long n4 = (long long)(inN / 4);
-        int nb = (int)((n4 + 1023) / 1024);
-        nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
-        hipLaunchKernelGGL(k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
-                           inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, w.bt.as<int8_t>(),
-                           ldb, w.sw.as<int>());
-        if (!check_launch("k_absmax_prep")) return false;
+        // With amax_in (the producing layer folded its output's max|x| in) the
+        // absmax pass is skipped and the quantizer reads that one "partial".
+        int nb = amax_in ? 0 : (int)((n4 + 1023) / 1024);
+        if (!amax_in) nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
+        if (nb + (prepared ? 0 : Cout) > 0) {
+            hipLaunchKernelGGL(k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
+                               inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, w.bt.as<int8_t>(),
+                               ldb, w.sw.as<int>());
+            if (!check_launch("k_absmax_prep")) return false;
+        }
         const long long groups = pix * (Cinp / 16);
         hipLaunchKernelGGL(k_quant16, g1(groups), dim3(256), 0, s, in, pix, g.Cin, Cinp,
-                           q.as<int8_t>(), part, nb, scal, wino ? 2 : 0, g.Cin & ~15);
+                           q.as<int8_t>(), amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
+                           scal, wino ? 2 : 0, g.Cin & ~15);
         if (!check_launch("k_quant16")) return false;
         I8M p{};
         i8mm_conv(p, q.as<int8_t>(), g, Cinp, bt, ldb, Cout);
         p.act = act; p.scal = scal; p.ws = ws; p.bias = bias; p.Cf = out;
         p.res = res; p.ldr = Cout;
+        p.amax = amax_out;
         if (wino) p.epi = EPI_WINO;
         else { p.epi = EPI_GEMM; p.Sw = sw; }
         return launch_i8mm(p, s);
     }
+    // (operands past 32-bit offsets: amax_in is not needed, the absmax pass
+    // below runs; amax_out is filled by a pass over the output at the end)
     if (res) {
         set_error("conv2d_int8: a fused residual needs operands within 32-bit offsets");
         return false;
@@ -1258,7 +1292,15 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     } else {
         p.epi = EPI_GEMM; p.alpha = alpha; p.beta = beta; p.Sw = sw;
     }
-    return launch_i8(p, true, true, s);
+    if (!launch_i8(p, true, true, s)) return false;
+    if (amax_out) {       // the partials by a pass over the output (nb <= kAmaxParts)
+        const size_t outN = (size_t)g.N * g.OH * g.OW * Cout;
+        int nbo = (int)((outN / 4 + 1023) / 1024);
+        nbo = nbo < 1 ? 1 : (nbo > kAmaxParts ? kAmaxParts : nbo);
+        hipLaunchKernelGGL(k_absmax_part, dim3(nbo), dim3(256), 0, s, out, outN, amax_out);
+        if (!check_launch("k_absmax_part")) return false;
+    }
+    return true;
 }
 
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,

@@ -406,6 +406,18 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
     // Execute.
     std::vector<float*> buf(L, nullptr);
     std::vector<Scratch> hold(L);
+    // int8 models: per-layer slots for an output's max|v|.  An int8 conv folds
+    // its output's max into its slot (in its own epilogue); an int8 conv whose
+    // input is such a tensor quantizes with it and skips its absmax pass.
+    Scratch amx;
+    float* slot = nullptr;                           // L x kI8AmaxParts partial maxima
+    std::vector<int> amax_of(L, -1);                 // slot holding layer i's output max
+    if (m->int8 && L > 0) {
+        amx = Scratch((size_t)L * kI8AmaxParts * sizeof(float), s);
+        if (!amx.p) return 0;
+        slot = amx.as<float>();
+        if (!fill_f32(slot, (size_t)L * kI8AmaxParts, 0.0f, s)) return 0;
+    }
     auto tensor_of = [&](int idx) -> const float* { return idx < 0 ? din : buf[idx]; };
     cur = Dims{m->inH, m->inW, m->inC};
     const float* x = din;
@@ -418,6 +430,7 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         size_t cap = (size_t)N * o.H * o.W * o.C;
         if (alias[i] != -2) {                        // fused into the previous layer, or an Input
             buf[i] = const_cast<float*>(tensor_of(alias[i]));
+            if (alias[i] >= 0) amax_of[i] = amax_of[alias[i]];
             for (int j = 0; j < i; ++j)
                 if (buf[j] && last_use[j] == i && hold[j].p) { hold[j] = Scratch(); buf[j] = nullptr; }
             cur = o;
@@ -450,7 +463,11 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                 const float* res = res_of[i] != -3 ? tensor_of(res_of[i]) : nullptr;
                 ConvShape g{N, in.H, in.W, in.C, F.p[0], F.p[1], F.p[3], F.p[4], o.H, o.W};
                 if (m->int8 && F.type == 1 && F.wq) {
-                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res);
+                    const float* ain =
+                        xi >= 0 && amax_of[xi] >= 0 ? slot + (size_t)amax_of[xi] * kI8AmaxParts : nullptr;
+                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res,
+                                         slot + (size_t)i * kI8AmaxParts, ain);
+                    amax_of[i] = i;
                 } else if (res && F.p[3] == 1 && F.p[4] == 0 && M < (1ll << 31) &&
                            gemm32_ok((int)M, o.C, in.C, x, in.C, F.w, o.C)) {
                     ok = gemm32_f32((int)M, o.C, in.C, x, in.C, F.w, o.C, y, o.C, F.b, act, s, res,

@@ -204,9 +204,15 @@ bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStr
 void i8_release(I8Weights& w);
 // res (nullable): a residual [pixels][Cout] added before the activation (a
 // model's Add fused into the conv; the same two roundings as a separate Add).
+// amax_out (nullable; kI8AmaxParts floats, zeroed by the caller): per-part
+// maxima of the output's |v|, written by the producing kernel itself.
+// amax_in (nullable): such partials of the input, from its producer, used in
+// place of the absmax pass.
+constexpr int kI8AmaxParts = 768;
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
-                     const I8Weights* pre = nullptr, const float* res = nullptr);
+                     const I8Weights* pre = nullptr, const float* res = nullptr,
+                     float* amax_out = nullptr, const float* amax_in = nullptr);
 // The int8 Winograd-route entry with caller-supplied scales.
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,
                        const float* ws, const float* bias, int Cout, float s_in, float inv_s,
