@@ -43,8 +43,8 @@ struct G32Conv {
 constexpr int g32_stage(int BM, int BN) { return BM * G32_KC + G32_KC * BN; }   // floats
 constexpr int g32_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-template <int BM, int BN, int NST, bool CONV>
-__global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
+template <int BM, int BN, int NST, bool CONV, int KS>
+__global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 float* __restrict__ C,
                                                 const float* __restrict__ bias,
@@ -61,7 +61,11 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    // KS = 2: two groups of four waves split K by chunk parity (group kg takes
+    // chunks kg, kg + 2, ...) with their own stages; their accumulators are
+    // summed through LDS at the end.
+    const int kg = KS == 2 ? wave >> 2 : 0, wl = wave & 3;
+    const int wm = wl >> 1, wn = wl & 1;
     // Tile order: the 1-D grid is cut into 8 contiguous runs, one per XCD
     // (workgroup id mod 8), and within a run tiles go in groups of 4 tile rows,
     // column-major inside a group -- so the workgroups one XCD runs at a time
@@ -75,7 +79,8 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     const int r_in = L - grp * GRP * gn;
     const int tm = gbase + r_in % rows, tn = r_in / rows;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int nch = (K + G32_KC - 1) / G32_KC;
+    const int nch0 = (K + G32_KC - 1) / G32_KC;
+    const int nch = (nch0 + KS - 1) / KS;                 // chunks per group (local)
 
     // ---- DMA descriptors.  A: wave w issues instructions w + 4t (t < AIT),
     // each 4 rows x 16 quads; lane l -> row 4(w + 4t) + l/16, quad slot l%16.
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
               0x00020000);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)B, (short)0, (int)((long long)K * ldb * 4), 0x00020000);
-    const int arow = 4 * wave + (lane >> 4);               // + 16t
+    const int arow = 4 * wl + (lane >> 4);                 // + 16t
     const int aq = (lane & 15) ^ (arow & 15);              // same for every t
     const unsigned av = (unsigned)(arow * lda + 4 * aq) * 4u;
     const unsigned astep = 16u * lda * 4u;                 // 16 rows per t
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     unsigned bv[BIT];
 #pragma unroll
     for (int t = 0; t < BIT; ++t) {
-        const int slot = 64 * (wave + 4 * t) + lane;
+        const int slot = 64 * (wl + 4 * t) + lane;
         const int krow = slot / BQ;
         const int q = (slot % BQ) ^ ((krow & 32) >> 2);    // quad q of k row r at slot q ^ 8[r >= 32]
         bok[t] = n0 + 4 * q < N;
@@ -134,11 +139,13 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 
     // Every variable part of an address is in the per-lane offset (which the
     // buffer range check covers); the scalar offset stays 0.
-    auto issue = [&](int t, int c, float* st) {            // item t of chunk c into stage st
-        const int k0 = c * G32_KC;
+    auto issue = [&](int t, int c, float* st) {            // item t of (local) chunk c into stage st
+        const int k0 = (KS * c + kg) * G32_KC;
         if (t < AIT) {
             unsigned v;
-            if (CONV) {
+            if (KS > 1 && k0 >= K) {
+                v = kOOB;                                   // a group's padding chunk: zeros
+            } else if (CONV) {
                 // a 64-channel chunk lies in one tap (Cin % 64 == 0): wave-uniform
                 const int tap = k0 / cv.Cin, ic0 = k0 - tap * cv.Cin;
                 const int kh = tap / cv.KW, kw = tap - kh * cv.KW;
@@ -148,13 +155,13 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
                 v = av + (unsigned)k0 * 4u + (unsigned)t * astep;
                 if (kragged && k0 + 4 * aq >= K) v = kOOB;
             }
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wave + 4 * t) * 256),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wl + 4 * t) * 256),
                                                      16, v, 0, 0, 0);
         } else {
             const int tt = t - AIT;
-            const unsigned v = bok[tt] ? bv[tt] + (unsigned)k0 * ldb * 4u : kOOB;
+            const unsigned v = bok[tt] && k0 < K ? bv[tt] + (unsigned)k0 * ldb * 4u : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                bres, (lds_void32*)(st + SB + (wave + 4 * tt) * 256), 16, v, 0, 0, 0);
+                bres, (lds_void32*)(st + SB + (wl + 4 * tt) * 256), 16, v, 0, 0, 0);
         }
     };
 
@@ -204,11 +211,12 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 
     // NST = 3: chunk c+2 is issued while chunk c is multiplied; NST = 2: c+1.
     constexpr int AHEAD = NST - 1;
+    float* const smg = sm + kg * NST * STAGE;           // this group's stages
 #pragma unroll
-    for (int t = 0; t < ITEMS; ++t) issue(t, 0, sm);
+    for (int t = 0; t < ITEMS; ++t) issue(t, 0, smg);
     if (AHEAD == 2 && nch > 1) {
 #pragma unroll
-        for (int t = 0; t < ITEMS; ++t) issue(t, 1, sm + STAGE);
+        for (int t = 0; t < ITEMS; ++t) issue(t, 1, smg + STAGE);
     }
 
     // Software pipeline per chunk c (operands in registers):
@@ -243,12 +251,12 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
     };
     if (nch > 0) {
         wait_chunk(0);
-        read_chunk(sm);
+        read_chunk(smg);
     }
     int st = 0;
     for (int c = 0; c < nch; ++c) {
         const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
-        float* NA = sm + sta * STAGE;
+        float* NA = smg + sta * STAGE;
         const bool more = c + AHEAD < nch;
 #pragma unroll
         for (int s = 0; s < 32 - DEFER; ++s) {
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
         st = AHEAD == 2 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
         if (c + 1 < nch) {
             wait_chunk(c + 1);
-            read_chunk(sm + st * STAGE);
+            read_chunk(smg + st * STAGE);
         }
 #pragma unroll
         for (int u = 0; u < DEFER; ++u)
@@ -284,6 +292,27 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(al[i][u], bl[j][u], acc[i][j], 0, 0, 0);
+    }
+
+    if (KS == 2) {                 // group 1's sums through LDS into group 0's
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stages no longer read
+        float* const red = sm + wl * (FM * FN * 16 * 64) + lane;
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) red[((i * FN + j) * 16 + e) * 64] = acc[i][j][e];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((i * FN + j) * 16 + e) * 64];
     }
 
     // ---- epilogue: lane l, register e of block (i, j) <->
@@ -320,7 +349,7 @@ __global__ __launch_bounds__(256) void k_gemm32(const float* __restrict__ A,
 }  // namespace
 
 namespace {
-struct G32Tile { int bm, bn, nst; };
+struct G32Tile { int bm, bn, nst, ks = 1; };
 
 // Tile choice.  Measured on MI355X (config 1 and the ResNet-50 batch-64
 // layers): 64 x 64 tiles, two or three workgroups per CU, beat the 128-row
@@ -341,28 +370,33 @@ G32Tile pick_g32(int M, int N, int K) {
     }
     if (K >= kmin && N > 64 && tiles(128, 128) >= cus) return G32Tile{128, 128, 2};
     if (K >= kmin && tiles(128, 64) >= cus) return G32Tile{128, 64, nch > 2 ? 3 : 2};
+    // At most one 64 x 64 tile per CU and a long K: two four-wave groups per
+    // workgroup split K (two waves per SIMD instead of one).
+    static int ks_off = -1;
+    if (ks_off < 0) ks_off = getenv("ACFUN_G32_NOKS") ? 1 : 0;
+    if (!ks_off && nch >= 8 && tiles(64, 64) <= cus) return G32Tile{64, 64, 2, 2};
     const bool deep = nch > 2 && tiles(64, 64) < 2 * cus;
     return G32Tile{64, 64, deep ? 3 : 2};
 }
 
-template <int BM, int BN, int NST, bool CONV>
+template <int BM, int BN, int NST, bool CONV, int KS = 1>
 bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
                 int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
                 const G32Conv& cv) {
-    const int nch = (K + G32_KC - 1) / G32_KC;
-    // LDS holds only the stages that can be in use
-    const int stages = nch < NST ? (nch < 1 ? 1 : nch) : NST;
-    const size_t lds = (size_t)stages * g32_stage(BM, BN) * 4;
+    const int nch = ((K + G32_KC - 1) / G32_KC + KS - 1) / KS;
+    // LDS holds only the stages that can be in use (per group)
+    const int stages = KS > 1 ? NST : (nch < NST ? (nch < 1 ? 1 : nch) : NST);
+    const size_t lds = (size_t)KS * stages * g32_stage(BM, BN) * 4;
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV>,
+        (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV, KS>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  NST * g32_stage(BM, BN) * 4);
+                                  KS * NST * g32_stage(BM, BN) * 4);
     }
     dim3 grid((unsigned)(((N + BN - 1) / BN) * ((M + BM - 1) / BM)));
-    ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<BM, BN, NST, CONV>), grid, dim3(256), lds, s, A, B, C, bias,
-                 res, M, N, K, lda, ldb, ldc, ldr, act, cv);
+    ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<BM, BN, NST, CONV, KS>), grid, dim3(256 * KS), lds, s, A, B, C,
+                 bias, res, M, N, K, lda, ldb, ldc, ldr, act, cv);
     return check_launch("k_gemm32");
 }
 
@@ -372,6 +406,8 @@ bool launch_gemm32(int M, int N, int K, const float* A, int lda, const float* B,
                    const G32Conv& cv) {
     if (M <= 0 || N <= 0) return true;
     const G32Tile t = pick_g32(M, N, K);
+    if (t.ks == 2)
+        return launch_g32<64, 64, 2, CONV, 2>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
     if (t.bm == 128 && t.bn == 128)
         return launch_g32<128, 128, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
     if (t.bm == 128 && t.nst == 3)
