@@ -779,42 +779,45 @@ __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, lo
         scal[3] = maxa;
     }
     const int groups = Cinp >> 4;
-    const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (g >= pix * groups) return;
-    const long long pp = g / groups;
-    const int c0 = (int)(g - pp * groups) * 16;
-    const float* src = x + pp * Cin + c0;
-    float v[16];
-    if (c0 + 16 <= Cin && (((uintptr_t)src) & 15u) == 0) {
+    // grid-stride: a bounded grid, so the partials above are reduced by a
+    // bounded number of blocks
+    for (long long g = (long long)blockIdx.x * 256 + threadIdx.x; g < pix * groups;
+         g += (long long)gridDim.x * 256) {
+        const long long pp = g / groups;
+        const int c0 = (int)(g - pp * groups) * 16;
+        const float* src = x + pp * Cin + c0;
+        float v[16];
+        if (c0 + 16 <= Cin && (((uintptr_t)src) & 15u) == 0) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float4 f = ((const float4*)src)[k];
-            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = c0 + k < Cin ? src[k] : 0.0f;
-    }
-    unsigned w[4] = {0u, 0u, 0u, 0u};
-    if (!zero) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int c = c0 + k;
-            int out = 0;
-            if (c < Cin) {
-                const float t = __fmul_rn(v[k], inv_s);
-                int r;
-                if (mode == 0) r = (int)rintf(t);
-                else if (c < cvec) r = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
-                else r = (int)roundf(t);
-                int u = r + 128;
-                u = u < 0 ? 0 : (u > 255 ? 255 : u);
-                out = u - 128;
+            for (int k = 0; k < 4; ++k) {
+                float4 f = ((const float4*)src)[k];
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
             }
-            w[k >> 2] |= ((unsigned)out & 0xffu) << (8 * (k & 3));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = c0 + k < Cin ? src[k] : 0.0f;
         }
+        unsigned w[4] = {0u, 0u, 0u, 0u};
+        if (!zero) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int c = c0 + k;
+                int out = 0;
+                if (c < Cin) {
+                    const float t = __fmul_rn(v[k], inv_s);
+                    int r;
+                    if (mode == 0) r = (int)rintf(t);
+                    else if (c < cvec) r = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
+                    else r = (int)roundf(t);
+                    int u = r + 128;
+                    u = u < 0 ? 0 : (u > 255 ? 255 : u);
+                    out = u - 128;
+                }
+                w[k >> 2] |= ((unsigned)out & 0xffu) << (8 * (k & 3));
+            }
+        }
+        *(i4*)(q + pp * Cinp + c0) = i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     }
-    *(i4*)(q + pp * Cinp + c0) = i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
 
 __global__ void k_fill_u32(unsigned* p, int n, unsigned v) {
@@ -1237,7 +1240,8 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
             if (!check_launch("k_absmax_prep")) return false;
         }
         const long long groups = pix * (Cinp / 16);
-        hipLaunchKernelGGL(k_quant16, g1(groups), dim3(256), 0, s, in, pix, g.Cin, Cinp,
+        const long long qb = std::min((groups + 255) / 256, 8ll * num_cus());
+        hipLaunchKernelGGL(k_quant16, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin, Cinp,
                            q.as<int8_t>(), amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
                            scal, wino ? 2 : 0, g.Cin & ~15);
         if (!check_launch("k_quant16")) return false;

@@ -386,6 +386,20 @@ def test_wino23_batches(gpu, rng, N, Cin, Cout):
     assert_bitexact(again, got, "repeat run")
 
 
+# F(2,3) units on rectangular images whose tile grid is ragged at the right
+# and bottom edges (odd pixel counts, partial 16-tile columns), with ragged
+# input and output channel counts.
+@pytest.mark.parametrize("N,H,W,Cin,Cout", [(3, 50, 46, 24, 48), (3, 22, 54, 20, 32), (2, 64, 64, 64, 64),
+                                            (5, 41, 27, 36, 40)])
+def test_wino23_unit_shapes(gpu, rng, N, H, W, Cin, Cout):
+    x = rng.uniform(0, 1, (N, H, W, Cin)).astype(np.float32)
+    w = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2 / (9 * Cin))).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
+    got = np.full((N, H, W, Cout), np.nan, np.float32)
+    gpu.acfun_conv2d_relu(P(x), N, H, W, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(got))
+    _check_images(got, x, w, b, Cout, WINO_TOL)
+
+
 # 8-wide F(2,3) units (images 12 to 22 pixels wide): ResNet-50's 28 x 28 stage
 # (1024 units, more than the persistent grid) and a ragged 36 -> 72 conv.
 @pytest.mark.parametrize("N,HW,Cin,Cout", [(32, 28, 128, 128), (5, 22, 36, 72)])
