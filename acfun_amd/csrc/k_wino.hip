@@ -734,13 +734,20 @@ template <int TC> struct W23Row<TC, 1> { static constexpr int A = 1, B = 2, PLUS
 template <int TC> struct W23Row<TC, 2> { static constexpr int A = 2, B = 1, PLUS = 0; };
 template <int TC> struct W23Row<TC, 3> { static constexpr int A = 3, B = 1, PLUS = 0; };
 
-template <int TC>
+// A unit is NB blocks of R x TC tiles (NB * R * TC = 32, the MFMA M side).
+// With NB = 2 the blocks are separate 4 x 4-tile squares: the lanes of the
+// two alternate (tile li of the unit is tile li >> 1 of block li & 1) and
+// block 1's staging starts an odd number of 16-byte slots after block 0's, so
+// the transform reads of 16 consecutive lanes cover all 64 banks once.
+template <int TC, int NB = 1>
 struct W23Cfg {
-    static constexpr int R = 32 / TC;
+    static constexpr int R = 32 / (TC * NB);
+    static constexpr int BT = R * TC;                  // tiles per block
     static constexpr int NR = 2 * R + 2;               // staged pixel rows
     static constexpr int TCP = TC + 1;                 // kk per plane (padded)
-    static constexpr int SWZ = TC == 16 ? 3 : 2;       // swizzle bit of kk
-    static constexpr int XSLOTS = NR * 2 * TCP * 2;
+    static constexpr int SWZ = NB == 2 ? -1 : (TC == 16 ? 3 : 2);   // swizzle bit of kk (-1: none)
+    static constexpr int BS = NR * 2 * TCP * 2 + (NB == 2 ? 1 : 0);   // slots per block
+    static constexpr int XSLOTS = NB * BS;
     static constexpr int XBLK = (XSLOTS + 63) / 64;    // 64-slot DMA blocks
     static constexpr int XFL = XBLK * 256;             // floats: whole DMA blocks (the slots
                                                        // past XSLOTS load zeros, never read)
@@ -751,6 +758,8 @@ struct W23Cfg {
     static_assert(3 * LDS <= 160 * 1024, "three workgroups per CU");
     template <int WAVE>                                // X blocks wave WAVE issues per chunk
     static constexpr int nxw() { return XBLK > WAVE + 4 * (KX - 1) ? KX : KX - 1; }
+    static constexpr __device__ int swz(int kk) { return SWZ < 0 ? 0 : (kk >> SWZ) & 1; }
+    static_assert(NB * R * TC == 32, "32 tiles per unit");
 };
 
 // s_waitcnt vmcnt(n) for a wave-uniform n in 0..4 (the count is an immediate)
@@ -1062,12 +1071,12 @@ bool launch_wino23u(const float* in, const float* U, const float* bias, float* o
 // longer).  The stores are inline asm, so the compiler's own wait insertion
 // sees only loads, whose counts are exact, instead of falling back to
 // vmcnt(0) for mixed loads and stores.
-template <int TC, int ACT>
+template <int TC, int NB, int ACT>
 __global__ __launch_bounds__(256, 3) void k_wino23p(
     const float* __restrict__ in, const float* __restrict__ U, const float* __restrict__ bias,
     float* __restrict__ out, int H, int W, int Cin, int Cinp, int Cout, int rblocks, int gx, int gz,
-    int nunits, int in_bytes) {
-    using CF = W23Cfg<TC>;
+    int nunits, int in_bytes, int nblk) {
+    using CF = W23Cfg<TC, NB>;
     constexpr int R = CF::R, TCP = CF::TCP;
     constexpr unsigned kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -1095,39 +1104,65 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void*)in, (short)0, in_bytes, 0x00020000);
     const bool ragged = (Cin & 7) != 0;
-    // per-lane LDS read offsets (floats, X buffer 0)
-    const int sr = li / TC, stx = li % TC;
+    // per-lane LDS read offsets (floats, X buffer 0): tile li of the unit is
+    // tile lt of block lb
+    const int lb = NB == 2 ? (li & 1) : 0, lt = NB == 2 ? (li >> 1) : li;
+    const int sr = lt / TC, stx = lt % TC;
     int xoff[2][2];                                    // [kk = stx + jj][plane]
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
         const int kk = stx + jj;
-        const int qs = g ^ ((kk >> CF::SWZ) & 1);
+        const int qs = g ^ CF::swz(kk);
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) xoff[jj][pl] = (((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
+        for (int pl = 0; pl < 2; ++pl)
+            xoff[jj][pl] = (lb * CF::BS + ((2 * sr * 2 + pl) * TCP + kk) * 2 + qs) * 4;
     }
     // X DMA slots of this lane: block k holds slot (wave + 4k)*64 + lane ->
-    // staged pixel (row, col) of the unit's window and channel quad q.
-    // xlo[k]: the slot's byte offset from the window origin (pixel (2 ty0 - 1,
-    // 2 tx0 - 1) of the unit's image), the same for every unit.
-    auto slot_q = [&](int k) {                         // channel quad of block k's slot
+    // tile block sb, staged pixel (row, col) of that block's window and
+    // channel quad q.  xlo[k]: the slot's byte offset from the window origin
+    // (pixel (2 ty0 - 1, 2 tx0 - 1) of the block's image), the same for every
+    // unit; bit k of sbits: sb.
+    struct Slot { int sb, rp, kk, q; };
+    auto slot = [&](int k) {
         const int sl = (wave + 4 * k) * 64 + lane;
-        return (sl & 1) ^ ((((sl >> 1) % TCP) >> CF::SWZ) & 1);
+        const int sb = NB == 2 && sl >= CF::BS ? 1 : 0;
+        const int s1 = sl - sb * CF::BS;
+        const int pk = s1 >> 1;                        // (row*2 + plane)*TCP + kk
+        const int rp = pk / TCP, kk = pk - rp * TCP;
+        return Slot{sb, rp, kk, (s1 & 1) ^ CF::swz(kk)};
     };
-    unsigned xlo[CF::KX];
+    unsigned xlo[CF::KX], sbits = 0;
 #pragma unroll
     for (int k = 0; k < CF::KX; ++k) {
-        const int sl = (wave + 4 * k) * 64 + lane;
-        const int pk = sl >> 1;                        // (row*2 + plane)*TCP + kk
-        const int rp = pk / TCP, kk = pk - rp * TCP;
-        xlo[k] = (unsigned)((((rp >> 1) * W + 2 * kk + (rp & 1)) * Cin + 4 * slot_q(k)) * 4);
+        const Slot q = slot(k);
+        xlo[k] = (unsigned)((((q.rp >> 1) * W + 2 * q.kk + (q.rp & 1)) * Cin + 4 * q.q) * 4);
+        sbits |= (unsigned)q.sb << k;
     }
-    struct UnitP { int n, ty0, tx0, cob; };
+    // Block b of a unit: px, the index of its window origin pixel (2 ty0 - 1,
+    // 2 tx0 - 1) of image n (negative at the first image's top left), and the
+    // pixel rows and columns from its first output row and column to the
+    // image's edge, rl = H - 2 ty0 and cl = W - 2 tx0 (-1: no block, the
+    // last unit's second block when the block count is odd).  A staged row
+    // or column i of the window (0 = origin) is in the image when
+    // 1 - (rl < H) <= i <= rl (columns: cl, W).
+    struct UnitP { int px[NB], rl[NB], cl[NB], cob; };
     auto decode = [&](int k) {                         // k-th unit of this workgroup
         const int u = rs + i0 + k * nwx;
         const int bz = u % gz, sp = u / gz;
-        const int bx = sp % gx, by = sp / gx;
-        const int n = by / rblocks;
-        return UnitP{n, (by - n * rblocks) * R, bx * TC, bz * 32};
+        UnitP P;
+        P.cob = bz * 32;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int blk = sp * NB + b;               // block: column fastest, then image x row
+            const int bx = blk % gx, by = blk / gx;
+            const int n = by / rblocks;
+            const int ty0 = (by - n * rblocks) * R, tx0 = bx * TC;
+            const bool live = NB == 1 || blk < nblk;
+            P.px[b] = (n * H + 2 * ty0 - 1) * W + 2 * tx0 - 1;
+            P.rl[b] = live ? H - 2 * ty0 : -1;
+            P.cl[b] = live ? W - 2 * tx0 : -1;
+        }
+        return P;
     };
     // in-image bits of the lane's slots for unit P: bit k (k < KX)
     auto inimg = [&](const UnitP& P, bool live) {
@@ -1135,17 +1170,19 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
 #pragma unroll
         for (int k = 0; k < CF::KX; ++k) {
             const int sl = (wave + 4 * k) * 64 + lane;
-            const int pk = sl >> 1;
-            const int rp = pk / TCP, kk = pk - rp * TCP;
-            const int ih = 2 * P.ty0 - 1 + (rp >> 1), iw = 2 * P.tx0 - 1 + 2 * kk + (rp & 1);
-            const bool ok = live && sl < CF::XSLOTS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            const Slot q = slot(k);
+            const int rl = q.sb ? P.rl[NB - 1] : P.rl[0], cl = q.sb ? P.cl[NB - 1] : P.cl[0];
+            const int i = q.rp >> 1, jc = 2 * q.kk + (q.rp & 1);
+            const bool ok = live && sl < CF::XSLOTS && i >= (rl < H ? 0 : 1) && i <= rl &&
+                            jc >= (cl < W ? 0 : 1) && jc <= cl;
             b |= (unsigned)ok << k;
         }
         return b;
     };
-    // byte offset of unit P's window origin (negative at the image's top
-    // left; origin + xlo is in range wherever the in-image bit is set)
-    auto origin = [&](const UnitP& P) { return ((P.n * H + 2 * P.ty0 - 1) * W + 2 * P.tx0 - 1) * Cin * 4; };
+    // byte offset of block b's window origin in unit P (negative at the
+    // image's top left; origin + xlo is in range wherever the in-image bit is
+    // set)
+    auto origin = [&](const UnitP& P, int b) { return P.px[b] * Cin * 4; };
     // U(j) of unit P: this wave's 4 points; out of range (zeros, no memory
     // access) when !live
     auto ld_u = [&](const UnitP& P, bool live, int j, f4* ub) {
@@ -1158,14 +1195,16 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
     };
     // X(j) of the unit with window origin org and in-image bits ib into base:
     // blocks WAVE, WAVE+4, ...
-    auto dma_x = [&](auto wavec, int org, unsigned ib, int j, float* base) {
+    auto dma_x = [&](auto wavec, const UnitP& P, unsigned ib, int j, float* base) {
         constexpr int WAVE = decltype(wavec)::value;
         const int ci = 8 * j;
+        const int org0 = origin(P, 0), org1 = origin(P, NB - 1);
 #pragma unroll
         for (int k = 0; k < CF::KX; ++k) {
             if (WAVE + 4 * k >= CF::XBLK) continue;
+            const int org = NB == 2 && ((sbits >> k) & 1) ? org1 : org0;
             unsigned v = (ib >> k) & 1 ? (unsigned)org + xlo[k] : kOOB;
-            if (ragged && ci + 8 > Cin && ci + 4 * slot_q(k) >= Cin) v = kOOB;
+            if (ragged && ci + 8 > Cin && ci + 4 * slot(k).q >= Cin) v = kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_void*)(base + (WAVE + 4 * k) * 256), 16, v,
                                                      ci * 4, 0, 0);
         }
@@ -1191,9 +1230,9 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
         // U(0), X(0) (and the bias staging, by the barrier's lgkmcnt)
         f4 uA[4], uB[4];
         ld_u(cur, true, 0, uA);
-        dma_x(rowc, origin(cur), ib, 0, smem);
-        dma_x(rowc, origin(cur), ib, 1, smem + CF::XFL);
-        dma_x(rowc, origin(cur), ib, 2, smem + 2 * CF::XFL);
+        dma_x(rowc, cur, ib, 0, smem);
+        dma_x(rowc, cur, ib, 1, smem + CF::XFL);
+        dma_x(rowc, cur, ib, 2, smem + 2 * CF::XFL);
         wait_vmcnt(2 * NXW);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -1240,7 +1279,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             {                                          // X(j+3) into X(j)'s buffer
                 const bool in_cur = j + 3 < m;
-                dma_x(rowc, origin(in_cur ? cur : nxt), in_cur ? ib : ib >> 4, in_cur ? j + 3 : j + 3 - m,
+                dma_x(rowc, in_cur ? cur : nxt, in_cur ? ib : ib >> 4, in_cur ? j + 3 : j + 3 - m,
                       smem + xb * CF::XFL);
             }
             f4 dA[4], dB[4];
@@ -1275,9 +1314,13 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
             wait_vmcnt(NXW);
             const int ec = cur.cob + ecq;
             const f4 bq = *(const f4*)&bsm[ec < Cout ? ec : 0];
-            const int tsr = etile / TC, tsx = etile % TC;
-            const int oh0 = 2 * (cur.ty0 + tsr), ow0 = 2 * (cur.tx0 + tsx);
-            float* const orow = out + (((long long)cur.n * H + oh0) * W + ow0) * Cout + ec;
+            const int eb = NB == 2 ? (etile & 1) : 0, et = NB == 2 ? (etile >> 1) : etile;
+            const int tsr = et / TC, tsx = et % TC;
+            // output rows / columns of this tile left before the image's edge
+            const int erl = (eb ? cur.rl[NB - 1] : cur.rl[0]) - 2 * tsr;
+            const int ecl = (eb ? cur.cl[NB - 1] : cur.cl[0]) - 2 * tsx;
+            const int epx = (eb ? cur.px[NB - 1] : cur.px[0]) + (2 * tsr + 1) * W + 2 * tsx + 1;
+            float* const orow = out + (long long)(erl > 0 ? epx : 0) * Cout + ec;
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 {
@@ -1294,10 +1337,10 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
                 for (int i = 0; i < 4; ++i) S[i] = *(const f4*)&epi[(i * 32 + etile) * CF::SST + ecq];
                 // the round-1 writes must not overtake these reads
                 if (cc == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                if (ec < Cout && ow0 + cc < W) {
+                if (ec < Cout && cc < ecl) {
 #pragma unroll
                     for (int r = 0; r < 2; ++r) {
-                        if (oh0 + r >= H) continue;
+                        if (r >= erl) continue;
                         f4 v = r == 0 ? S[0] + S[1] + S[2] : S[1] - S[2] + S[3];
                         v = v + bq;
 #pragma unroll
@@ -1338,49 +1381,50 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
     }
 }
 
-template <int TC>
+template <int TC, int NB>
 size_t wino23p_lds(int Cout) {
-    return ((size_t)3 * W23Cfg<TC>::XFL + 4 * 32 * W23Cfg<TC>::SST + (size_t)(Cout + 3) / 4 * 4) *
-           sizeof(float);
+    using CF = W23Cfg<TC, NB>;
+    return ((size_t)3 * CF::XFL + 4 * 32 * CF::SST + (size_t)(Cout + 3) / 4 * 4) * sizeof(float);
 }
 
 // Persistent launch: 3 workgroups per CU (a multiple of 8 workgroups), each
 // running its share of the units.  False when the shape does not suit it
 // (fewer than 4 chunks per unit, the input past 2 GB or the LDS budget).
-template <int TC>
+template <int TC, int NB = 1>
 bool launch_wino23p(const float* in, const float* U, const float* bias, float* out, int N, int H,
                     int W, int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s,
                     bool* launched) {
-    using CF = W23Cfg<TC>;
+    using CF = W23Cfg<TC, NB>;
     *launched = false;
-    const size_t lds = wino23p_lds<TC>(Cout);
+    const size_t lds = wino23p_lds<TC, NB>(Cout);
     const long long in_bytes = (long long)N * H * W * Cin * 4;
     if (Cinp / 8 < 4 || in_bytes >= (1ll << 31) || lds * 3 > 160 * 1024) return true;
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 0>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024 / 3);
-        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024 / 3);
-        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024 / 3);
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 0>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 1>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
+        (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 2>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
     }
     const int rblocks = (tH + CF::R - 1) / CF::R;
     const long long gx = (tW + TC - 1) / TC, gy = (long long)N * rblocks, gz = (Cout + 31) / 32;
-    const long long nunits = gx * gy * gz;
+    const long long nblk = gx * gy;                    // R x TC tile blocks
+    const long long nunits = (nblk + NB - 1) / NB * gz;
     if (nunits >= (1ll << 30)) return true;
     const long long slots = 3ll * num_cus() / 8, need = (nunits + 7) / 8;
     const unsigned grid = (unsigned)(8 * (slots < need ? slots : need));
     if (act == 1)
-        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 1>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
-                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, NB, 1>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H,
+                     W, Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes, (int)nblk);
     else if (act == 2)
-        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 2>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
-                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, NB, 2>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H,
+                     W, Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes, (int)nblk);
     else
-        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, 0>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H, W,
-                     Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes);
+        ACFUN_LAUNCH("k_wino23", (k_wino23p<TC, NB, 0>), dim3(grid), dim3(256), lds, s, in, U, bias, out, H,
+                     W, Cin, Cinp, Cout, rblocks, (int)gx, (int)gz, (int)nunits, (int)in_bytes, (int)nblk);
     *launched = true;
     return check_launch("k_wino23p");
 }
@@ -1399,14 +1443,23 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     // 32-tile units (three workgroups per CU) when the image is wide enough to
     // fill them; buffer resources address one image and the filter with 32-bit
     // byte offsets.  They read the chunked filter layout.
+    // Images of at most 4 x 4 tiles (5 to 8 pixels a side, ResNet-50's 7 x 7
+    // stage) run units of two images' tile blocks.
+    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
     const bool unit32 = (long long)H * W * Cin * 4 < (1ll << 31) &&
                         16ll * Cout * Cinp * 4 < (1ll << 31) && (long long)N * ((tH + 1) / 2) < 65536 &&
-                        tW >= 6;
+                        (tW >= 6 || small);
     if (unit32) {
         ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, true>), dim3((Cout + 15) / 16, Cinp / 16),
                      dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
         if (!check_launch("k_wino_filter_t")) return false;
         bool launched = false;
+        if (small) {
+            if (!launch_wino23p<4, 2>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+                                      s, &launched))
+                return false;
+            if (launched) return true;
+        }
         if (tW >= 12) {
             if (!launch_wino23p<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
                                     s, &launched))
@@ -1494,11 +1547,13 @@ bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin,
     // Measured on MI355X at BASELINE config 2(b) (8 x 112^2 x 64 -> 64): the
     // F(2,3) unit kernel (k_wino23u) takes about half the time of k_wino_fused<4>,
     // so the F(4,3) route runs it whenever its staging conditions hold.
-    const bool unit23 = Cin % 4 == 0 && ((uintptr_t)in & 15u) == 0 && (W + 1) / 2 >= 6;
+    const int tW = (W + 1) / 2, tH = (H + 1) / 2;
+    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cin >= 32;
+    const bool unit23 = Cin % 4 == 0 && ((uintptr_t)in & 15u) == 0 && (tW >= 6 || small);
     if (tile == 4 && unit23) tile = 2;
-    // Images too narrow for the unit kernel (ResNet's 7 x 7 stage): the
-    // implicit GEMM on the LDS-DMA engine, about 3x faster there than k_wino23
-    // (which pads 7 x 7 to 8 x 8 tiles and fills few workgroups).
+    // Other images too narrow for the unit kernels: the implicit GEMM on the
+    // LDS-DMA engine.  (Images of at most 4 x 4 tiles, such as ResNet-50's
+    // 7 x 7 stage, run units of two images' tile blocks.)
     ConvShape g{N, H, W, Cin, 3, 3, 1, 1, H, W};
     if (!unit23 && conv32_ok(g, Cout, in, w)) return conv32_f32(g, in, w, bias, Cout, out, act, s);
     return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);

@@ -400,6 +400,23 @@ def test_wino23_unit_shapes(gpu, rng, N, H, W, Cin, Cout):
     _check_images(got, x, w, b, Cout, WINO_TOL)
 
 
+# Images of at most 4 x 4 tiles (5 to 8 pixels a side; ResNet-50's 7 x 7 stage)
+# run F(2,3) units of two images' 4 x 4-tile blocks: an odd image count leaves
+# the last unit's second block empty, and a single image is a unit by itself.
+@pytest.mark.parametrize("N,H,W,Cin,Cout", [(6, 7, 7, 64, 96), (5, 8, 8, 32, 40), (3, 5, 6, 36, 32),
+                                            (1, 7, 7, 512, 64)])
+def test_wino23_small_images(gpu, rng, N, H, W, Cin, Cout):
+    x = rng.uniform(0, 1, (N, H, W, Cin)).astype(np.float32)
+    w = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2 / (9 * Cin))).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
+    got = np.full((N, H, W, Cout), np.nan, np.float32)
+    gpu.acfun_conv2d_relu(P(x), N, H, W, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(got))
+    _check_images(got, x, w, b, Cout, WINO_TOL)
+    again = np.full_like(got, np.nan)
+    gpu.acfun_conv2d_relu(P(x), N, H, W, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(again))
+    assert_bitexact(again, got, "repeat run")
+
+
 # 8-wide F(2,3) units (images 12 to 22 pixels wide): ResNet-50's 28 x 28 stage
 # (1024 units, more than the persistent grid) and a ragged 36 -> 72 conv.
 @pytest.mark.parametrize("N,HW,Cin,Cout", [(32, 28, 128, 128), (5, 22, 36, 72)])
