@@ -166,7 +166,7 @@ def main():
                      "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32, 4) if achieved else None,
                      "traffic": traffic,
-                     "kernel": "k_wino23p<16,1>", "kernel_ms": round(kms, 5) if kms else None,
+                     "kernel": "k_wino23p<16,1,1>", "kernel_ms": round(kms, 5) if kms else None,
                      "work": "executed F(2,3) MFMA FLOPs 3.288 GFLOP per launch (2 * 25088 "
                              "tiles * 16 points * 64 * 64)"},
     }
