@@ -87,7 +87,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by batch with no exchange, see DESIGN.md", file=sys.stderr)
+              "the path would shard by batch with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch

@@ -87,6 +87,10 @@ CONV_CASES = [
     (2, 14, 14, 32, 1, 1, 48, 1, 0, 1, 4, GEMM_TOL),     # 1x1 zero-copy
     (2, 15, 15, 32, 1, 1, 40, 2, 0, 1, 4, GEMM_TOL),     # 1x1 strided (projection)
     (2, 30, 30, 3, 7, 7, 64, 2, 3, 1, 7, GEMM_TOL),      # conv1 7x7/2, Cin=3 (scalar A path)
+    (1, 15, 18, 3, 3, 3, 5, 2, 1, 1, 7, GEMM_TOL),       # stride 2, Cin=3, odd sizes
+    (2, 9, 10, 1, 5, 5, 4, 2, 2, 1, 7, GEMM_TOL),        # stride 2, Cin=1, 5x5
+    (1, 11, 13, 2, 3, 3, 3, 2, 0, 1, 7, GEMM_TOL),       # stride 2, Cin=2, pad 0
+    (1, 12, 12, 3, 4, 4, 4, 2, 1, 1, 7, GEMM_TOL),       # stride 2, even kernel
     (2, 16, 16, 32, 3, 3, 64, 2, 1, 1, 7, GEMM_TOL),     # 3x3/2 im2col
     (1, 9, 11, 6, 3, 3, 5, 1, 0, 1, 7, GEMM_TOL),        # 3x3 pad 0 -> im2col, odd channels
     (2, 20, 18, 16, 3, 3, 24, 1, 1, 1, 6, WINO_TOL),     # F(2,3)
