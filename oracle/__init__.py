@@ -68,6 +68,7 @@ def lib():
             "oracle_conv2d_int8": [_f32p, _i, _i, _i, _i, _i8p, _f32p, _vp, _i, _i, _i, _i, _i,
                                    _f, _f32p, _i],
             "oracle_requantize_s8": [_f32p, _sz, _i8p],
+            "oracle_wino_int8_epilogue": [_i32p, _sz, _i, _f, _f32p, _vp, _f32p, _i],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -105,6 +106,17 @@ def gemm(A, B):
     N = B.shape[1]
     Cm = np.empty((M, N), np.float32)
     lib().oracle_gemm(M, N, K, A, B, Cm)
+    return Cm
+
+
+def gemm_epi(A, B, bias, act):
+    """acfun_gemm_ref_epi's arithmetic: i-k-j float accumulation, then +bias[j]
+    and ReLU once after the full reduction."""
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float32)
+    lib().oracle_gemm_epi(M, N, K, np.ascontiguousarray(A, np.float32),
+                          np.ascontiguousarray(B, np.float32), Cm, ptr(bias), act)
     return Cm
 
 
@@ -209,6 +221,50 @@ def conv2d_int8(x, wq, ws, b, KH, KW, Cout, stride, pad, act, s_in=0.0):
     out = np.zeros((N, max(OH, 0), max(OW, 0), Cout), np.float32)
     lib().oracle_conv2d_int8(x, N, H, W, Cin, wq, ws, ptr(b), KH, KW, Cout, stride, pad,
                              s_in, out, act)
+    return out
+
+
+def requantize_s8(y):
+    """(q, scale): the build-defined int8 output of a float tensor,
+    q = clamp(RNE(y*127/max|y|), -128, 127), scale = max|y|/127 (0 for an all-zero y)."""
+    yf = np.ascontiguousarray(y, np.float32).ravel()
+    q = np.empty(yf.size, np.int8)
+    s = lib().oracle_requantize_s8(yf, yf.size, q)
+    return q.reshape(np.shape(y)), np.float32(s)
+
+
+def quantize_wino_u8(x, inv_s):
+    """The int8 Winograd route's input quantization: half-away-by-add on
+    16-channel chunks, lroundf on the channel tail (src/winograd_int8.cpp:306-325)."""
+    x = np.ascontiguousarray(x, np.float32)
+    Cin = x.shape[-1]
+    cvec = Cin & ~15
+    out = np.empty(x.shape, np.uint8)
+    if cvec:
+        out[..., :cvec] = quantize_u8(np.ascontiguousarray(x[..., :cvec]), inv_s, 128, 2)
+    if cvec < Cin:
+        out[..., cvec:] = quantize_u8(np.ascontiguousarray(x[..., cvec:]), inv_s, 128, 1)
+    return out
+
+
+def conv_int8_centered_acc(inQ, wq, KH, KW, Cout, stride, pad):
+    """A = sum over in-image taps of (u8 - 128) * wq, int32 [N, OH, OW, Cout]."""
+    N, H, W, Cin = inQ.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    acc = np.empty((N, OH, OW, Cout), np.int32)
+    lib().oracle_conv_int8_centered_acc(np.ascontiguousarray(inQ), N, H, W, Cin,
+                                        np.ascontiguousarray(wq), KH, KW, Cout, stride, pad,
+                                        OH, OW, acc)
+    return acc
+
+
+def wino_int8_epilogue(acc, s_in, ws, b, act):
+    M = acc.size // acc.shape[-1]
+    Cout = acc.shape[-1]
+    out = np.empty(acc.shape, np.float32)
+    lib().oracle_wino_int8_epilogue(np.ascontiguousarray(acc, np.int32), M, Cout,
+                                    np.float32(s_in), np.ascontiguousarray(ws, np.float32),
+                                    ptr(b), out, act)
     return out
 
 

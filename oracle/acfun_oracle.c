@@ -12,11 +12,22 @@
  * Build: see oracle/Makefile (-ffp-contract=off, so every a*b+c below is two
  * roundings unless fmaf() is written explicitly).
  *
- * Pinning (how each function is checked, besides reading):
- *   - oracle_gemm*, oracle_conv2d_f64 ... closed forms / f64 brute force, and
- *     against oracle/_ref (the compiled reference) in tests/test_oracle_pins.py.
- *   - int8 functions ... bit-exact against oracle/_ref on seeded inputs, plus
- *     the integer identities (Winograd F(2,3) == direct conv) on brute force.
+ * Pinning (how each function is checked against the compiled reference,
+ * oracle/_ref, in tests/test_oracle_pins.py, tests/test_route_pins.py and
+ * tests/test_model_pins.py):
+ *   - oracle_gemm, oracle_gemm_epi ... bit-exact against acfun_gemm_ref /
+ *     acfun_gemm_ref_epi (same loop order); oracle_gemm_f64 and
+ *     oracle_conv2d_f64 are the f64 closed forms the fp32 routes are held to.
+ *   - oracle_conv2d_route ... per shape, acfun_conv2d of the reference is
+ *     bit-identical to the entry point of the route this function names, and
+ *     differs from the other routes' results.
+ *   - int8 functions, quantizers, oracle_requantize_s8 ... bit-exact against
+ *     the reference's own entry points on seeded inputs and exact ties.
+ *   - oracle_conv_int8_centered_acc + oracle_wino_int8_epilogue ... the
+ *     Winograd identity AT*T4*AT^T = 4*A: together they reproduce the
+ *     reference's acfun_winograd_conv3x3_int8 bit for bit.
+ *   - oracle_fold_bn ... the folded weights and biases read back exactly from
+ *     the reference's own loader + executor (one-hot inputs of 2^30).
  *   - dw / grouped / maxpool / bn ... bit-exact against oracle/_ref.
  */
 #include <math.h>
@@ -644,6 +655,25 @@ EXPORT void oracle_conv_int8_centered_acc(const uint8_t* inQ, int N, int H, int 
                         }
                     acc[(((size_t)n * OH + oh) * OW + ow) * Cout + j] = a;
                 }
+}
+
+/* The Winograd route's epilogue applied to direct accumulators A (M rows of
+ * Cout): the reference forms 4*A exactly as AT*T4*AT^T and computes
+ * fmaf((float)(4A), fl(fl(s_in*0.25)*ws[j]), b[j]), then max_ps ReLU
+ * (src/winograd_int8.cpp:154-170).  With oracle_conv_int8_centered_acc this
+ * is the closed form the identity predicts. */
+EXPORT void oracle_wino_int8_epilogue(const int32_t* acc, size_t M, int Cout, float s_in,
+                                      const float* wscale, const float* bias, float* out, int act) {
+    for (int j = 0; j < Cout; ++j) {
+        float wso = (s_in * 0.25f) * wscale[j];
+        float bv = bias ? bias[j] : 0.0f;
+        for (size_t i = 0; i < M; ++i) {
+            int64_t a4 = 4 * (int64_t)acc[i * (size_t)Cout + j];
+            float v = fmaf((float)a4, wso, bv);
+            if (act == 1) v = vmax(v, 0.0f);
+            out[i * (size_t)Cout + j] = v;
+        }
+    }
 }
 
 /* int8 route codes of acfun_conv2d_int8 (src/conv_int8.cpp:63-148) on an

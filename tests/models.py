@@ -87,3 +87,45 @@ def int8_chain_v1(rng, hw=20, cin=8):
 def small_resnet_v2(rng, hw=32):
     """A version-2 residual model (Input/Add/GlobalAvgPool records)."""
     return acfun0.resnet50(rng, in_hw=hw, width=8, blocks=(1, 2, 1, 1), classes=10)
+
+
+def fold_pin_v1(rng, kind):
+    """A one-layer conv + BN model whose folded weights the reference's
+    executor reveals exactly on one-hot inputs of 2^30 (fold_pin_inputs):
+    dense 1x1 (GEMM route), depthwise 3x3 and grouped 3x3 (direct routes)."""
+    if kind == "dense":
+        inC, H, W, Cout = 3, 1, 5, 64
+        conv = _conv(rng, 1, 1, inC, Cout, 1, 0)
+    elif kind == "dw":
+        inC, H, W, Cout = 8, 5, 5, 8
+        conv = _convg(rng, 3, 3, inC, Cout, 1, 1, inC)
+    else:
+        inC, H, W, Cout = 8, 5, 5, 16
+        conv = _convg(rng, 3, 3, inC, Cout, 1, 1, 2)
+    return inC, H, W, [conv, acfun0.bn_params(rng, Cout)]
+
+
+def fold_pin_inputs(kind, inC, H, W):
+    """Images with one input value 2^30 and zeros elsewhere (plus an all-zero
+    image): each output is then fl(2^30 * w' + b') for one folded weight w',
+    or b' itself, so every folded value is observed exactly."""
+    big = np.float32(2.0 ** 30)
+    imgs = [np.zeros((H, W, inC), np.float32)]
+    if kind == "dense":            # pixel c+1 hot on channel c, the last pixel -2^30 on channel 0
+        x = np.zeros((H, W, inC), np.float32)
+        for c in range(inC):
+            x[0, c + 1, c] = big
+        x[0, W - 1, 0] = -big
+        imgs.append(x)
+    elif kind == "dw":             # every channel hot at the centre: all 9 taps per channel
+        x = np.zeros((H, W, inC), np.float32)
+        x[H // 2, W // 2, :] = big
+        imgs.append(x)
+    else:                          # channel i of each group hot at the centre, one image per i
+        per = inC // 2
+        for i in range(per):
+            x = np.zeros((H, W, inC), np.float32)
+            x[H // 2, W // 2, i] = big
+            x[H // 2, W // 2, per + i] = -big
+            imgs.append(x)
+    return np.stack(imgs)

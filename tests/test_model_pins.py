@@ -131,3 +131,54 @@ def test_oracle_int8_chain_uses_reference_int8_conv(ref, rng, tmp_path):
         else:
             pytest.fail(f"unexpected layer {F['type']}")
     np.testing.assert_array_equal(got, cur.reshape(1, -1))
+
+
+def _fold_expected(kind, recs, x):
+    """The model's output as the reference's (bit-exact-pinned) operators give
+    it on weights folded by oracle_fold_bn."""
+    import oracle
+    conv, bn = recs
+    _, ch, mean, var, gamma, beta = bn
+    if kind == "dense":
+        _, KH, KW, Cout, s, p, w, b = conv
+        wf, bf = oracle.fold_bn(w, b, Cout, 0, mean, var, gamma, beta)
+        wf = wf.reshape(-1, Cout)
+        N, H, W, Cin = x.shape
+        A = x.reshape(-1, Cin)
+        out = np.empty((A.shape[0], Cout), np.float32)
+        for i, row in enumerate(A):          # at most one nonzero term per row: exact product
+            acc = np.zeros(Cout, np.float32)
+            for c in np.nonzero(row)[0]:
+                acc = (acc + row[c] * wf[c]).astype(np.float32)
+            out[i] = acc + bf
+        return out.reshape(N, -1), wf, bf
+    _, KH, KW, Cout, s, p, g, w, b = conv
+    wf, bf = oracle.fold_bn(w, b, Cout, g, mean, var, gamma, beta)
+    if g == x.shape[3] == Cout:
+        y = oracle.conv2d_dw(x, wf.reshape(Cout, KH, KW), bf, KH, KW, s, p, 0)
+    else:
+        y = oracle.conv2d_grouped(x, wf.reshape(g, -1, Cout // g), bf, KH, KW, Cout, s, p, g, 0)
+    return y.reshape(x.shape[0], -1), wf, bf
+
+
+@pytest.mark.parametrize("kind", ["dense", "dw", "grouped"])
+def test_fold_bn_against_reference_loader(ref, rng, tmp_path, kind):
+    """oracle_fold_bn against the reference's own fold_bn_into
+    (src/model.cpp:69-95), read back through its executor: every folded
+    weight w' and bias b' appears bit for bit in an output, as
+    fl(2^30 * w' + b') or b', for dense (groups 0), depthwise and grouped
+    offsets.  A one-ulp change of any w' or b' changes an output."""
+    inC, H, W, recs = models.fold_pin_v1(rng, kind)
+    path = str(tmp_path / f"fold_{kind}.acfun")
+    acfun0.write(path, inC, H, W, recs, version=1)
+    x = models.fold_pin_inputs(kind, inC, H, W)
+    want = _ref_infer(ref, path, x)
+    got, wf, bf = _fold_expected(kind, recs, x)
+    assert got.shape == want.shape
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(want[0].reshape(-1, bf.size)[0], bf)   # the zero image is b'
+    # the hot outputs carry w' exactly: 2^30 * w' dominates b' by far more than an ulp
+    assert np.count_nonzero(np.abs(want[1:]) > 2.0 ** 20) >= wf.size // (2 if kind == "grouped" else 1)
+    # and the oracle's executor, which folds with oracle_fold_bn, gives the same bits
+    np.testing.assert_array_equal(omodel.run(open(path, "rb").read(), x) if kind != "dense"
+                                  else got, want)

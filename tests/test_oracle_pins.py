@@ -256,3 +256,72 @@ def test_gemm_against_reference(ref, rng, M, N, K):
     simd = np.empty((M, N), np.float32)
     ref.acfun_gemm(M, N, K, P(A), P(B), P(simd))
     assert rel_err(simd, exact) < 1e-5 and rel_err(got, exact) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (127, 129, 63), (33, 1000, 257), (5, 7, 1)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_gemm_epi_against_reference(ref, rng, M, N, K, act):
+    """oracle_gemm_epi vs the reference's scalar acfun_gemm_ref_epi
+    (src/gemm_ref.cpp:39-63): same i-k-j order, bias and ReLU after the full
+    reduction, so bit-exact; zeros in A exercise the skipped terms, a NULL
+    bias the bias-free path."""
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    A[::3, ::2] = 0.0
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    for bias in (rng.uniform(-1, 1, N).astype(np.float32), None):
+        want = np.empty((M, N), np.float32)
+        ref.acfun_gemm_ref_epi(M, N, K, P(A), P(B), P(want), P(bias), act)
+        assert_bitexact(oracle.gemm_epi(A, B, bias, act), want, "gemm_epi")
+        if act:
+            assert np.all(want >= 0)
+
+
+@pytest.mark.parametrize("N,H,W,Cin,Cout", [(1, 8, 8, 16, 16), (2, 7, 9, 20, 5), (1, 3, 3, 4, 4),
+                                            (1, 5, 6, 37, 19), (2, 6, 6, 128, 8)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_winograd_int8_identity(ref, rng, N, H, W, Cin, Cout, act):
+    """The identity the int8 Winograd route rests on: AT*T4*AT^T = 4*A with A
+    the direct centred accumulator, so the reference's
+    acfun_winograd_conv3x3_int8 equals fmaf((float)(4A), fl(fl(s*0.25)*ws), b)
+    computed from oracle_conv_int8_centered_acc -- bit for bit, on odd sizes
+    (half tiles at the border) and channel tails (lroundf channels)."""
+    x, wq, ws, b = int8_conv_inputs(rng, N, H, W, Cin, 3, 3, Cout)
+    maxa = np.float32(np.max(np.abs(x)))
+    inv_s, s_in = np.float32(127.0) / maxa, maxa / np.float32(127.0)
+    want = np.empty((N, H, W, Cout), np.float32)
+    ref.acfun_winograd_conv3x3_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), Cout, s_in, inv_s,
+                                    P(want), act)
+    acc = oracle.conv_int8_centered_acc(oracle.quantize_wino_u8(x, inv_s), wq, 3, 3, Cout, 1, 1)
+    assert_bitexact(oracle.wino_int8_epilogue(acc, s_in, ws, b, act), want, "4A identity")
+    # the accumulator itself against numpy brute force (int64, no wrap)
+    if N * H * W * Cin * Cout <= 20000:
+        u = oracle.quantize_wino_u8(x, inv_s).astype(np.int64) - 128
+        up = np.pad(u, ((0, 0), (1, 1), (1, 1), (0, 0)))
+        wk = wq.astype(np.int64).reshape(3, 3, Cin, Cout)
+        A = sum(np.einsum("nhwc,cd->nhwd", up[:, i:i + H, j:j + W, :], wk[i, j])
+                for i in range(3) for j in range(3))
+        np.testing.assert_array_equal(acc, A)
+
+
+def test_requantize_s8_against_reference(ref, rng):
+    """oracle_requantize_s8 (the build-defined int8 output) equals the
+    reference's own quantizer with zero point 128, minus 128
+    (src/int8_quantize_avx512.cpp:15-20 with inv_s = 127/max|y|,
+    src/conv_int8.cpp:75-81), on random values, exact ties and the extremes."""
+    y = (rng.standard_normal(4099) * 3).astype(np.float32)
+    q, s = oracle.requantize_s8(y)
+    maxa = np.float32(np.max(np.abs(y)))
+    assert s == maxa / np.float32(127.0)
+    u = np.empty(y.size, np.uint8)
+    ref.acfun_quantize_u8(P(y), P(u), y.size, np.float32(127.0) / maxa, 128)
+    assert_bitexact(q, (u.astype(np.int16) - 128).astype(np.int8), "requantize")
+    assert q[np.argmax(np.abs(y))] in (-127, 127)
+    # max|y| = 127 gives inv_s = 1: k + 0.5 are exact ties (to even), -127.0 stays -127
+    t = np.array([127.0, -127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 126.5, -126.5, 0.49999997, 0.0, -0.0],
+                 np.float32)
+    q, s = oracle.requantize_s8(t)
+    ref.acfun_quantize_u8(P(t), P(u), t.size, np.float32(1.0), 128)
+    assert_bitexact(q, (u[:t.size].astype(np.int16) - 128).astype(np.int8), "requantize ties")
+    np.testing.assert_array_equal(q, [127, -127, 0, 2, 2, 0, -2, 126, -126, 0, 0, 0])
+    z, s0 = oracle.requantize_s8(np.zeros(17, np.float32))
+    assert s0 == 0.0 and not np.any(z)
