@@ -83,7 +83,7 @@ def bn_params(rng, ch, gamma_lo=0.5, gamma_hi=1.5):
     return ("bn", ch, mean, var, gamma, beta)
 
 
-def resnet50(rng, in_hw=224, width=64, blocks=(3, 4, 6, 3), classes=1000, in_ch=3):
+def resnet50(rng, in_hw=224, width=64, blocks=(3, 4, 6, 3), classes=1000, in_ch=3, head=True):
     """ResNet-50 v1.5 (stride on the 3x3), random init, as version-2 records.
 
     conv1 7x7/2 -> BN -> 3x3/2 MaxPool -> ReLU (MaxPool absorbs the ReLU, so the
@@ -92,7 +92,8 @@ def resnet50(rng, in_hw=224, width=64, blocks=(3, 4, 6, 3), classes=1000, in_ch=
     with Conv+BN+ReLU fused at load, projection shortcuts on each stage's first
     block, global average pool, FC and softmax.  The last BN of each residual
     branch draws gamma from U[0.1,0.3] so activations stay O(1) through the
-    16 residual additions of a random-init network.
+    16 residual additions of a random-init network.  head=False ends the
+    model at the last block's Add+ReLU (no pool, FC or softmax).
     """
     R = []
 
@@ -128,6 +129,8 @@ def resnet50(rng, in_hw=224, width=64, blocks=(3, 4, 6, 3), classes=1000, in_ch=
             else:
                 last = add(("add", block_in, 1))
             cin = cout
+    if not head:
+        return in_ch, in_hw, in_hw, R
     add(("gap",))
     fcw = (rng.standard_normal((cin, classes)) / np.sqrt(cin)).astype(np.float32)
     add(("fc", classes, cin, fcw, np.zeros(classes, np.float32)))

@@ -10,7 +10,10 @@
 // shape, and writes them to $HOME/.cache/acfun_amd/tune_gfx950.txt, which
 // later processes read at first use.  ACFUN_AUTOTUNE=1 runs the search at the
 // first GEMM of a process.
+#include <sys/stat.h>
+
 #include <algorithm>
+#include <cerrno>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -51,11 +54,20 @@ void load_cache_locked() {
     if (n) g_status = "tile table from cache " + cache_path() + " (" + std::to_string(n) + " shapes)";
 }
 
+// mkdir -p with mkdir(2) on each path component (no shell, no child process).
+bool make_dirs(const std::string& dir) {
+    for (size_t i = 1; i <= dir.size(); ++i) {
+        if (i < dir.size() && dir[i] != '/') continue;
+        const std::string part = dir.substr(0, i);
+        if (mkdir(part.c_str(), 0755) != 0 && errno != EEXIST) return false;
+    }
+    struct stat st;
+    return stat(dir.c_str(), &st) == 0 && S_ISDIR(st.st_mode);
+}
+
 void save_cache_locked() {
     std::string p = cache_path();
-    std::string dir = p.substr(0, p.rfind('/'));
-    std::string mk = "mkdir -p '" + dir + "'";
-    if (std::system(mk.c_str()) != 0) return;
+    if (!make_dirs(p.substr(0, p.rfind('/')))) return;
     FILE* f = fopen(p.c_str(), "w");
     if (!f) return;
     for (auto& kv : g_table)

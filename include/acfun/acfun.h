@@ -195,13 +195,19 @@ int acfun_dev_softmax(const float* input, int rows, int cols, float* output, voi
 
 /* acfun_model_load with options: flags & 1 quantizes every dense conv (type 1)
  * to int8 at load (per-output-channel weights, acfun_quantize_weights rule) and
- * runs it through the acfun_conv2d_int8 path with a per-batch dynamic
- * activation scale; other layers stay fp32. */
+ * runs it through the acfun_conv2d_int8 rules; other layers stay fp32.  The
+ * activation scale of each int8 conv is dynamic and per tensor, i.e. max|x|
+ * over the whole batch, exactly as acfun_conv2d_int8 computes it for an N-image
+ * input (src/conv_int8.cpp:75-81 of the reference). */
 AcfunModel* acfun_model_load_ex(const char* path, int flags);
 
-/* Batched inference: input [N, inH, inW, inC], output [N, outSize].  Each image
- * gives the same result as acfun_model_infer on it alone.  Returns outSize
- * (per image), 0 on error. */
+/* Batched inference: input [N, inH, inW, inC], output [N, outSize].  Returns
+ * outSize (per image), 0 on error.  For fp32 models each image's result is
+ * that of acfun_model_infer on it alone, up to the kernels' fp32 rounding (the
+ * arithmetic per output element does not depend on the batch).  For int8
+ * models (acfun_model_load_ex flags & 1) it is not: every int8 conv quantizes
+ * its input with one scale for the whole batch, so an image's result depends
+ * on the other images of its batch; with N = 1 it is acfun_model_infer's. */
 int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* output);
 /* The same on device pointers, queued on `stream` (not synchronized). */
 int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float* output,

@@ -5,8 +5,11 @@ record parser (:130-196), the load-time fusion (:199-247: BN folded by
 fold_bn_into, ReLU fused, a ReLU before MaxPool dropped, MaxPool absorbing a
 following ReLU) and the layer loop (:274-349), run on the oracle operators.
 Version-2 residual records (Add/GlobalAvgPool/Input) follow the definitions
-the library documents for them.  Batched: image n of a batch equals a batch-1
-run on image n (softmax per image, as the reference runs rows=1 per image).
+the library documents for them.  Batched: for fp32 models image n of a batch
+equals a batch-1 run on image n (softmax per image, as the reference runs
+rows=1 per image).  In int8 mode every conv is acfun_conv2d_int8 on the whole
+batch, whose activation scale is max|x| over all images (src/conv_int8.cpp:75-81),
+so an image's int8 result depends on its batch.
 """
 import struct
 

@@ -87,11 +87,12 @@ def test_model_device_batch(gpu, rng, tmp_path):
     try:
         host = np.full((3, 10), np.nan, np.float32)
         assert gpu.acfun_model_infer_batch(m, 3, P(x), P(host)) == 10
-        dx = torch.from_numpy(x).cuda()
-        dy = torch.full((3, 10), float("nan"), device="cuda")
-        s = torch.cuda.current_stream()
-        assert gpu.acfun_dev_model_infer_batch(m, 3, dx.data_ptr(), dy.data_ptr(),
-                                               s.cuda_stream) == 10
+        s = torch.cuda.Stream()               # non-null: NULL would mean the library's stream
+        with torch.cuda.stream(s):
+            dx = torch.from_numpy(x).cuda()
+            dy = torch.full((3, 10), float("nan"), device="cuda")
+            assert gpu.acfun_dev_model_infer_batch(m, 3, dx.data_ptr(), dy.data_ptr(),
+                                                   s.cuda_stream) == 10
         s.synchronize()
     finally:
         gpu.acfun_model_destroy(m)
@@ -156,3 +157,30 @@ def test_resnet50_224_matches_oracle(gpu, rng, tmp_path, int8):
     want = omodel.run(open(path, "rb").read(), x, int8=int8)
     assert rel_err(got, want) < TOL, rel_err(got, want)
     assert abs(float(got.sum()) - 1.0) < 1e-4
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_resnet50_headless_batch8(gpu, rng, tmp_path, int8):
+    """Config 5's graph without its head (the output is the last block's
+    Add+ReLU, 7 x 7 x 2048 per image) at batch 8.  int8: bit-exact against the
+    oracle's chain of acfun_conv2d_int8 calls on the whole batch (one dynamic
+    activation scale per tensor over the 8 images), which covers the fused
+    residual epilogue and the producer-to-consumer absmax handoff of every
+    block; fp32 within the Winograd tolerance."""
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5), head=False)
+    path = _write(tmp_path, "r50h.acfun", inC, H, W, recs, 2)
+    n = 8
+    x = rng.uniform(0, 1, (n, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path, 1 if int8 else 0)
+    try:
+        got = np.full((n, 7 * 7 * 2048), np.nan, np.float32)
+        assert gpu.acfun_model_infer_batch(m, n, P(x), P(got)) == got.shape[1], capi.last_error()
+    finally:
+        gpu.acfun_model_destroy(m)
+    print("oracle ResNet-50 batch", n, "int8" if int8 else "fp32", flush=True)
+    want = omodel.run(open(path, "rb").read(), x, int8=int8)
+    assert np.count_nonzero(want) > want.size // 4          # ReLU leaves a live tensor
+    if int8:
+        assert_bitexact(got, want, "int8 ResNet-50 body, batch 8")
+    else:
+        assert rel_err(got, want) < TOL, rel_err(got, want)

@@ -459,7 +459,10 @@ def test_device_pointer_variants(gpu, rng):
     want = oracle.conv2d_int8(x, wq, ws, b, 3, 3, 32, 1, 1, 1)
     tx, tw, ts, tb = (torch.from_numpy(a).to(dev) for a in (x, wq, ws, b))
     ty = torch.full((2, 14, 14, 32), float("nan"), device=dev)
-    stream = torch.cuda.current_stream().cuda_stream
+    # NULL: the library's own stream, which does not wait for torch's null
+    # stream -- so the operands are made complete first
+    stream = None
+    torch.cuda.synchronize()
     rc = gpu.acfun_dev_conv2d_int8(tx.data_ptr(), 2, 14, 14, 64, tw.data_ptr(), ts.data_ptr(),
                                    tb.data_ptr(), 3, 3, 32, 1, 1, ty.data_ptr(), 1, stream)
     torch.cuda.synchronize()
@@ -473,6 +476,7 @@ def test_device_pointer_variants(gpu, rng):
     A = torch.rand(300, 200, device=dev)
     B = torch.rand(200, 100, device=dev)
     Cm = torch.zeros(300, 100, device=dev)
+    torch.cuda.synchronize()
     assert gpu.acfun_dev_gemm_epi(300, 100, 200, A.data_ptr(), B.data_ptr(), Cm.data_ptr(), None, 0,
                                   stream) == 0
     torch.cuda.synchronize()
