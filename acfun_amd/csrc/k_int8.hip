@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 
 namespace acfun {
 namespace {
@@ -1197,9 +1198,11 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
     return launch_i8(p, true, true, s);
 }
 
-bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
-                     const float* bias, int Cout, float* out, int act, hipStream_t s,
-                     const I8Weights* pre, const float* res, float* amax_out,
+namespace {
+// acfun_conv2d_int8 on device with every temporary taken from `ar`.
+bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
+                     const float* bias, int Cout, float* out, int act, hipStream_t s, Arena& ar,
+                     bool region, const I8Weights* pre, const float* res, float* amax_out,
                      const float* amax_in) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
@@ -1207,26 +1210,29 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     int Cinp = rup(g.Cin, 16);
     long long pix = (long long)g.N * g.H * g.W;
     size_t inN = (size_t)pix * g.Cin;
-    PrepW w;
     const int8_t* bt;
     const int* sw;
+    int8_t* nbt = nullptr;       // weights prepared by this call
+    int* nsw = nullptr;
     int ldb;
     const bool prepared = pre && pre->bt && pre->taps == g.KH * g.KW && pre->Cin == g.Cin &&
                           pre->N == Cout;
     if (prepared) {
         bt = pre->bt; sw = pre->sw; ldb = pre->ldb;
     } else {
-        if (!alloc_weights(g.KH * g.KW, Cinp, Cout, s, w)) return false;
-        bt = w.bt.as<int8_t>(); sw = w.sw.as<int>(); ldb = w.ldb;
+        ldb = rup(g.KH * g.KW * Cinp, 128);
+        nbt = (int8_t*)ar.get((size_t)Cout * ldb);
+        nsw = (int*)ar.get((size_t)Cout * sizeof(int));
+        if (!nbt || !nsw) return false;
+        bt = nbt; sw = nsw;
     }
     if (i8mm_fits(pix * Cinp, Cout, ldb)) {
         // absmax partials -> quantize (reduces them, writes the scalars) -> k_i8mm,
         // whose epilogue forms the per-channel factors from the scalars
         constexpr int kParts = 512;
-        Scratch par((size_t)(8 + kParts) * sizeof(float), s);
-        Scratch q((size_t)pix * Cinp, s);
-        if (!par.p || !q.p) return false;
-        float* scal = par.as<float>();
+        float* scal = (float*)ar.get((size_t)(8 + kParts) * sizeof(float));
+        int8_t* q = (int8_t*)ar.get((size_t)pix * Cinp);
+        if (!scal || !q) return false;
         float* part = scal + 8;
         long long n4 = (long long)(inN / 4);
         // With amax_in (the producing layer folded its output's max|x| in) the
@@ -1235,18 +1241,17 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
         if (!amax_in) nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
         if (nb + (prepared ? 0 : Cout) > 0) {
             hipLaunchKernelGGL(k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
-                               inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, w.bt.as<int8_t>(),
-                               ldb, w.sw.as<int>());
+                               inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, nbt, ldb, nsw);
             if (!check_launch("k_absmax_prep")) return false;
         }
         const long long groups = pix * (Cinp / 16);
         const long long qb = std::min((groups + 255) / 256, 8ll * num_cus());
         hipLaunchKernelGGL(k_quant16, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin, Cinp,
-                           q.as<int8_t>(), amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
+                           q, amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
                            scal, wino ? 2 : 0, g.Cin & ~15);
         if (!check_launch("k_quant16")) return false;
         I8M p{};
-        i8mm_conv(p, q.as<int8_t>(), g, Cinp, bt, ldb, Cout);
+        i8mm_conv(p, q, g, Cinp, bt, ldb, Cout);
         p.act = act; p.scal = scal; p.ws = ws; p.bias = bias; p.Cf = out;
         p.res = res; p.ldr = Cout;
         p.amax = amax_out;
@@ -1256,20 +1261,23 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
     }
     // (operands past 32-bit offsets: amax_in is not needed, the absmax pass
     // below runs; amax_out is filled by a pass over the output at the end)
+    if (region) {
+        set_error("conv2d_int8: operands past 32-bit offsets need the allocating entry point");
+        return false;
+    }
     if (res) {
         set_error("conv2d_int8: a fused residual needs operands within 32-bit offsets");
         return false;
     }
     if (!prepared) {
         hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
-                           Cinp, Cout, w.bt.as<int8_t>(), ldb, w.sw.as<int>());
+                           Cinp, Cout, nbt, ldb, nsw);
         if (!check_launch("k_prep_weights")) return false;
     }
     // device block: [0..3] scalars+maxbits, then alpha, beta, alpha_w
-    Scratch par((size_t)(8 + 3 * Cout) * sizeof(float), s);
-    Scratch q((size_t)pix * Cinp, s);
-    if (!par.p || !q.p) return false;
-    float* scal = par.as<float>();
+    float* scal = (float*)ar.get((size_t)(8 + 3 * Cout) * sizeof(float));
+    int8_t* q = (int8_t*)ar.get((size_t)pix * Cinp);
+    if (!scal || !q) return false;
     unsigned* bits = (unsigned*)(scal + 4);
     float* alpha = scal + 8;
     float* beta = alpha + Cout;
@@ -1284,10 +1292,10 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
                        Cout, alpha, beta, alpha_w, scal);
     if (!check_launch("k_int8_params")) return false;
     hipLaunchKernelGGL(k_quant_act, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp,
-                       q.as<int8_t>(), scal, wino ? 2 : 0, g.Cin & ~15);
+                       q, scal, wino ? 2 : 0, g.Cin & ~15);
     if (!check_launch("k_quant_act")) return false;
     I8P p{};
-    p.A = q.as<int8_t>(); p.Bt = bt; p.M = g.N * g.OH * g.OW; p.N = Cout;
+    p.A = q; p.Bt = bt; p.M = g.N * g.OH * g.OW; p.N = Cout;
     p.K = g.KH * g.KW * Cinp; p.ldb = ldb;
     p.H = g.H; p.W = g.W; p.Cinp = Cinp; p.KW = g.KW; p.stride = g.stride; p.pad = g.pad;
     p.OH = g.OH; p.OW = g.OW; p.act = act; p.scal = scal; p.Cf = out; p.ldc = Cout;
@@ -1305,6 +1313,70 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
         if (!check_launch("k_absmax_part")) return false;
     }
     return true;
+}
+
+// The file-scope scratch of the allocation-free entry point: one copy per
+// device, for the life of the process.  Host code never passes `scratch`
+// itself to a kernel: its device address on the current device comes from
+// hipGetSymbolAddress (noalloc_region), taken once per device.
+constexpr size_t kNoAllocBytes = size_t(64) << 20;
+__device__ __align__(256) char scratch[kNoAllocBytes];
+
+constexpr int kNoAllocDev = 16;
+void* g_scratch_ptr[kNoAllocDev] = {};
+std::mutex g_scratch_mu;
+
+void* noalloc_region() {
+    int d = -1;
+    if (!check(hipGetDevice(&d), "hipGetDevice")) return nullptr;
+    if (d < 0 || d >= kNoAllocDev) {
+        set_error("device %d: no scratch slot", d);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[d]) {
+        void* ptr = nullptr;
+        if (!check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+            return nullptr;
+        g_scratch_ptr[d] = ptr;
+    }
+    return g_scratch_ptr[d];
+}
+}  // namespace
+
+bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
+                     const float* bias, int Cout, float* out, int act, hipStream_t s,
+                     const I8Weights* pre, const float* res, float* amax_out,
+                     const float* amax_in) {
+    Arena ar(s);
+    return conv2d_int8_run(in, g, wq, ws, bias, Cout, out, act, s, ar, false, pre, res, amax_out,
+                           amax_in);
+}
+
+size_t conv2d_int8_noalloc_need(const ConvShape& g, int Cout) {
+    const int Cinp = rup(g.Cin, 16);
+    const size_t ldb = (size_t)rup(g.KH * g.KW * Cinp, 128);
+    return Arena::aligned((size_t)Cout * ldb) + Arena::aligned((size_t)Cout * sizeof(int)) +
+           Arena::aligned((size_t)(8 + 512) * sizeof(float)) +
+           Arena::aligned((size_t)g.N * g.H * g.W * Cinp);
+}
+
+size_t conv2d_int8_noalloc_max() { return kNoAllocBytes; }
+
+bool conv2d_int8_noalloc(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
+                         const float* bias, int Cout, float* out, int act, hipStream_t s) {
+    if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
+    const size_t need = conv2d_int8_noalloc_need(g, Cout);
+    if (need > kNoAllocBytes) {
+        set_error("conv2d_int8_noalloc: this shape needs %zu bytes of scratch, more than the "
+                  "%zu-byte static region (use acfun_dev_conv2d_int8)", need, kNoAllocBytes);
+        return false;
+    }
+    void* region = noalloc_region();
+    if (!region) return false;
+    Arena ar(s, region, kNoAllocBytes);
+    return conv2d_int8_run(in, g, wq, ws, bias, Cout, out, act, s, ar, true, nullptr, nullptr,
+                           nullptr, nullptr);
 }
 
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,

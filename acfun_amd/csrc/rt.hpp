@@ -94,6 +94,28 @@ struct Scratch {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
+// Device memory for the buffers of one call: taken from the stream-ordered
+// pool (and returned to it when the arena goes out of scope), or -- region
+// mode -- carved out of a caller-provided device region of `cap` bytes, which
+// allocates nothing.  Every buffer starts on a 256-byte boundary.  get()
+// returns nullptr (and sets the error) when the pool cannot allocate or the
+// region is exhausted.
+class Arena {
+  public:
+    explicit Arena(hipStream_t s) : s_(s) {}
+    Arena(hipStream_t s, void* region, size_t cap) : s_(s), base_((char*)region), cap_(cap) {}
+    void* get(size_t bytes);
+    // Bytes get() has handed out in region mode (with alignment), for size checks.
+    size_t used() const { return used_; }
+    static size_t aligned(size_t b) { return (b + 255) & ~size_t(255); }
+
+  private:
+    hipStream_t s_;
+    char* base_ = nullptr;
+    size_t cap_ = 0, used_ = 0;
+    std::vector<Scratch> owned_;
+};
+
 bool is_device_ptr(const void* p);
 
 // Staging for the synchronous host-pointer API (the reference's contract):
@@ -213,6 +235,13 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre = nullptr, const float* res = nullptr,
                      float* amax_out = nullptr, const float* amax_in = nullptr);
+// The same on a file-scope static device region (no allocation, no free):
+// conv2d_int8_noalloc_need bytes must not exceed conv2d_int8_noalloc_max().
+// Calls that overlap on one device share the region and race.
+bool conv2d_int8_noalloc(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
+                         const float* bias, int Cout, float* out, int act, hipStream_t s);
+size_t conv2d_int8_noalloc_need(const ConvShape& g, int Cout);
+size_t conv2d_int8_noalloc_max();
 // The int8 Winograd-route entry with caller-supplied scales.
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,
                        const float* ws, const float* bias, int Cout, float s_in, float inv_s,

@@ -194,6 +194,23 @@ void pool_free(void* p, hipStream_t s) {
     g_free.emplace(PoolKey{current_device(), s, it->second}, p);
 }
 
+void* Arena::get(size_t bytes) {
+    if (!base_) {
+        owned_.emplace_back(bytes ? bytes : 1, s_);
+        if (!owned_.back().p) return nullptr;
+        return owned_.back().p;
+    }
+    const size_t need = aligned(bytes ? bytes : 1);
+    if (need > cap_ - used_) {
+        set_error("scratch region exhausted (%zu of %zu bytes used, %zu more needed)", used_, cap_,
+                  need);
+        return nullptr;
+    }
+    void* p = base_ + used_;
+    used_ += need;
+    return p;
+}
+
 bool is_device_ptr(const void* p) {
     if (!p) return false;
     hipPointerAttribute_t a;

@@ -187,6 +187,20 @@ int acfun_dev_conv2d_int8(const float* input, int N, int H, int W, int Cin,
                           const int8_t* wq, const float* wscale, const float* bias,
                           int KH, int KW, int Cout, int stride, int pad, float* output,
                           int act, void* stream);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): acfun_dev_conv2d_int8 with every temporary (quantized
+ * activations, prepared weights, absmax partials, scale scalars) carved out of
+ * a 64 MiB static device region that each GPU holds for the life of the
+ * process; it calls no hipMalloc/hipFree.  A shape needing more than 64 MiB
+ * of temporaries (about N*H*W*roundup(Cin,16) + Cout*roundup(KH*KW*
+ * roundup(Cin,16),128) bytes) returns -1 with the reason in acfun_last_error().
+ * Every call on a device shares that device's region: calls that overlap on one
+ * device (two streams, two threads) race; serialize them. */
+int acfun_dev_conv2d_int8_noalloc(const float* input, int N, int H, int W, int Cin,
+                                  const int8_t* wq, const float* wscale, const float* bias,
+                                  int KH, int KW, int Cout, int stride, int pad, float* output,
+                                  int act, void* stream);
 int acfun_dev_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride,
                       int pad, float* output, int post_relu, void* stream);
 int acfun_dev_fc(const float* input, int N, int Cin, const float* weight, const float* bias,
