@@ -225,3 +225,117 @@ def _bn(v, ch, P):
     gamma = np.ascontiguousarray(P[2 * ch:3 * ch], np.float32)
     beta = np.ascontiguousarray(P[3 * ch:], np.float32)
     lib().oracle_batchnorm(v, v.size, ch, mean, var, gamma.ctypes.data, beta.ctypes.data, 1e-5)
+
+
+# ---- the same graph on the compiled reference's own per-op entry points ----
+
+def prepare_reference(ref, blob, int8=False):
+    """Parses and fuses a model (as run() does) and, in int8 mode, quantizes
+    every dense conv's folded weights once with the reference's own
+    acfun_quantize_weights -- the load-time part of run_reference()."""
+    import ctypes as C
+    version, inC, inH, inW, raw = parse(blob)
+    layers = fuse(raw)
+    covered = {F["last"]: fi for fi, F in enumerate(layers)}
+    P = lambda a: C.c_void_p(a.ctypes.data)
+    prev_c = inC
+    for F in layers:
+        F["w"] = None if F["w"] is None else np.ascontiguousarray(F["w"], np.float32)
+        F["b"] = None if F["b"] is None else np.ascontiguousarray(F["b"], np.float32)
+        t = F["type"]
+        if t == 10:
+            prev_c = inC if F["p"][0] == -1 else layers[covered[F["p"][0]]]["outC"]
+        if t in (1, 7):
+            F["inC"] = prev_c
+            prev_c = F["p"][2]
+        elif t == 2:
+            prev_c = F["p"][0]
+        F["outC"] = prev_c
+        if int8 and t == 1:
+            KH, KW, Cout = F["p"][:3]
+            K = KH * KW * F["inC"]
+            F["ws"] = np.empty(Cout, np.float32)
+            F["wq"] = np.empty((K, Cout), np.int8)
+            ref.acfun_quantize_weights(P(F["w"]), K, Cout, P(F["ws"]), P(F["wq"]))
+    return {"layers": layers, "covered": covered, "int8": int8}
+
+
+def run_reference(ref, prep, x):
+    """Executes a prepared model on the compiled reference: every conv, FC,
+    pool, ReLU, BN and softmax is one call of the reference's API on the whole
+    batch (acfun_conv2d(_relu)/_g, acfun_conv2d_int8, acfun_maxpool(_relu),
+    acfun_fc, acfun_relu, acfun_batchnorm, acfun_softmax per image); the
+    version-2 Add and GlobalAvgPool records, which the reference has no call
+    for, are numpy float32 in the order run() gives them.  This is the CPU
+    baseline of a version-2 model and is pinned to run() by the tests."""
+    import ctypes as C
+    P = lambda a: C.c_void_p(a.ctypes.data)
+    layers, covered = prep["layers"], prep["covered"]
+    x = np.ascontiguousarray(x, np.float32)
+    N = x.shape[0]
+    outs = []
+    cur = x
+    for F in layers:
+        t = F["type"]
+        if t in (1, 7):
+            KH, KW, Cout, s, p = F["p"][:5]
+            n, h, w_, ci = cur.shape
+            OH, OW = (h + 2 * p - KH) // s + 1, (w_ + 2 * p - KW) // s + 1
+            y = np.empty((n, OH, OW, Cout), np.float32)
+            if t == 7:
+                ref.acfun_conv2d_g(P(cur), n, h, w_, ci, P(F["w"]), P(F["b"]), KH, KW, Cout, s, p,
+                                   F["p"][5], P(y), F["act"])
+            elif prep["int8"]:
+                ref.acfun_conv2d_int8(P(cur), n, h, w_, ci, P(F["wq"]), P(F["ws"]), P(F["b"]),
+                                      KH, KW, Cout, s, p, C.c_float(0.0), P(y), F["act"])
+            else:
+                fn = ref.acfun_conv2d_relu if F["act"] else ref.acfun_conv2d
+                fn(P(cur), n, h, w_, ci, P(F["w"]), P(F["b"]), KH, KW, Cout, s, p, P(y))
+        elif t == 2:
+            Cout = F["p"][0]
+            flat = np.ascontiguousarray(cur.reshape(N, -1))
+            y = np.empty((N, Cout), np.float32)
+            fn = ref.acfun_fc_relu if F["act"] else ref.acfun_fc
+            fn(P(flat), N, flat.shape[1], P(F["w"]), P(F["b"]), Cout, P(y))
+            y = y.reshape(N, 1, 1, Cout)
+        elif t == 3:
+            y = cur.copy()
+            ref.acfun_relu(P(y), y.size)
+        elif t == 4:
+            pool, s, p = F["p"][:3]
+            n, h, w_, ci = cur.shape
+            OH, OW = (h + 2 * p - pool) // s + 1, (w_ + 2 * p - pool) // s + 1
+            y = np.empty((n, OH, OW, ci), np.float32)
+            fn = ref.acfun_maxpool_relu if F["post_relu"] else ref.acfun_maxpool
+            fn(P(cur), n, h, w_, ci, pool, s, p, P(y))
+        elif t == 5:
+            per = cur[0].size
+            y = np.empty_like(cur)
+            flat = np.ascontiguousarray(cur.reshape(N, per))
+            ref.acfun_softmax(P(flat), N, per, P(y))
+        elif t == 6:
+            ch = F["p"][0]
+            mean, var, gamma, beta = (np.array(F["w"][k * ch:(k + 1) * ch], np.float32)
+                                      for k in range(4))
+            y = cur.copy()
+            ref.acfun_batchnorm(P(y), y.size, ch, P(mean), P(var), P(gamma), P(beta),
+                                C.c_float(1e-5))
+        elif t == 8:
+            other = x if F["p"][0] == -1 else outs[covered[F["p"][0]]]
+            y = np.add(cur, other, dtype=np.float32)
+            if F["p"][1]:
+                np.maximum(y, 0.0, out=y, where=y < 0)
+        elif t == 9:
+            n, h, w_, ci = cur.shape
+            flat = cur.reshape(n, h * w_, ci)
+            sm = np.zeros((n, ci), np.float32)
+            for k in range(h * w_):
+                sm += flat[:, k, :]
+            y = (sm / np.float32(h * w_)).astype(np.float32).reshape(n, 1, 1, ci)
+        elif t == 10:
+            y = x if F["p"][0] == -1 else outs[covered[F["p"][0]]]
+        else:
+            raise ValueError(t)
+        outs.append(y)
+        cur = np.ascontiguousarray(y)
+    return cur.reshape(N, -1)

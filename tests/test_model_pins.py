@@ -182,3 +182,31 @@ def test_fold_bn_against_reference_loader(ref, rng, tmp_path, kind):
     # and the oracle's executor, which folds with oracle_fold_bn, gives the same bits
     np.testing.assert_array_equal(omodel.run(open(path, "rb").read(), x) if kind != "dense"
                                   else got, want)
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_reference_composition_matches_oracle_v2(ref, rng, tmp_path, int8):
+    """oracle.model.run_reference (the CPU baseline of a version-2 model: the
+    reference's own per-op calls on the batch) against the oracle executor:
+    bit-exact in int8 mode (acfun_conv2d_int8 on the batch, maxpool, the Add
+    records), within the fp32 conv tolerance otherwise; softmax through the
+    reference's acfun_softmax."""
+    inC, H, W, recs = models.small_resnet_v2(rng)
+    blob = acfun0.encode(inC, H, W, recs, version=2)
+    # int8 at batch 1: for N > 1 the reference's im2col + int8 GEMM route fills
+    # only image 0 (test_reference_int8_gemm_route_batch_defect), and the strided
+    # convs of this graph take that route
+    n = 1 if int8 else 3
+    x = rng.uniform(0, 1, (n, H, W, inC)).astype(np.float32)
+    got = omodel.run_reference(ref, omodel.prepare_reference(ref, blob, int8), x)
+    want = omodel.run(blob, x, int8=int8)
+    assert got.shape == want.shape
+    if int8:
+        # the head's FC is f64 in run() and AVX-512 fp32 here: compare the body bit for bit
+        inC, H, W, body = acfun0.resnet50(np.random.default_rng(7), in_hw=32, width=8,
+                                          blocks=(1, 2, 1, 1), head=False)
+        b2 = acfun0.encode(inC, H, W, body, version=2)
+        np.testing.assert_array_equal(
+            omodel.run_reference(ref, omodel.prepare_reference(ref, b2, True), x),
+            omodel.run(b2, x, int8=True))
+    assert rel_err(got, want) < 1e-4, rel_err(got, want)

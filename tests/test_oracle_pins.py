@@ -325,3 +325,35 @@ def test_requantize_s8_against_reference(ref, rng):
     np.testing.assert_array_equal(q, [127, -127, 0, 2, 2, 0, -2, 126, -126, 0, 0, 0])
     z, s0 = oracle.requantize_s8(np.zeros(17, np.float32))
     assert s0 == 0.0 and not np.any(z)
+
+
+def test_reference_int8_gemm_route_batch_defect(ref, rng):
+    """The reference's im2col + int8 GEMM route (src/conv_int8.cpp:133-141)
+    builds the im2col rows of image 0 only: for N > 1 the rows of images
+    1..N-1 stay zero-initialised (u8 0), so those images come out as beta[j]
+    everywhere.  Its own model executor always calls with N = 1 and never
+    meets this.  The oracle (and the GPU library) give every image its own
+    rows; this pins that to the reference itself: in a 2-image call
+    [image n, the image holding max|x|], image 0 is image n computed with the
+    whole batch's activation scale, and must equal the oracle's image n."""
+    N, H, Cin, Cout = 4, 15, 16, 32
+    x, wq, ws, b = int8_conv_inputs(rng, N, H, H, Cin, 3, 3, Cout)
+    x = x + rng.uniform(-0.3, 0.3, x.shape).astype(np.float32)   # distinct per image
+    assert oracle.conv2d_int8_route(H, H, Cin, 3, 3, Cout, 2, 1) == 5
+    OH = (H + 2 - 3) // 2 + 1
+    got = oracle.conv2d_int8(x, wq, ws, b, 3, 3, Cout, 2, 1, 0)
+    y = np.empty((N, OH, OH, Cout), np.float32)
+    ref.acfun_conv2d_int8(P(x), N, H, H, Cin, P(wq), P(ws), P(b), 3, 3, Cout, 2, 1,
+                          np.float32(0), P(y), 0)
+    assert_bitexact(got[0], y[0], "image 0")
+    maxa = np.float32(np.max(np.abs(x)))
+    alpha = maxa / np.float32(127.0) * ws
+    beta = b - (alpha * np.float32(128.0)) * wq.astype(np.float32).sum(0, dtype=np.float32)
+    assert np.array_equal(y[1:], np.broadcast_to(beta.astype(np.float32), y[1:].shape))
+    imax = int(np.argmax(np.abs(x).reshape(N, -1).max(1)))
+    for n in range(N):
+        pair = np.ascontiguousarray(np.stack([x[n], x[imax]]))
+        y2 = np.empty((2, OH, OH, Cout), np.float32)
+        ref.acfun_conv2d_int8(P(pair), 2, H, H, Cin, P(wq), P(ws), P(b), 3, 3, Cout, 2, 1,
+                              np.float32(0), P(y2), 0)
+        assert_bitexact(got[n], y2[0], f"image {n} with the batch scale")
