@@ -67,6 +67,8 @@ SIGNATURES = {
     "acfun_dev_conv2d": (_i, [_p, _i, _i, _i, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "acfun_dev_conv2d_int8": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i,
                                    _p]),
+    "acfun_dev_conv2d_int8_q": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i,
+                                     _p, _p, _i, _i, _p]),
     "acfun_dev_conv2d_int8_noalloc": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i,
                                            _p, _i, _p]),
     "acfun_dev_maxpool": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _i, _p]),

@@ -487,6 +487,19 @@ int acfun_dev_conv2d_int8(const float* input, int N, int H, int W, int Cin, cons
     return conv2d_int8_dev(input, g, wq, wscale, bias, Cout, output, act, resolve(stream)) ? 0 : -1;
 }
 
+int acfun_dev_conv2d_int8_q(const int8_t* input, const float* s_in, int N, int H, int W,
+                            int Cin, const int8_t* wq, const float* wscale, const float* bias,
+                            int KH, int KW, int Cout, int stride, int pad, int8_t* output,
+                            float* s_out, int act, int out_rule, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0) return 0;
+    int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return 0;
+    ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
+    return conv2d_int8_q8_api(input, s_in, g, wq, wscale, bias, Cout, output, s_out, act,
+                              out_rule, resolve(stream)) ? 0 : -1;
+}
+
 int acfun_dev_conv2d_int8_noalloc(const float* input, int N, int H, int W, int Cin,
                                   const int8_t* wq, const float* wscale, const float* bias, int KH,
                                   int KW, int Cout, int stride, int pad, float* output, int act,

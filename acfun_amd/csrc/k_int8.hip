@@ -27,7 +27,7 @@
 // GEMM entries (acfun_gemm_int8*, acfun_conv1x1_int8) and operands too large
 // for k_i8mm's 32-bit offsets run k_igemm_i8 (register-staged,
 // v_mfma_i32_16x16x64_i8).
-#include "rt.hpp"
+#include "i8mm.hpp"
 
 #include <algorithm>
 #include <cstdio>
@@ -42,7 +42,6 @@ typedef int i4 __attribute__((ext_vector_type(4)));
 constexpr int IBK = 128;       // k bytes per LDS tile (two MFMA k-steps of 64)
 constexpr int ILD = IBK + 16;  // padded LDS row (bytes): rows 36 banks apart
 
-enum { EPI_I32 = 0, EPI_GEMM = 1, EPI_WINO = 2 };
 
 struct I8P {
     const int8_t* A;   // s8 (or u8 with a_xor) activations
@@ -227,453 +226,6 @@ __global__ __launch_bounds__(256) void k_igemm_i8(I8P p) {
                     p.Cf[o] = v;
                 }
             }
-    }
-}
-
-// ---------------------------------------------------------------- k_i8mm
-// int8 implicit GEMM for the convolution routes: LDS-DMA staging and int8
-// MFMA, persistent workgroups.
-//
-// Workgroup = 256 threads; its waves own a BM x BN output tile as 2 x 2 waves
-// of FM x FN v_mfma_i32_32x32x32_i8 blocks (FM = BM/64, FN = BN/64).  K (k' =
-// tap*Cinp + ic) is consumed in chunks of 128 bytes; a stage holds A: BM rows
-// x 8 quads of 16 bytes and B: BN rows x 8 quads, quad q of row r at slot
-// r*8 + (q ^ swz(r)), swz(r) = (r ^ (r >> 3)) & 7, so 8 and 16 consecutive
-// rows read at one quad fall on distinct banks.  Both are filled by
-// buffer_load_dwordx4 ... lds: a wave instruction fills 64 consecutive slots
-// (8 rows); lane l the 16 bytes of row 8I + l/8, slot l%8.  A's 16 bytes are
-// 16 channels of one input pixel at one tap (NHWC s8, channels padded to
-// Cinp, a multiple of 16); a tap outside the image, a row past M or a k past
-// K reads zeros through an out-of-range offset -- s8 0 is the reference's
-// padding value u8 128.  NST stages: chunk c+NST-1 is issued while chunk c is
-// multiplied, across tile boundaries (a workgroup runs its tiles back to
-// back).  In k-step s (32 k) lane half h reads quad 2s+h of its A and B rows
-// with one ds_read_b128 each.  At a tile's last chunk each lane forms the
-// reference's epilogue for its 16 x FM x FN accumulators, adds the fused
-// residual, applies the activation and stores dwords (inline asm, so the
-// compiler's wait insertion keeps exact counts for the loads; the waits stay
-// correct with stores queued, since loads complete in issue order).
-//
-// The workgroups' tiles are cut into 8 contiguous runs, one per XCD
-// (workgroup id mod 8), so the BN-blocks of one pixel block share an L2.
-// A-operand addressing: AM_C128 when Cinp is a multiple of 128 (a chunk lies
-// in one tap: tap, offset and bounds test are per chunk and wave-uniform),
-// AM_C64 when Cinp = 64 (two taps per chunk), AM_GEN otherwise.
-struct I8M {
-    const int8_t* A;     // s8 NHWC [N*H*W][Cinp]
-    const int8_t* Bt;    // [N][ldb], ldb a multiple of 128, zero beyond taps*Cinp
-    int M, N, K, ldb;    // K = taps * Cinp
-    int H, W, Cinp, KW, stride, pad, OH, OW;
-    unsigned a_bytes, b_bytes;
-    int epi, act;
-    const int* Sw;       // EPI_GEMM: column sums of the weights
-    const float* ws;     // per-channel weight scales (with scal: factors made here)
-    const float* bias;   // nullable
-    const float* scal;   // device scalars [0] inv_s [1] sa [2] zero flag (nullable)
-    const float* alpha;  // explicit per-channel factors (nullable: made from scal, ws)
-    const float* beta;
-    const float* res;    // residual added before the activation (nullable)
-    float* Cf;
-    int ldc, ldr;
-    int vec;             // Cf (and res) rows allow 16-byte stores/loads
-    int gm, gn;          // grid in tiles
-    float* amax;         // per-workgroup max|stored value| at [blockIdx.x] (nullable)
-};
-
-// Workgroups of k_i8mm when it reports the output's absmax: its consumer's
-// quantizer reduces this many per-workgroup partials (unused ones zero).
-constexpr int kAmaxParts = kI8AmaxParts;
-
-enum { AM_GEN = 0, AM_C128 = 1, AM_C64 = 2 };
-
-__device__ __forceinline__ int i8swz(int r) { return (r ^ (r >> 3)) & 7; }
-
-// floor(a / b) for 0 <= a < 2^24, b >= 1 via a float reciprocal, corrected.
-__device__ __forceinline__ int udiv_small(int a, int b, float rb) {
-    int q = (int)((float)a * rb);
-    q -= (q * b > a);
-    q += ((q + 1) * b <= a);
-    return q;
-}
-
-constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
-
-constexpr size_t i8mm_lds(int BM, int BN, int NST) { return (size_t)NST * (BM + BN) * 128; }
-
-template <int BM, int BN, int NST, int AM>
-__global__ __launch_bounds__(256) void k_i8mm(I8M p) {
-    constexpr int FM = BM / 64, FN = BN / 64;
-    constexpr int SA = BM * 128, STG = (BM + BN) * 128;
-    constexpr int AIT = BM / 32, BIT = BN / 32;      // DMA instructions per wave per chunk
-    constexpr int ITEMS = AIT + BIT;
-    constexpr int AHEAD = NST - 1;
-    constexpr unsigned kOOB = 0x80000000u;
-    typedef __attribute__((address_space(3))) void lds_void;
-    typedef int i16v __attribute__((ext_vector_type(16)));
-    extern __shared__ __attribute__((aligned(16))) int8_t sm8[];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nch = (p.K + 127) >> 7;
-
-    // ---- tiles of this workgroup: t0, t0 + tstr, ... (cnt of them)
-    const int total = p.gm * p.gn, G = gridDim.x, b = blockIdx.x;
-    int t0, tstr, cnt;
-    if ((G & 7) == 0) {
-        const int x = b & 7, i = b >> 3, gx = G >> 3;
-        const int sx = (int)(((long long)x * total) >> 3);
-        const int ex = (int)(((long long)(x + 1) * total) >> 3);
-        t0 = sx + i;
-        tstr = gx;
-        cnt = ex > t0 ? (ex - t0 + gx - 1) / gx : 0;
-    } else {
-        t0 = b;
-        tstr = G;
-        cnt = b < total ? (total - b + G - 1) / G : 0;
-    }
-    const int nit = cnt * nch;
-
-    // =============================== compute waves
-    const int wm = wave >> 1, wn = wave & 1;
-    const __amdgpu_buffer_rsrc_t ares =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.A, (short)0, (int)p.a_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t bres =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.Bt, (short)0, (int)p.b_bytes, 0x00020000);
-
-    // ---- DMA rows of this lane: row 8*(wave + 4t) + lane/8 of the A and B
-    // stages, quad slot lane%8 holding data quad aq/bq
-    const int sl = lane & 7, rl = lane >> 3;
-    int aq[AIT], bk[BIT];
-#pragma unroll
-    for (int t = 0; t < AIT; ++t) aq[t] = sl ^ i8swz(8 * (wave + 4 * t) + rl);
-#pragma unroll
-    for (int t = 0; t < BIT; ++t) bk[t] = 16 * (sl ^ i8swz(8 * (wave + 4 * t) + rl));
-    // issue-side per-tile state
-    int abase[AIT], amask[AIT];          // fast modes: byte offset at tap 0, in-bounds taps
-    int apix[AIT], aih[AIT], aiw[AIT];   // AM_GEN
-    unsigned bv[BIT];
-    // Per-tile pixel decode.  A 1x1 / stride 1 / pad 0 convolution's row m is
-    // input pixel m; otherwise m -> (image, oh, ow) by float-reciprocal
-    // division while m < 2^24 (exact after udiv_small's correction).
-    const bool gemm1 = p.K == p.Cinp && p.KW == 1 && p.stride == 1 && p.pad == 0 && p.OH == p.H &&
-                       p.OW == p.W;
-    const bool small_m = p.M < (1 << 24);
-    const int ohw = p.OH * p.OW;
-    const float rohw = 1.0f / (float)ohw, row_ = 1.0f / (float)p.OW;
-    // bits [lo, hi) of 8
-    auto span8 = [](int lo, int hi) -> unsigned {
-        lo = lo > 0 ? lo : 0;
-        hi = hi < 8 ? hi : 8;
-        return hi > lo ? (1u << hi) - (1u << lo) : 0u;
-    };
-    auto setup = [&](int k) {
-        const int L = t0 + k * tstr;
-        const int tm = L / p.gn, tn = L - tm * p.gn;
-#pragma unroll
-        for (int t = 0; t < AIT; ++t) {
-            const int m = tm * BM + 8 * (wave + 4 * t) + rl;
-            int pix = 0, ih0 = -(1 << 28), iw0 = 0;
-            if (m < p.M) {
-                if (gemm1) {
-                    pix = m;
-                    ih0 = iw0 = 0;
-                } else {
-                    int n, oh;
-                    if (small_m) {
-                        n = udiv_small(m, ohw, rohw);
-                        oh = udiv_small(m - n * ohw, p.OW, row_);
-                    } else {
-                        n = m / ohw;
-                        oh = (m - n * ohw) / p.OW;
-                    }
-                    const int ow = m - n * ohw - oh * p.OW;
-                    pix = n * p.H * p.W;
-                    ih0 = oh * p.stride - p.pad;
-                    iw0 = ow * p.stride - p.pad;
-                }
-            }
-            if (AM == AM_GEN) {
-                apix[t] = pix;
-                aih[t] = ih0;
-                aiw[t] = iw0;
-            } else {
-                const int q16 = AM == AM_C64 ? 16 * (aq[t] & 3) : 16 * aq[t];
-                abase[t] = m < p.M ? (pix + ih0 * p.W + iw0) * p.Cinp + q16 : 0;
-                // bit kh*8 + kw: tap (kh, kw) inside the image (KW <= 8, kh < 4:
-                // the fast modes need KH <= 4).  Rows and columns in range form
-                // bit spans; the kh-th byte of the mask is the column span when
-                // row kh is in range.
-                const unsigned rm = span8(-ih0, p.H - ih0), cm = span8(-iw0, p.W - iw0);
-                const unsigned rs4 = (rm & 1u) | ((rm & 2u) << 7) | ((rm & 4u) << 14) | ((rm & 8u) << 21);
-                amask[t] = (int)(rs4 * cm);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < BIT; ++t) {
-            const int n = tn * BN + 8 * (wave + 4 * t) + rl;
-            bv[t] = n < p.N ? (unsigned)(n * p.ldb + bk[t]) : kOOB;
-        }
-    };
-    // issue-side per-chunk state (wave-uniform): fast modes track the tap of
-    // the chunk's first quad (kh, kw) and its channel offset ic0
-    int ikh = 0, ikw = 0, iic = 0;
-    const float rcinp = 1.0f / (float)p.Cinp, rkw = 1.0f / (float)p.KW;
-    const int taps = p.K / p.Cinp;
-    auto tap_off = [&](int kh, int kw) { return (kh * p.W + kw) * p.Cinp; };
-    auto issue = [&](int t, int c, int8_t* st) {      // DMA item t of chunk c into stage st
-        if (t < AIT) {
-            unsigned v = kOOB;
-            if (AM == AM_GEN) {
-                const int k = (c << 7) + 16 * aq[t];
-                if (k < p.K) {
-                    const int tap = udiv_small(k, p.Cinp, rcinp);
-                    const int ic = k - tap * p.Cinp;
-                    const int kh = udiv_small(tap, p.KW, rkw);
-                    const int kw = tap - kh * p.KW;
-                    const int ih = aih[t] + kh, iw = aiw[t] + kw;
-                    if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
-                        v = (unsigned)((apix[t] + ih * p.W + iw) * p.Cinp + ic);
-                }
-            } else if (AM == AM_C128) {
-                const bool ok = (amask[t] >> (ikh * 8 + ikw)) & 1;
-                v = ok ? (unsigned)(abase[t] + tap_off(ikh, ikw) + iic) : kOOB;
-            } else {
-                // two taps per chunk: quads 0-3 at (ikh, ikw), quads 4-7 at the next tap
-                int kh = ikh, kw = ikw + 1;
-                if (kw == p.KW) { kw = 0; ++kh; }
-                const bool second = aq[t] >= 4;
-                const bool inK = !second || (2 * c + 1 < taps);
-                const int th = second ? kh : ikh, tw = second ? kw : ikw;
-                const bool ok = inK && ((amask[t] >> (th * 8 + tw)) & 1);
-                v = ok ? (unsigned)(abase[t] + tap_off(th, tw)) : kOOB;
-            }
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ares, (lds_void*)(st + (wave + 4 * t) * 1024), 16, v, 0, 0, 0);
-        } else {
-            const int tt = t - AIT;
-            // (a local, not the captured array element, as the builtin's operand:
-            // with the latter clang drops the kernel's host-side stub)
-            const unsigned v = bv[tt] + (unsigned)(c << 7);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                bres, (lds_void*)(st + SA + (wave + 4 * tt) * 1024), 16, v, 0, 0, 0);
-        }
-    };
-    auto advance = [&]() {                             // the issue cursor's next chunk
-        if (AM == AM_C128) {
-            iic += 128;
-            if (iic == p.Cinp) { iic = 0; if (++ikw == p.KW) { ikw = 0; ++ikh; } }
-        } else if (AM == AM_C64) {
-            ikw += 2;
-            while (ikw >= p.KW) { ikw -= p.KW; ++ikh; }
-        }
-    };
-
-    // ---- LDS read offsets (bytes within a stage) of this lane, per k-step
-    const int r32 = lane & 31, hq = lane >> 5;
-    int rda[4][FM], rdb[4][FN];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int r = wm * (BM / 2) + 32 * i + r32;
-            rda[s][i] = r * 128 + 16 * ((2 * s + hq) ^ i8swz(r));
-        }
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int r = wn * (BN / 2) + 32 * j + r32;
-            rdb[s][j] = SA + r * 128 + 16 * ((2 * s + hq) ^ i8swz(r));
-        }
-    }
-    i16v acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
-
-    // ---- prologue: the first AHEAD chunks of the item stream (tile, chunk)
-    int ik = 0, ic = 0;                         // issue cursor
-    if (nit > 0) setup(0);
-#pragma unroll
-    for (int a = 0; a < AHEAD; ++a) {
-        if (a < nit) {
-#pragma unroll
-            for (int t = 0; t < ITEMS; ++t) issue(t, ic, sm8 + a * STG);
-            advance();
-            if (++ic == nch) {
-                ic = 0;
-                ikh = ikw = iic = 0;
-                if (++ik < cnt) setup(ik);
-            }
-        }
-    }
-
-    const bool zero = p.scal && p.scal[2] != 0.0f;
-    const float sa = p.scal ? p.scal[1] : 0.0f;
-    int st = 0, ck = 0, cc = 0;                 // compute cursor
-    float pv0[FN], pv1[FN];                     // epilogue inputs of the current tile
-    int pv2[FN];
-    float amx = 0.0f;                           // max|stored value| of this lane
-    for (int g = 0; g < nit; ++g) {
-        // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
-        // chunks issued after it may stay in flight.  A previous tile's
-        // epilogue stores may sit in the counter's queue after some of those
-        // loads: a wait that leaves only the later chunks' loads outstanding
-        // still proves chunk g landed (a store completing early cannot stand
-        // in for an older load, since the loads complete in order).  The
-        // stores are inline asm, so the compiler's own waits see loads only.
-        const int later = nit - 1 - g < AHEAD - 1 ? nit - 1 - g : AHEAD - 1;
-        if (later <= 0) __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
-        else if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * ITEMS));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const int L = t0 + ck * tstr;
-        const int tm = L / p.gn, tn = L - tm * p.gn;
-        const int m0 = tm * BM, n0 = tn * BN;
-        if (cc == 0) {                          // the tile's epilogue inputs, a chunk early
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int n = n0 + wn * (BN / 2) + 32 * j + r32;
-                const int nn = n < p.N ? n : p.N - 1;
-                pv0[j] = p.alpha ? p.alpha[nn] : p.ws[nn];
-                pv1[j] = (p.epi == EPI_GEMM && p.alpha) ? p.beta[nn] : (p.bias ? p.bias[nn] : 0.0f);
-                pv2[j] = p.epi == EPI_GEMM ? p.Sw[nn] : 0;
-            }
-        }
-        const int8_t* S = sm8 + st * STG;
-        const int sta = st == 0 ? NST - 1 : st - 1;   // (g + AHEAD) % NST
-        int8_t* NA = sm8 + sta * STG;
-        const bool more = g + AHEAD < nit;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            i4 fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = *(const i4*)(S + rda[s][i]);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) fb[j] = *(const i4*)(S + rdb[s][j]);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-            if (more) {
-#pragma unroll
-                for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, ic, NA);
-            }
-        }
-        if (more) {
-            advance();
-            if (++ic == nch) {
-                ic = 0;
-                ikh = ikw = iic = 0;
-                if (++ik < cnt) setup(ik);
-            }
-        }
-        st = st == NST - 1 ? 0 : st + 1;
-        if (++cc < nch) continue;
-        // ---- epilogue of tile ck: lane l, register e of block (i, j) <->
-        //      row m0 + wm*BM/2 + 32i + 8(e/4) + 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32
-        if (nch == 1) {                          // parameters were loaded in this iteration
-            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
-        }
-        const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
-        const bool gemm = p.epi == EPI_GEMM;
-        const bool relu1 = p.act == 1, relu2 = p.act == 2;
-        float al[FN], be[FN];
-        int corr[FN];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            corr[j] = 0;
-            if (gemm) {
-                corr[j] = 128 * pv2[j];
-                if (p.alpha) {
-                    al[j] = pv0[j];
-                    be[j] = pv1[j];
-                } else {   // src/conv_int8.cpp:100-107: alpha = sa*ws; beta = b - (alpha*128)*Sw
-                    al[j] = __fmul_rn(sa, pv0[j]);
-                    be[j] = __fsub_rn(pv1[j], __fmul_rn(__fmul_rn(al[j], 128.0f), (float)pv2[j]));
-                }
-            } else {       // src/winograd_int8.cpp:155: (s_in*0.25)*ws, then fma with the bias
-                al[j] = p.alpha ? pv0[j] : __fmul_rn(__fmul_rn(sa, 0.25f), pv0[j]);
-                be[j] = pv1[j];
-            }
-        }
-        // Lane l, register e of block (i, j) <-> row m0 + wm*BM/2 + 32i + 8(e/4) +
-        // 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32.  The element loop is
-        // straight-line: both routes' formulas and both ReLU forms are computed
-        // and selected by wave-uniform flags; only whole-tile properties (in
-        // range, fused residual) pick one of four copies of the loop.
-        const int mb = m0 + wm * (BM / 2) + 4 * hq, nb = n0 + wn * (BN / 2) + r32;
-        float* const cl = p.Cf + (long long)mb * p.ldc + nb;      // this lane's first row
-        auto tile_out = [&](auto fullc, auto resc) {
-            constexpr bool FULL = decltype(fullc)::value, RES = decltype(resc)::value;
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int n = nb + 32 * j;
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-                    float rv[16];
-                    if (RES) {     // residual of the fused Add, all 16 loads in flight at once
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) {
-                            const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3);
-                            rv[e] = (FULL || (m < p.M && n < p.N)) ? p.res[(long long)m * p.ldr + n] : 0.0f;
-                        }
-                    }
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3);
-                        const int a = acc[i][j][e];
-                        acc[i][j][e] = 0;
-                        // GEMM routes: fl(fl(acc_u * alpha) + beta); Winograd route:
-                        // fmaf(4*acc_s, alpha_w, bias), with (float)(4a) = 4*(float)a exactly.
-                        // An all-zero input gives 0 without the bias (src/conv_int8.cpp:78).
-                        const float ug =
-                            __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr[j]), al[j]), be[j]);
-                        const float uw = fmaf(4.0f * (float)a, al[j], be[j]);
-                        const float u = gemm ? ug : uw;
-                        float v = zero ? 0.0f : u;
-                        if (RES) v = __fadd_rn(v, rv[e]);
-                        v = act_select(v, relu1, relu2);
-                        if (FULL || (m < p.M && n < p.N)) {
-                            float* dst = cl + (32 * i + 8 * (e >> 2) + (e & 3)) * (long long)p.ldc + 32 * j;
-                            asm volatile("global_store_dword %0, %1, off" ::"v"(dst), "v"(v) : "memory");
-                            const float av = fabsf(v);
-                            amx = av > amx ? av : amx;             // NaN never wins
-                        }
-                    }
-                }
-            }
-        };
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-        if (full) {
-            if (p.res) tile_out(T_{}, T_{});
-            else tile_out(T_{}, F_{});
-        } else {
-            if (p.res) tile_out(F_{}, T_{});
-            else tile_out(F_{}, F_{});
-        }
-        cc = 0;
-        ++ck;
-    }
-    // this workgroup's max|v| of the output tensor, a partial of the next
-    // layer's absmax (the reference's max|x| of its input, src/conv_int8.cpp:77)
-    if (p.amax) {
-        __shared__ float wmax[4];
-        for (int off = 32; off > 0; off >>= 1) {
-            const float o = __shfl_xor(amx, off, 64);
-            amx = o > amx ? o : amx;
-        }
-        if (lane == 0) wmax[wave] = amx;
-        __syncthreads();
-        if (tid == 0) {
-            float mm = wmax[0];
-            for (int w = 1; w < 4; ++w) mm = wmax[w] > mm ? wmax[w] : mm;
-            p.amax[blockIdx.x] = mm;
-        }
     }
 }
 
@@ -1018,7 +570,6 @@ bool launch_i8(const I8P& p, bool conv, bool va, hipStream_t s) {
 // k_i8mm tile choice.  ACFUN_I8_TILE="BMxBNxNST" overrides the tile and
 // ACFUN_I8_GRID=<workgroups per CU> the persistent grid (0: one tile per
 // workgroup); both exist for tile sweeps.
-struct I8Tile { int bm, bn, nst, per_cu; };
 I8Tile pick_i8mm_tile(int M, int N, int K) {
     static int forced = -1;
     static I8Tile ft{64, 64, 3, 0};
@@ -1057,43 +608,13 @@ bool i8mm_fits(long long a_bytes, long long n, int ldb) {
     return a_bytes < 0x7fffffffll && n * ldb < 0x7fffffffll;
 }
 
-template <int BM, int BN, int NST, int AM>
-bool launch_i8mm_t(I8M& p, int cap, hipStream_t s) {
-    constexpr size_t lds = i8mm_lds(BM, BN, NST);
-    static_assert(lds <= 160 * 1024, "k_i8mm LDS");
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
-        (void)hipFuncSetAttribute((const void*)k_i8mm<BM, BN, NST, AM>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    }
-    p.gm = (p.M + BM - 1) / BM;
-    p.gn = (p.N + BN - 1) / BN;
-    // one tile per workgroup, or (cap > 0) at most cap persistent workgroups per
-    // CU, a multiple of 8 (the per-XCD runs)
-    const long long total = (long long)p.gm * p.gn;
-    long long gsz = total;
-    if (cap > 0) {
-        gsz = std::min(total, (long long)cap * num_cus());
-        if (gsz >= 8) gsz &= ~7ll;
-    }
-    if (p.amax && gsz > kAmaxParts) gsz = kAmaxParts;     // one absmax partial per workgroup
-    dim3 grid((unsigned)gsz);
-    ACFUN_LAUNCH("k_igemm_i8", (k_i8mm<BM, BN, NST, AM>), grid, dim3(256), lds, s, p);
-    return check_launch("k_i8mm");
-}
-
-template <int AM>
-bool launch_i8mm_am(I8M& p, const I8Tile& t, hipStream_t s) {
-#define ACFUN_I8MM(BM, BN, NST) \
-    if (t.bm == BM && t.bn == BN && t.nst == NST) return launch_i8mm_t<BM, BN, NST, AM>(p, t.per_cu, s);
-    ACFUN_I8MM(128, 128, 2) ACFUN_I8MM(128, 128, 3) ACFUN_I8MM(128, 128, 4)
-    ACFUN_I8MM(64, 128, 2) ACFUN_I8MM(64, 128, 3) ACFUN_I8MM(64, 128, 4)
-    ACFUN_I8MM(128, 64, 2) ACFUN_I8MM(128, 64, 3) ACFUN_I8MM(128, 64, 4)
-    ACFUN_I8MM(64, 64, 2) ACFUN_I8MM(64, 64, 3) ACFUN_I8MM(64, 64, 4)
-#undef ACFUN_I8MM
-    set_error("k_i8mm: no tile %dx%dx%d", t.bm, t.bn, t.nst);
-    return false;
+// The addressing mode k_i8mm uses for p's A operand.
+int i8mm_am(const I8M& p) {
+    const int KH = p.K / p.Cinp / p.KW;
+    const bool small = p.KW <= 8 && KH <= 4;    // the fast modes' tap bitmask: 4 rows x 8 columns
+    if (small && p.Cinp % 128 == 0) return AM_C128;
+    if (small && p.Cinp == 64) return AM_C64;
+    return AM_GEN;
 }
 
 bool launch_i8mm(I8M& p, hipStream_t s) {
@@ -1101,11 +622,26 @@ bool launch_i8mm(I8M& p, hipStream_t s) {
     const I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
     p.vec = al16(p.Cf) && p.ldc % 4 == 0 && (!p.res || (al16(p.res) && p.ldr % 4 == 0));
-    const int KH = p.K / p.Cinp / p.KW;
-    const bool small = p.KW <= 8 && KH <= 4;    // the fast modes' tap bitmask: 4 rows x 8 columns
-    if (small && p.Cinp % 128 == 0) return launch_i8mm_am<AM_C128>(p, t, s);
-    if (small && p.Cinp == 64) return launch_i8mm_am<AM_C64>(p, t, s);
-    return launch_i8mm_am<AM_GEN>(p, t, s);
+    return launch_i8mm_f32(p, t, i8mm_am(p), s);
+}
+
+// A requantized s8 output: the first pass writes the per-workgroup maxima of
+// the float output into parts (kAmaxParts floats), the second recomputes the
+// tile and stores clamp(rule(v * 127/max)) with s_out = max/127.
+bool launch_i8mm_rq(I8M& p, float* parts, hipStream_t s) {
+    if (p.M <= 0 || p.N <= 0) return true;
+    I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
+    t.bm = t.bn = 64;                           // the s8 epilogue stages 64 x 64 tiles
+    if (t.per_cu <= 0) t.per_cu = 3;
+    p.vec = 0;
+    p.res = nullptr;
+    p.amax = parts;
+    const int am = i8mm_am(p);
+    if (!launch_i8mm_q8(p, t, am, OUT_AMAX, s)) return false;
+    p.amax = nullptr;
+    p.qparts = parts;
+    p.nqparts = i8mm_grid(p, t);
+    return launch_i8mm_q8(p, t, am, OUT_Q8, s);
 }
 
 // Fills the convolution part of k_i8mm's arguments.
@@ -1377,6 +913,100 @@ bool conv2d_int8_noalloc(const float* in, const ConvShape& g, const int8_t* wq, 
     Arena ar(s, region, kNoAllocBytes);
     return conv2d_int8_run(in, g, wq, ws, bias, Cout, out, act, s, ar, true, nullptr, nullptr,
                            nullptr, nullptr);
+}
+
+namespace {
+// [pix][Cin] s8 -> [pix][Cinp] s8 with zero channel padding, and back.
+__global__ void k_s8_repad(const int8_t* __restrict__ x, long long pix, int Cx, int Cy,
+                           int8_t* __restrict__ y) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pix * Cy) return;
+    long long p = i / Cy;
+    int c = (int)(i - p * Cy);
+    y[i] = c < Cx ? x[p * Cx + c] : (int8_t)0;
+}
+}  // namespace
+
+bool conv2d_int8_q8_dev(const int8_t* q, int ldq_in, const float* s_in, const ConvShape& g,
+                        const int8_t* wq, const float* ws, const float* bias, int Cout,
+                        int8_t* out, int ldo, float* s_out, int act, int rule, hipStream_t s,
+                        const I8Weights* pre) {
+    if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
+    const int Cinp = rup(g.Cin, 16);
+    if (ldq_in != Cinp || ldo % 16 != 0 || ldo < Cout || (((uintptr_t)q | (uintptr_t)out) & 15u)) {
+        set_error("conv2d_int8_q8: s8 rows must be 16-byte aligned and padded to 16 channels");
+        return false;
+    }
+    const long long pix = (long long)g.N * g.H * g.W;
+    const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
+                      g.W >= 3 && g.Cin >= 4 && Cout >= 4;
+    Arena ar(s);
+    const int8_t* bt;
+    const int* sw;
+    int ldb;
+    const bool prepared = pre && pre->bt && pre->taps == g.KH * g.KW && pre->Cin == g.Cin &&
+                          pre->N == Cout;
+    if (prepared) {
+        bt = pre->bt; sw = pre->sw; ldb = pre->ldb;
+    } else {
+        ldb = rup(g.KH * g.KW * Cinp, 128);
+        int8_t* nbt = (int8_t*)ar.get((size_t)Cout * ldb);
+        int* nsw = (int*)ar.get((size_t)Cout * sizeof(int));
+        if (!nbt || !nsw) return false;
+        hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
+                           Cinp, Cout, nbt, ldb, nsw);
+        if (!check_launch("k_prep_weights")) return false;
+        bt = nbt; sw = nsw;
+    }
+    if (!i8mm_fits(pix * Cinp, Cout, ldb) ||
+        (long long)g.N * g.OH * g.OW * ldo >= 0x7fffffffll) {
+        set_error("conv2d_int8_q8: operands past 32-bit offsets");
+        return false;
+    }
+    float* parts = (float*)ar.get((size_t)kAmaxParts * sizeof(float));
+    if (!parts) return false;
+    I8M p{};
+    i8mm_conv(p, q, g, Cinp, bt, ldb, Cout);
+    p.act = act; p.s_in = s_in; p.ws = ws; p.bias = bias;
+    p.Cq = out; p.ldq = ldo; p.rule = rule; p.s_out = s_out;
+    if (wino) p.epi = EPI_WINO;
+    else { p.epi = EPI_GEMM; p.Sw = sw; }
+    return launch_i8mm_rq(p, parts, s);
+}
+
+bool conv2d_int8_q8_api(const int8_t* in, const float* s_in, const ConvShape& g,
+                        const int8_t* wq, const float* ws, const float* bias, int Cout,
+                        int8_t* out, float* s_out, int act, int rule, hipStream_t s) {
+    if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
+    if (rule != 0 && rule != 1) {
+        set_error("acfun_dev_conv2d_int8_q: out_rule must be 0 or 1 (got %d)", rule);
+        return false;
+    }
+    const int Cinp = rup(g.Cin, 16), Coutp = rup(Cout, 16);
+    const long long pix = (long long)g.N * g.H * g.W, pixo = (long long)g.N * g.OH * g.OW;
+    Arena ar(s);
+    const int8_t* qin = in;
+    if (g.Cin != Cinp || ((uintptr_t)in & 15u)) {
+        int8_t* t = (int8_t*)ar.get((size_t)pix * Cinp);
+        if (!t) return false;
+        hipLaunchKernelGGL(k_s8_repad, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp, t);
+        if (!check_launch("k_s8_repad")) return false;
+        qin = t;
+    }
+    const bool direct = Cout == Coutp && ((uintptr_t)out & 15u) == 0;
+    int8_t* qo = out;
+    if (!direct) {
+        qo = (int8_t*)ar.get((size_t)pixo * Coutp);
+        if (!qo) return false;
+    }
+    if (!conv2d_int8_q8_dev(qin, Cinp, s_in, g, wq, ws, bias, Cout, qo, Coutp, s_out, act, rule,
+                            s, nullptr))
+        return false;
+    if (!direct) {
+        hipLaunchKernelGGL(k_s8_repad, g1(pixo * Cout), dim3(256), 0, s, qo, pixo, Coutp, Cout, out);
+        if (!check_launch("k_s8_repad")) return false;
+    }
+    return true;
 }
 
 bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8_t* wq,

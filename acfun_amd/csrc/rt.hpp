@@ -235,6 +235,20 @@ bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, cons
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre = nullptr, const float* res = nullptr,
                      float* amax_out = nullptr, const float* amax_in = nullptr);
+// The int8-in / int8-out convolution (a requantized s8 output): s8 activations
+// q [pix][ldq_in = roundup(Cin,16)] with per-tensor scale *s_in (device; 0 =
+// all-zero input) -> s8 out [pixo][ldo] (ldo a multiple of 16, columns Cout..
+// zero) and *s_out = max|y|/127, y being what acfun_conv2d_int8's route computes
+// with activation scale *s_in.  rule 0 rounds y*127/max|y| to nearest even;
+// rule 1 as the Winograd route quantizes its input.  Two passes of k_i8mm.
+bool conv2d_int8_q8_dev(const int8_t* q, int ldq_in, const float* s_in, const ConvShape& g,
+                        const int8_t* wq, const float* ws, const float* bias, int Cout,
+                        int8_t* out, int ldo, float* s_out, int act, int rule, hipStream_t s,
+                        const I8Weights* pre = nullptr);
+// The same on unpadded NHWC s8 tensors [N,H,W,Cin] -> [N,OH,OW,Cout].
+bool conv2d_int8_q8_api(const int8_t* in, const float* s_in, const ConvShape& g,
+                        const int8_t* wq, const float* ws, const float* bias, int Cout,
+                        int8_t* out, float* s_out, int act, int rule, hipStream_t s);
 // The same on a file-scope static device region (no allocation, no free):
 // conv2d_int8_noalloc_need bytes must not exceed conv2d_int8_noalloc_max().
 // Calls that overlap on one device share the region and race.

@@ -187,6 +187,24 @@ int acfun_dev_conv2d_int8(const float* input, int N, int H, int W, int Cin,
                           const int8_t* wq, const float* wscale, const float* bias,
                           int KH, int KW, int Cout, int stride, int pad, float* output,
                           int act, void* stream);
+/* The int8-in / int8-out convolution: the requantized int8 output the
+ * reference's int8 path has no entry point for (it returns float,
+ * src/conv_int8.cpp:63-148), so int8 layers can chain without float tensors.
+ * input: s8 NHWC [N,H,W,Cin], the activations quantized with per-tensor scale
+ * *s_in (a device float; x = q * s_in, and *s_in == 0 marks an all-zero
+ * input).  The float result y is exactly acfun_conv2d_int8's on x with its
+ * activation scale equal to *s_in (same routes, epilogues, bias and ReLU);
+ * output: s8 NHWC [N,OH,OW,Cout] = clamp(round(y * 127/max|y|), -128, 127)
+ * with max over the whole output, and *s_out = max|y|/127 (device; 0 and an
+ * all-zero output when max|y| < 1e-12).  out_rule 0 rounds half to even (the
+ * rule of acfun_quantize_u8, src/int8_quantize_avx512.cpp:15-20); 1 rounds as
+ * the Winograd route quantizes its input (src/winograd_int8.cpp:306-325), so
+ * the output equals what a following 3x3/s1/p1 int8 conv would have made of
+ * y.  Returns 0, or -1 with acfun_last_error(). */
+int acfun_dev_conv2d_int8_q(const int8_t* input, const float* s_in, int N, int H, int W,
+                            int Cin, const int8_t* wq, const float* wscale, const float* bias,
+                            int KH, int KW, int Cout, int stride, int pad, int8_t* output,
+                            float* s_out, int act, int out_rule, void* stream);
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): acfun_dev_conv2d_int8 with every temporary (quantized

@@ -69,6 +69,8 @@ def lib():
                                    _f, _f32p, _i],
             "oracle_requantize_s8": [_f32p, _sz, _i8p],
             "oracle_wino_int8_epilogue": [_i32p, _sz, _i, _f, _f32p, _vp, _f32p, _i],
+            "oracle_conv2d_int8_q": [_i8p, _f, _i, _i, _i, _i, _i8p, _f32p, _vp, _i, _i, _i, _i,
+                                     _i, _i8p, C.POINTER(_f), _i, _i],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -266,6 +268,20 @@ def wino_int8_epilogue(acc, s_in, ws, b, act):
                                     np.float32(s_in), np.ascontiguousarray(ws, np.float32),
                                     ptr(b), out, act)
     return out
+
+
+def conv2d_int8_q(q, s_in, wq, ws, b, KH, KW, Cout, stride, pad, act, rule=0):
+    """(out s8 [N,OH,OW,Cout], s_out): the int8-in / int8-out convolution
+    (oracle_conv2d_int8_q) of s8 activations q with per-tensor scale s_in."""
+    N, H, W, Cin = q.shape
+    OH, OW = out_hw(H, W, KH, KW, stride, pad)
+    out = np.zeros((N, max(OH, 0), max(OW, 0), Cout), np.int8)
+    so = C.c_float(0.0)
+    lib().oracle_conv2d_int8_q(np.ascontiguousarray(q, np.int8), np.float32(s_in), N, H, W, Cin,
+                               np.ascontiguousarray(wq, np.int8),
+                               np.ascontiguousarray(ws, np.float32), ptr(b), KH, KW, Cout, stride,
+                               pad, out, C.byref(so), act, rule)
+    return out, np.float32(so.value)
 
 
 def conv2d_int8_route(H, W, Cin, KH, KW, Cout, stride, pad):

@@ -751,3 +751,80 @@ EXPORT float oracle_requantize_s8(const float* y, size_t n, int8_t* q) {
     for (size_t i = 0; i < n; ++i) q[i] = (int8_t)(quant_one(y[i], inv, 128, 0) - 128);
     return maxa / 127.0f;
 }
+
+/* The int8-in / int8-out convolution (the build-defined requantized output,
+ * no reference counterpart of its own).  Input: s8 activations q [N,H,W,Cin]
+ * with per-tensor scale s_in (x = q * s_in; s_in == 0 marks an all-zero
+ * input).  The float result y is exactly what acfun_conv2d_int8
+ * (src/conv_int8.cpp:63-148) computes from u8 = q + 128 with its activation
+ * scale sa = s_in: the Winograd route's fmaf((float)(4A), fl(fl(sa*0.25)*ws), b)
+ * (src/winograd_int8.cpp:154-170) for 3x3/s1/p1, else the direct / 1x1 /
+ * im2col+GEMM epilogue fl(fl((float)acc_u*alpha)+beta) with
+ * alpha = fl(sa*ws), beta = fl(b - fl(fl(alpha*128)*Sw)) (:100-107); every
+ * image computed from its own pixels.  Then y is requantized per tensor:
+ * maxy = max|y|; maxy < 1e-12 -> out = 0 and *s_out = 0; else
+ * inv = 127/maxy, *s_out = maxy/127, out = clamp(rule(y*inv), -128, 127) with
+ * rule 0 = RNE (acfun_quantize_u8, src/int8_quantize_avx512.cpp:15-20) and
+ * rule 1 = the rule the Winograd route applies to its own input
+ * (half-away-by-add on channels below Cout & ~15, lroundf above,
+ * src/winograd_int8.cpp:306-325), so the s8 tensor is what the next layer
+ * would have quantized the float tensor to. */
+EXPORT void oracle_conv2d_int8_q(const int8_t* q, float s_in, int N, int H, int W, int Cin,
+                                 const int8_t* wq, const float* wscale, const float* bias,
+                                 int KH, int KW, int Cout, int stride, int pad, int8_t* out,
+                                 float* s_out, int act, int rule) {
+    int OH = (H + 2 * pad - KH) / stride + 1;
+    int OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH <= 0 || OW <= 0) return;
+    size_t M = (size_t)N * OH * OW;
+    size_t inN = (size_t)N * H * W * Cin;
+    float* y = (float*)malloc(sizeof(float) * (M * (size_t)Cout > 0 ? M * (size_t)Cout : 1));
+    if (s_in == 0.0f) {
+        memset(y, 0, sizeof(float) * M * Cout);
+    } else {
+        uint8_t* u = (uint8_t*)malloc(inN ? inN : 1);
+        for (size_t i = 0; i < inN; ++i) u[i] = (uint8_t)((int)q[i] + 128);
+        int route = oracle_conv2d_int8_route(H, W, Cin, KH, KW, Cout, stride, pad);
+        if (route == I8_WINO) {
+            int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (M * (size_t)Cout > 0 ? M * (size_t)Cout : 1));
+            oracle_conv_int8_centered_acc(u, N, H, W, Cin, wq, 3, 3, Cout, 1, 1, OH, OW, acc);
+            oracle_wino_int8_epilogue(acc, M, Cout, s_in, wscale, bias, y, act);
+            free(acc);
+        } else {
+            int K = KH * KW * Cin;
+            float* alpha = (float*)malloc(sizeof(float) * Cout);
+            float* beta = (float*)malloc(sizeof(float) * Cout);
+            for (int j = 0; j < Cout; ++j) {
+                float Swj = 0.0f;
+                for (int k = 0; k < K; ++k) Swj += (float)wq[(size_t)k * Cout + j];
+                float a = s_in * wscale[j];
+                alpha[j] = a;
+                float t = a * 128.0f;
+                t = t * Swj;
+                beta[j] = (bias ? bias[j] : 0.0f) - t;
+            }
+            if (route == I8_1X1)
+                oracle_conv1x1_int8(u, (int)M, K, Cout, wq, alpha, beta, y, act);
+            else
+                oracle_conv2d_int8_direct(u, N, H, W, Cin, wq, alpha, beta, KH, KW, Cout, stride,
+                                          pad, OH, OW, y, act);
+            free(alpha); free(beta);
+        }
+        free(u);
+    }
+    float maxy = oracle_absmax(y, M * Cout);
+    if (maxy < 1e-12f) {
+        memset(out, 0, M * Cout);
+        *s_out = 0.0f;
+    } else {
+        float inv = 127.0f / maxy;
+        int cvec = Cout & ~15;
+        for (size_t i = 0; i < M; ++i)
+            for (int c = 0; c < Cout; ++c) {
+                int mode = rule == 0 ? 0 : (c < cvec ? 2 : 1);
+                out[i * Cout + c] = (int8_t)(quant_one(y[i * Cout + c], inv, 128, mode) - 128);
+            }
+        *s_out = maxy / 127.0f;
+    }
+    free(y);
+}

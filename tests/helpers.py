@@ -68,3 +68,23 @@ def bf16_probe_values(rng):
 
 def same_or_both_nan(a, b):
     return bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+
+
+def int8_q_inputs(rng, N, H, W, Cin, KH, KW, Cout, bias=True):
+    """s8 activations q (|q| <= 127, with +-127 present) and a scale s_in such
+    that the float tensor x = fl(q * s_in) has max|x|/127 == s_in exactly in
+    float32: the reference's acfun_conv2d_int8 on x then quantizes x back to q
+    with activation scale s_in (its int8-input equivalent).  Returns
+    (q, s_in, x, wq, ws, b)."""
+    q = rng.integers(-127, 128, size=(N, H, W, Cin)).astype(np.int8)
+    q.reshape(-1)[0] = 127
+    q.reshape(-1)[-1] = -127
+    while True:
+        s_in = np.float32(rng.uniform(0.005, 0.05))
+        if np.float32(np.float32(127.0) * s_in) / np.float32(127.0) == s_in:
+            break
+    x = (q.astype(np.float32) * s_in).astype(np.float32)
+    wq = rng.integers(-127, 128, size=(KH * KW * Cin, Cout)).astype(np.int8)
+    ws = rng.uniform(0.005, 0.05, Cout).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32) if bias else None
+    return q, s_in, x, wq, ws, b

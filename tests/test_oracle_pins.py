@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import (P, assert_bitexact, bf16_probe_values, f32, int8_conv_inputs, rel_err,
-                           s8, same_or_both_nan, u8)
+from tests.helpers import (P, assert_bitexact, bf16_probe_values, f32, int8_conv_inputs,
+                           int8_q_inputs, rel_err, s8, same_or_both_nan, u8)
 
 EPI_SHAPES = [(64, 64, 64), (100, 100, 100), (255, 255, 255), (127, 129, 63), (16, 16, 16),
               (1, 16, 255), (513, 17, 131), (4, 4, 4), (33, 65, 129), (1023, 4, 7), (7, 1023, 5)]
@@ -357,3 +357,56 @@ def test_reference_int8_gemm_route_batch_defect(ref, rng):
         ref.acfun_conv2d_int8(P(pair), 2, H, H, Cin, P(wq), P(ws), P(b), 3, 3, Cout, 2, 1,
                               np.float32(0), P(y2), 0)
         assert_bitexact(got[n], y2[0], f"image {n} with the batch scale")
+
+
+# (N, H, W, Cin, KH, KW, Cout, stride, pad): every int8 route; N = 1 on the
+# im2col + GEMM route (the reference unrolls image 0 only there)
+Q8_CASES = [
+    (2, 10, 12, 16, 3, 3, 24, 1, 1),     # Winograd
+    (2, 9, 9, 20, 3, 3, 19, 1, 1),       # Winograd, channel tails in and out
+    (2, 14, 14, 32, 1, 1, 48, 1, 0),     # 1x1
+    (2, 12, 12, 3, 3, 3, 16, 1, 1),      # Cin 3 -> direct
+    (1, 15, 15, 16, 3, 3, 32, 2, 1),     # im2col + GEMM
+    (2, 11, 11, 8, 1, 1, 16, 2, 0),      # 1x1 s2, K = 8 -> direct
+]
+
+
+@pytest.mark.parametrize("shape", Q8_CASES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv2d_int8_q_against_reference(ref, rng, shape, act):
+    """oracle_conv2d_int8_q (s8 in with scale s_in, s8 out requantized per
+    tensor) against the reference's own API: its acfun_conv2d_int8 on
+    x = fl(q * s_in), which quantizes back to exactly q with activation scale
+    s_in (max|x|/127 == s_in), then its acfun_quantize_u8(y, 127/max|y|, 128) - 128
+    for rule 0.  Rule 1 (the Winograd route's input rule) is checked with
+    oracle.quantize_wino_u8, pinned by test_winograd_int8_identity."""
+    N, H, W, Cin, KH, KW, Cout, st, pd = shape
+    q, s_in, x, wq, ws, b = int8_q_inputs(rng, N, H, W, Cin, KH, KW, Cout)
+    assert np.float32(np.max(np.abs(x))) / np.float32(127) == s_in
+    OH, OW = oracle.out_hw(H, W, KH, KW, st, pd)
+    y = np.empty((N, OH, OW, Cout), np.float32)
+    ref.acfun_conv2d_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), KH, KW, Cout, st, pd,
+                          np.float32(0), P(y), act)
+    maxy = np.float32(np.max(np.abs(y)))
+    inv = np.float32(127.0) / maxy
+    u = np.empty(y.size, np.uint8)
+    ref.acfun_quantize_u8(P(y), P(u), y.size, inv, 128)
+    want0 = (u.astype(np.int16) - 128).astype(np.int8).reshape(y.shape)
+    got0, s0 = oracle.conv2d_int8_q(q, s_in, wq, ws, b, KH, KW, Cout, st, pd, act, rule=0)
+    assert_bitexact(got0, want0, "rule 0")
+    assert s0 == maxy / np.float32(127.0)
+    got1, s1 = oracle.conv2d_int8_q(q, s_in, wq, ws, b, KH, KW, Cout, st, pd, act, rule=1)
+    want1 = (oracle.quantize_wino_u8(y, inv).astype(np.int16) - 128).astype(np.int8)
+    assert_bitexact(got1, want1, "rule 1")
+    assert s1 == s0
+
+
+def test_conv2d_int8_q_zero(rng):
+    """s_in == 0 marks an all-zero input: zero output and s_out = 0, as the
+    reference returns zeros without the bias for max|x| < 1e-12
+    (src/conv_int8.cpp:78)."""
+    q = np.zeros((1, 6, 6, 8), np.int8)
+    wq = rng.integers(-127, 128, (72, 8)).astype(np.int8)
+    out, so = oracle.conv2d_int8_q(q, 0.0, wq, np.full(8, 0.01, np.float32),
+                                   np.full(8, 0.5, np.float32), 3, 3, 8, 1, 1, 1)
+    assert so == 0.0 and not np.any(out)
