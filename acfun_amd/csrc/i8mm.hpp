@@ -97,7 +97,11 @@ __device__ __forceinline__ int udiv_small(int a, int b, float rb) {
 
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-constexpr size_t i8mm_lds(int BM, int BN, int NST) { return (size_t)NST * (BM + BN) * 128; }
+// LDS of k_i8mm: NST operand stages, then NST slots of the per-channel
+// epilogue parameters of a tile (three arrays of BN words each).
+constexpr size_t i8mm_lds(int BM, int BN, int NST) {
+    return (size_t)NST * (BM + BN) * 128 + (size_t)NST * 3 * BN * 4;
+}
 
 template <int BM, int BN, int NST, int AM, int EPI, int OUT>
 __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
@@ -142,6 +146,25 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         __builtin_amdgcn_make_buffer_rsrc((void*)p.A, (short)0, (int)p.a_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t bres =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.Bt, (short)0, (int)p.b_bytes, 0x00020000);
+    // The tile's per-channel epilogue parameters travel by the same LDS DMA as
+    // the operands (issued just before the items of the tile's last chunk, so
+    // the wait for that chunk covers them), into slot (tile index mod NST):
+    // array 0 alpha (or the weight scales), 1 beta (or the bias), 2 the weight
+    // column sums.  A missing array is a zero-length buffer and reads as 0.
+    // No vector load of the loop then has a register result, which would
+    // make the compiler wait for every DMA in flight.
+    constexpr int PSLOT = 3 * BN * 4;
+    int8_t* const prm = sm8 + NST * STG;
+    const float* pa0 = p.alpha ? p.alpha : p.ws;
+    const float* pa1 = (EPI == EPI_GEMM && p.alpha) ? p.beta : p.bias;
+    const int* pa2 = EPI == EPI_GEMM ? p.Sw : nullptr;
+    // wave w (< 3) loads array w: one descriptor per wave from scalar selects
+    const void* pbase = wave == 0 ? (const void*)pa0
+                      : wave == 1 ? (pa1 ? (const void*)pa1 : (const void*)pa0)
+                                  : (pa2 ? (const void*)pa2 : (const void*)pa0);
+    const int psize = wave == 0 ? p.N * 4 : wave == 1 ? (pa1 ? p.N * 4 : 0) : (pa2 ? p.N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)pbase, (short)0, psize, 0x00020000);
 
     // ---- DMA rows of this lane: row 8*(wave + 4t) + lane/8 of the A and B
     // stages, quad slot lane%8 holding data quad aq/bq
@@ -169,9 +192,12 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         hi = hi < 8 ? hi : 8;
         return hi > lo ? (1u << hi) - (1u << lo) : 0u;
     };
+    int ik = 0;                                       // the issue cursor's tile (index in this workgroup)
+    int itn = 0;                                      // column block of the issue cursor's tile
     auto setup = [&](int k) {
         const int L = t0 + k * tstr;
         const int tm = L / p.gn, tn = L - tm * p.gn;
+        itn = tn;
 #pragma unroll
         for (int t = 0; t < AIT; ++t) {
             const int m = tm * BM + 8 * (wave + 4 * t) + rl;
@@ -224,6 +250,13 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     const int taps = p.K / p.Cinp;
     auto tap_off = [&](int kh, int kw) { return (kh * p.W + kw) * p.Cinp; };
     auto issue = [&](int t, int c, int8_t* st) {      // DMA item t of chunk c into stage st
+        if (t == 0 && c == nch - 1 && wave < 3) {     // the tile's epilogue parameters
+            if (lane < BN / 4) {
+                const unsigned off = (unsigned)((itn * BN + 4 * lane) * 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    prs, (lds_void*)(prm + (ik % NST) * PSLOT + wave * BN * 4), 16, off, 0, 0, 0);
+            }
+        }
         if (t < AIT) {
             unsigned v = kOOB;
             if (AM == AM_GEN) {
@@ -295,8 +328,20 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
+    // OUT_Q8: the first pass's partial maxima (at most kAmaxParts = 768 floats)
+    // come by DMA into the last stage, which the prologue leaves free; they are
+    // reduced after the first chunk's wait, which covers them.
+    static_assert(kAmaxParts <= 768, "k_i8mm: the partial maxima fill at most 3 DMA rows");
+    if (OUT == OUT_Q8 && wave < 3) {
+        const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)p.qparts, (short)0, p.nqparts * 4, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            qrs, (lds_void*)(sm8 + (NST - 1) * STG + wave * 1024), 16,
+            (unsigned)(wave * 1024 + 16 * lane), 0, 0, 0);
+    }
+
     // ---- prologue: the first AHEAD chunks of the item stream (tile, chunk)
-    int ik = 0, ic = 0;                         // issue cursor
+    int ic = 0;                                 // issue cursor: chunk of tile ik
     if (nit > 0) setup(0);
 #pragma unroll
     for (int a = 0; a < AHEAD; ++a) {
@@ -318,10 +363,13 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     // DMA is already in flight; these loads sit behind it in the counter)
     float qinv = 0.0f;
     bool qzero = false;
-    if (OUT == OUT_Q8) {
+    // the output's max|v| from the partials (slots past nqparts read 0)
+    auto reduce_qparts = [&]() {
         __shared__ float qred[4];
-        float m = 0.0f;
-        for (int i = tid; i < p.nqparts; i += 256) { const float a = p.qparts[i]; m = a > m ? a : m; }
+        const float* qp = (const float*)(sm8 + (NST - 1) * STG);
+        float m = qp[tid];
+        m = qp[tid + 256] > m ? qp[tid + 256] : m;
+        m = qp[tid + 512] > m ? qp[tid + 512] : m;
         for (int off = 32; off > 0; off >>= 1) {
             const float o = __shfl_xor(m, off, 64);
             m = o > m ? o : m;
@@ -333,10 +381,13 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         qzero = m < 1e-12f;                     // as src/conv_int8.cpp:78 for the consumer
         qinv = 127.0f / m;
         if (blockIdx.x == 0 && tid == 0) p.s_out[0] = qzero ? 0.0f : m / 127.0f;
+    };
+    if (OUT == OUT_Q8 && nit == 0) {            // (no tile: the partials have landed after this wait)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        reduce_qparts();
     }
     int st = 0, ck = 0, cc = 0;                 // compute cursor
-    float pv0[FN], pv1[FN];                     // epilogue inputs of the current tile
-    int pv2[FN];
     float amx = 0.0f;                           // max|stored value| of this lane
     for (int g = 0; g < nit; ++g) {
         // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
@@ -351,35 +402,33 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         else if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * ITEMS));
         else __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // (before this iteration's DMA reuses the stage the partials came into)
+        if (OUT == OUT_Q8 && g == 0) reduce_qparts();
         const int L = t0 + ck * tstr;
         const int tm = L / p.gn, tn = L - tm * p.gn;
         const int m0 = tm * BM, n0 = tn * BN;
-        if (cc == 0) {                          // the tile's epilogue inputs, a chunk early
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int n = n0 + wn * (BN / 2) + 32 * j + r32;
-                const int nn = n < p.N ? n : p.N - 1;
-                pv0[j] = p.alpha ? p.alpha[nn] : p.ws[nn];
-                pv1[j] = (EPI == EPI_GEMM && p.alpha) ? p.beta[nn] : (p.bias ? p.bias[nn] : 0.0f);
-                pv2[j] = EPI == EPI_GEMM ? p.Sw[nn] : 0;
-            }
-        }
         const int8_t* S = sm8 + st * STG;
         const int sta = st == 0 ? NST - 1 : st - 1;   // (g + AHEAD) % NST
         int8_t* NA = sm8 + sta * STG;
         const bool more = g + AHEAD < nit;
+        // All of the chunk's operand reads go out first (one LDS round trip per
+        // chunk instead of one per k-step), then the MFMAs with the DMA of
+        // chunk g + AHEAD issued between them.
+        i4 fa[4][FM], fb[4][FN];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            i4 fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = *(const i4*)(S + rda[s][i]);
+            for (int i = 0; i < FM; ++i) fa[s][i] = *(const i4*)(S + rda[s][i]);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) fb[j] = *(const i4*)(S + rdb[s][j]);
+            for (int j = 0; j < FN; ++j) fb[s][j] = *(const i4*)(S + rdb[s][j]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
             if (more) {
 #pragma unroll
                 for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, ic, NA);
@@ -397,9 +446,18 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         if (++cc < nch) continue;
         // ---- epilogue of tile ck: lane l, register e of block (i, j) <->
         //      row m0 + wm*BM/2 + 32i + 8(e/4) + 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32
-        if (nch == 1) {                          // parameters were loaded in this iteration
-            if (more) __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
+        // the tile's parameters landed with its last chunk (waited for above)
+        float pv0[FN], pv1[FN];
+        int pv2[FN];
+        {
+            const int8_t* ps = prm + (ck % NST) * PSLOT;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = wn * (BN / 2) + 32 * j + r32;
+                pv0[j] = ((const float*)ps)[col];
+                pv1[j] = ((const float*)(ps + BN * 4))[col];
+                pv2[j] = ((const int*)(ps + 2 * BN * 4))[col];
+            }
         }
         const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
         const bool relu1 = p.act == 1, relu2 = p.act == 2;
@@ -448,10 +506,9 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                         const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3), n = nb + 32 * j;
                         const float v = act_select(epi(acc[i][j][e], j), relu1, relu2);
                         acc[i][j][e] = 0;
-                        if (full || (m < p.M && n < p.N)) {
-                            const float av = fabsf(v);
-                            amx = av > amx ? av : amx;       // NaN never wins
-                        }
+                        // (a select, not a branch per element)
+                        const float av = (full || (m < p.M && n < p.N)) ? fabsf(v) : 0.0f;
+                        amx = av > amx ? av : amx;           // NaN never wins
                     }
         } else if (STAGED) {
             // (1) every wave is done reading the last chunk's stage; (2) each wave
@@ -512,6 +569,12 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                 const int r = tid >> 2, c0 = 16 * (tid & 3);
                 const int m = m0 + r, n = n0 + c0;
                 if (m < p.M && n < p.ldq) {
+                    // straight-line per element: all three rounding forms are
+                    // formed and selected (rule 0: RNE; rule 1: the add-then-
+                    // truncate rule below N & ~15, lroundf's half-away above),
+                    // then clamped; padding columns and an all-zero output give 0
+                    const int cvec = p.N & ~15;
+                    const bool rne = p.rule == 0;
                     unsigned w4[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
                     for (int k4 = 0; k4 < 4; ++k4) {
@@ -519,18 +582,13 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const int c = n + 4 * k4 + k;
-                            int qv = 0;
-                            if (c < p.N && !qzero) {
-                                const float t = __fmul_rn(act_select(v[k], relu1, relu2), qinv);
-                                int rq;
-                                if (p.rule == 0 || c >= (p.N & ~15)) {
-                                    rq = p.rule == 0 ? (int)rintf(t) : (int)roundf(t);
-                                } else {
-                                    rq = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
-                                }
-                                rq = rq < -128 ? -128 : (rq > 127 ? 127 : rq);
-                                qv = rq;
-                            }
+                            const float t = __fmul_rn(act_select(v[k], relu1, relu2), qinv);
+                            const float r_even = rintf(t);
+                            const float r_away = roundf(t);
+                            const float r_add = truncf(__fadd_rn(t, copysignf(0.5f, t)));
+                            float rq = rne ? r_even : (c < cvec ? r_add : r_away);
+                            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+                            const int qv = (c < p.N && !qzero) ? (int)rq : 0;
                             w4[k4] |= ((unsigned)qv & 0xffu) << (8 * k);
                         }
                     }
