@@ -20,7 +20,7 @@ namespace acfun {
 // conv2d_impl of the reference (src/layers.cpp:106-195), route for route.
 bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float* w,
                       const float* bias, int KH, int KW, int Cout, int stride, int pad, int groups,
-                      float* out, int act, hipStream_t s) {
+                      float* out, int act, hipStream_t s, const float* wino_U) {
     if (groups > 1) {
         if (groups == Cin && groups == Cout)  // :112-116
             return dwconv_f32(in, N, H, W, Cin, w, bias, KH, KW, stride, pad, out, act, s);
@@ -59,7 +59,7 @@ bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float
     if (KH == 3 && KW == 3 && stride == 1 && pad == 1 && H >= 3 && W >= 3 && Cin >= 4 &&
         Cout >= 4) {  // :169-176
         int tile = (H >= 112 && W >= 112 && Cin >= 64 && Cout >= 64) ? 4 : 2;
-        return winograd_route_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
+        return winograd_route_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s, wino_U);
     }
     int OH = (H + 2 * pad - KH) / stride + 1;  // :178-194
     int OW = (W + 2 * pad - KW) / stride + 1;
@@ -510,6 +510,31 @@ int acfun_dev_conv2d_int8_noalloc(const float* input, int N, int H, int W, int C
     if (OH <= 0 || OW <= 0) return 0;
     ConvShape g{N, H, W, Cin, KH, KW, stride, pad, OH, OW};
     return conv2d_int8_noalloc(input, g, wq, wscale, bias, Cout, output, act, resolve(stream))
+               ? 0 : -1;
+}
+
+int acfun_dev_conv2d_dw_maxpool(const float* input, int N, int H, int W, int C,
+                                const float* weight, const float* bias, int KH, int KW, int stride,
+                                int pad, int act, int pool, int pool_stride, int pool_pad,
+                                float* output, int post_relu, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0 || pool_stride <= 0 || KH <= 0 || KW <= 0 || pool <= 0) return 0;
+    const int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return 0;
+    const int PH = conv_out(OH, pool, pool_stride, pool_pad),
+              PW = conv_out(OW, pool, pool_stride, pool_pad);
+    if (PH <= 0 || PW <= 0) return 0;
+    hipStream_t s = resolve(stream);
+    if (dwconv_pool_ok(H, W, C, KH, KW, stride, pad, pool, pool_stride, pool_pad, input, weight,
+                       output))
+        return dwconv_pool_f32(input, N, H, W, C, weight, bias, stride, pad, act, pool_pad, output,
+                               post_relu, s) ? 0 : -1;
+    // other shapes: the two kernels through a pooled intermediate
+    Scratch y((size_t)N * OH * OW * C * sizeof(float), s);
+    if (!y.p) return -1;
+    return dwconv_f32(input, N, H, W, C, weight, bias, KH, KW, stride, pad, y.as<float>(), act, s) &&
+                   maxpool_f32(y.as<float>(), N, OH, OW, C, pool, pool_stride, pool_pad, output,
+                               post_relu, s)
                ? 0 : -1;
 }
 

@@ -244,6 +244,128 @@ __global__ __launch_bounds__(256) void k_maxpool3s2_row(const float4* __restrict
     }
 }
 
+// Depthwise 3x3 (stride S) + activation fused with the 3x3 / stride-2 MaxPool
+// that follows it (pool padding PP), for C % 4 == 0: the depthwise output
+// never reaches HBM.  A workgroup (5 waves) owns image n, pool rows
+// ph0, ph0+1, pool columns pw0 .. pw0+13 and 8 channel quads.  Phase 1: wave
+// w computes depthwise output row y0 + w (y0 = 2*ph0 - PP) for columns
+// x0 .. x0+28 (x0 = 2*pw0 - PP) into LDS, a lane owning 4 consecutive columns
+// of one quad (the column loads shared between them); the arithmetic per
+// channel is k_dwconv3_blk's (the reference's: bias, fmaf per in-range tap in
+// kh, kw order, then the activation).  Phase 2: each pooled value is the max
+// from -1e30 over its in-range taps in kh, kw order (max_ps), then the optional
+// ReLU -- the two reference calls' results bit for bit.
+constexpr int DWP_ROWS = 5, DWP_PWB = 14, DWP_COLS = 2 * DWP_PWB + 1, DWP_Q = 8;
+template <int S>
+__global__ __launch_bounds__(320) void k_dwconv3_pool(const float4* __restrict__ in, int H, int W,
+                                                      int C4, const float* __restrict__ w,
+                                                      const float* __restrict__ bias, int pad,
+                                                      int OH, int OW, int act, int PP, int PH,
+                                                      int PW, int nPHB, int nPWB, int nQG,
+                                                      float4* __restrict__ out, int post_relu) {
+    __shared__ float4 ys[DWP_ROWS][DWP_COLS][DWP_Q];
+    int b = blockIdx.x;
+    const int qg = b % nQG;
+    b /= nQG;
+    const int pwb = b % nPWB;
+    b /= nPWB;
+    const int phb = b % nPHB;
+    const int n = b / nPHB;
+    const int ph0 = 2 * phb, pw0 = DWP_PWB * pwb;
+    const int y0 = 2 * ph0 - PP, x0 = 2 * pw0 - PP;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // ---- phase 1: depthwise row y0 + wave, lane = (column run r, quad q)
+    {
+        const int q = lane & 7, run = lane >> 3;         // 8 runs of 4 columns cover 29
+        const int c4 = qg * DWP_Q + q;
+        const int yr = y0 + wave;
+        const int yc0 = x0 + 4 * run;
+        const bool live = c4 < C4 && (unsigned)yr < (unsigned)OH;
+        float4 acc[4];
+        if (live) {
+            const int c = 4 * c4;
+            float wk[4][9];
+            const float4* w4 = (const float4*)(w + (size_t)c * 9);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) {
+                const float4 v = w4[i];
+                wk[(4 * i + 0) / 9][(4 * i + 0) % 9] = v.x;
+                wk[(4 * i + 1) / 9][(4 * i + 1) % 9] = v.y;
+                wk[(4 * i + 2) / 9][(4 * i + 2) % 9] = v.z;
+                wk[(4 * i + 3) / 9][(4 * i + 3) % 9] = v.w;
+            }
+            const float4 b4 = bias ? make_float4(bias[c], bias[c + 1], bias[c + 2], bias[c + 3])
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int o = 0; o < 4; ++o) acc[o] = b4;
+            const float4* img = in + (size_t)n * H * W * C4 + c4;
+            constexpr int NCOL = 3 * S + 3;              // input columns of 4 outputs
+            const int iw0 = yc0 * S - pad;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ih = yr * S - pad + kh;
+                if ((unsigned)ih >= (unsigned)H) continue;
+                float4 col[NCOL];
+                bool cok[NCOL];
+#pragma unroll
+                for (int j = 0; j < NCOL; ++j) {
+                    const int iw = iw0 + j;
+                    cok[j] = (unsigned)iw < (unsigned)W;
+                    col[j] = cok[j] ? img[((size_t)ih * W + iw) * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+#pragma unroll
+                    for (int kw = 0; kw < 3; ++kw) {
+                        const int j = o * S + kw;
+                        const int tp = kh * 3 + kw;
+                        if (cok[j]) {
+                            acc[o].x = fmaf(col[j].x, wk[0][tp], acc[o].x);
+                            acc[o].y = fmaf(col[j].y, wk[1][tp], acc[o].y);
+                            acc[o].z = fmaf(col[j].z, wk[2][tp], acc[o].z);
+                            acc[o].w = fmaf(col[j].w, wk[3][tp], acc[o].w);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < 4; ++o) {
+            const int cc = 4 * run + o;
+            if (cc >= DWP_COLS) break;
+            float4 v = acc[o];
+            v.x = act_apply(v.x, act); v.y = act_apply(v.y, act);
+            v.z = act_apply(v.z, act); v.w = act_apply(v.w, act);
+            if (live) ys[wave][cc][q] = v;
+        }
+    }
+    __syncthreads();
+    // ---- phase 2: 2 pool rows x 14 pool columns x 8 quads
+    if (tid < 2 * DWP_PWB * DWP_Q) {
+        const int q = tid & 7, pc = (tid >> 3) % DWP_PWB, pr = (tid >> 3) / DWP_PWB;
+        const int ph = ph0 + pr, pw = pw0 + pc, c4 = qg * DWP_Q + q;
+        if (ph < PH && pw < PW && c4 < C4) {
+            float4 m = make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int yr = 2 * ph - PP + kh;
+                if ((unsigned)yr >= (unsigned)OH) continue;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int yc = 2 * pw - PP + kw;
+                    if ((unsigned)yc >= (unsigned)OW) continue;
+                    const float4 v = ys[yr - y0][yc - x0][q];
+                    m.x = vmax(m.x, v.x); m.y = vmax(m.y, v.y); m.z = vmax(m.z, v.z); m.w = vmax(m.w, v.w);
+                }
+            }
+            if (post_relu) {
+                m.x = vmax(m.x, 0.f); m.y = vmax(m.y, 0.f); m.z = vmax(m.z, 0.f); m.w = vmax(m.w, 0.f);
+            }
+            out[(((size_t)n * PH + ph) * PW + pw) * C4 + c4] = m;
+        }
+    }
+}
+
 // Grouped direct conv, weights [g][KH*KW*Cin_p][Cout_p].  vec_end / fma_all
 // encode which channels the reference's dispatcher (src/group_conv.cpp:60-79)
 // runs through a fused-multiply-add vector kernel.
@@ -570,6 +692,40 @@ bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, con
     ACFUN_LAUNCH("k_dwconv", k_dwconv, grid1d(total), dim3(256), 0, s, in, N, H, W, C, w, bias, KH, KW,
                        stride, pad, OH, OW, out, act);
     return check_launch("k_dwconv");
+}
+
+bool dwconv_pool_ok(int H, int W, int C, int KH, int KW, int stride, int pad, int pool,
+                    int pstride, int ppad, const void* in, const void* w, const void* out) {
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    return KH == 3 && KW == 3 && (stride == 1 || stride == 2) && C % 4 == 0 && pool == 3 &&
+           pstride == 2 && (ppad == 0 || ppad == 1) && OH > 0 && OW > 0 &&
+           (OH + 2 * ppad - 3) / 2 + 1 > 0 && (OW + 2 * ppad - 3) / 2 + 1 > 0 &&
+           ((((uintptr_t)in) | ((uintptr_t)w) | ((uintptr_t)out)) & 15u) == 0;
+}
+
+bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w,
+                     const float* bias, int stride, int pad, int act, int ppad, float* out,
+                     int post_relu, hipStream_t s) {
+    const int OH = (H + 2 * pad - 3) / stride + 1, OW = (W + 2 * pad - 3) / stride + 1;
+    const int PH = (OH + 2 * ppad - 3) / 2 + 1, PW = (OW + 2 * ppad - 3) / 2 + 1;
+    if (OH <= 0 || OW <= 0 || PH <= 0 || PW <= 0 || N <= 0) return true;
+    const int C4 = C / 4;
+    const int nPHB = (PH + 1) / 2, nPWB = (PW + DWP_PWB - 1) / DWP_PWB,
+              nQG = (C4 + DWP_Q - 1) / DWP_Q;
+    const long long blocks = (long long)N * nPHB * nPWB * nQG;
+    if (blocks >= (1ll << 31)) {
+        set_error("dwconv_pool: grid too large");
+        return false;
+    }
+    if (stride == 1)
+        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<1>, dim3((unsigned)blocks), dim3(320), 0, s,
+                     (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
+                     nPWB, nQG, (float4*)out, post_relu);
+    else
+        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<2>, dim3((unsigned)blocks), dim3(320), 0, s,
+                     (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
+                     nPWB, nQG, (float4*)out, post_relu);
+    return check_launch("k_dwconv3_pool");
 }
 
 bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,

@@ -1429,58 +1429,80 @@ bool launch_wino23p(const float* in, const float* U, const float* bias, float* o
     return check_launch("k_wino23p");
 }
 
-bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
-                int Cout, float* out, int act, hipStream_t s) {
-    int tH = (H + 1) / 2, tW = (W + 1) / 2;
-    int Cinp = (Cin + 15) / 16 * 16;
+// Which F(2,3) engine run_wino23 takes for a shape: 1 the unit kernels (their
+// filter transform in the chunked layout), 0 k_wino23 (the plain layout), -1
+// neither (the implicit GEMM; no filter transform).
+int wino23_plan_impl(int N, int H, int W, int Cin, int Cout, const void* in) {
+    const int tH = (H + 1) / 2, tW = (W + 1) / 2;
+    const int Cinp = (Cin + 15) / 16 * 16;
     // The DMA staging moves whole 4-channel quads from 16-byte aligned rows.
-    if (Cin % 4 != 0 || ((uintptr_t)in & 15u) != 0) {
-        ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
-        return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
-    }
-    Scratch U((size_t)16 * Cout * Cinp * sizeof(float), s);
-    if (!U.p) return false;
+    if (Cin % 4 != 0 || ((uintptr_t)in & 15u) != 0) return -1;
     // 32-tile units (three workgroups per CU) when the image is wide enough to
     // fill them; buffer resources address one image and the filter with 32-bit
-    // byte offsets.  They read the chunked filter layout.
-    // Images of at most 4 x 4 tiles (5 to 8 pixels a side, ResNet-50's 7 x 7
-    // stage) run units of two images' tile blocks.
+    // byte offsets.  Images of at most 4 x 4 tiles (5 to 8 pixels a side,
+    // ResNet-50's 7 x 7 stage) run units of two images' tile blocks.
     const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
     const bool unit32 = (long long)H * W * Cin * 4 < (1ll << 31) &&
                         16ll * Cout * Cinp * 4 < (1ll << 31) && (long long)N * ((tH + 1) / 2) < 65536 &&
                         (tW >= 6 || small);
-    if (unit32) {
+    return unit32 ? 1 : 0;
+}
+
+// The filter transform for a plan (16 points x Cout x Cinp floats).
+bool wino23_filter_impl(const float* w, int Cin, int Cout, int plan, float* U, hipStream_t s) {
+    const int Cinp = (Cin + 15) / 16 * 16;
+    if (plan == 1)
         ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, true>), dim3((Cout + 15) / 16, Cinp / 16),
-                     dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
-        if (!check_launch("k_wino_filter_t")) return false;
+                     dim3(256), 0, s, w, Cin, Cinp, Cout, U);
+    else
+        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, false>), dim3((Cout + 15) / 16, Cinp / 16),
+                     dim3(256), 0, s, w, Cin, Cinp, Cout, U);
+    return check_launch("k_wino_filter_t");
+}
+
+// Upre: the filter already transformed for this shape's plan (a model's cached
+// transform), or null to transform it here.
+bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+                int Cout, float* out, int act, hipStream_t s, const float* Upre = nullptr) {
+    int tH = (H + 1) / 2, tW = (W + 1) / 2;
+    int Cinp = (Cin + 15) / 16 * 16;
+    const int plan = wino23_plan_impl(N, H, W, Cin, Cout, in);
+    if (plan < 0) {
+        ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
+        return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
+    }
+    Scratch Uown(Upre ? 0 : (size_t)16 * Cout * Cinp * sizeof(float), s);
+    if (!Upre && !Uown.p) return false;
+    const float* Up = Upre ? Upre : Uown.as<float>();
+    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
+    if (plan == 1) {
+        if (!Upre && !wino23_filter_impl(w, Cin, Cout, 1, Uown.as<float>(), s)) return false;
         bool launched = false;
         if (small) {
-            if (!launch_wino23p<4, 2>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+            if (!launch_wino23p<4, 2>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
                                       s, &launched))
                 return false;
             if (launched) return true;
         }
         if (tW >= 12) {
-            if (!launch_wino23p<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+            if (!launch_wino23p<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
                                     s, &launched))
                 return false;
             if (launched) return true;
-            return launch_wino23u<16>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
+            return launch_wino23u<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
                                       act, s);
         }
         // 8-wide units: the persistent kernel measured faster at 8 chunks per
         // unit and slower at 32 (ResNet-50's 14 x 14 x 256 stage)
         if (Cinp <= 64) {
-            if (!launch_wino23p<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s,
+            if (!launch_wino23p<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s,
                                    &launched))
                 return false;
             if (launched) return true;
         }
-        return launch_wino23u<8>(in, U.as<float>(), bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
+        return launch_wino23u<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
     }
-    ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, false>), dim3((Cout + 15) / 16, Cinp / 16),
-                 dim3(256), 0, s, w, Cin, Cinp, Cout, U.as<float>());
-    if (!check_launch("k_wino_filter_t")) return false;
+    if (!Upre && !wino23_filter_impl(w, Cin, Cout, 0, Uown.as<float>(), s)) return false;
     // Block: TC tile columns x R tile rows of one image, R*TC <= 128 slots and
     // two LDS buffers (padded X region + 16*32*16 filter floats) within 160 KB.
     auto buf_floats = [](int R, int TC) {
@@ -1509,7 +1531,7 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     }
     int rblocks = (tH + R - 1) / R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
-    ACFUN_LAUNCH("k_wino23", k_wino23, grid, dim3(512), lds, s, in, U.as<float>(), bias, out, N, H, W,
+    ACFUN_LAUNCH("k_wino23", k_wino23, grid, dim3(512), lds, s, in, Up, bias, out, N, H, W,
                        Cin, Cinp, Cout, tH, tW, R, TC, act);
     return check_launch("k_wino23");
 }
@@ -1535,15 +1557,28 @@ bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, co
 
 }  // namespace
 
+int wino23_plan(int N, int H, int W, int Cin, int Cout, const void* in) {
+    return wino23_plan_impl(N, H, W, Cin, Cout, in);
+}
+
+size_t wino23_filter_bytes(int Cin, int Cout) {
+    return (size_t)16 * Cout * ((Cin + 15) / 16 * 16) * sizeof(float);
+}
+
+bool wino23_filter(const float* w, int Cin, int Cout, int plan, float* U, hipStream_t s) {
+    return wino23_filter_impl(w, Cin, Cout, plan, U, s);
+}
+
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
-                  const float* bias, int Cout, float* out, int act, hipStream_t s) {
+                  const float* bias, int Cout, float* out, int act, hipStream_t s, const float* Upre) {
     if (N <= 0 || H <= 0 || W <= 0) return true;
     if (tile == 4) return run_fused<4, 16, 4, 8>(in, N, H, W, Cin, w, bias, Cout, out, act, s);
-    return run_wino23(in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    return run_wino23(in, N, H, W, Cin, w, bias, Cout, out, act, s, Upre);
 }
 
 bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
-                        const float* bias, int Cout, float* out, int act, hipStream_t s) {
+                        const float* bias, int Cout, float* out, int act, hipStream_t s,
+                        const float* Upre) {
     // Measured on MI355X at BASELINE config 2(b) (8 x 112^2 x 64 -> 64): the
     // F(2,3) unit kernel (k_wino23u) takes about half the time of k_wino_fused<4>,
     // so the F(4,3) route runs it whenever its staging conditions hold.
@@ -1556,7 +1591,7 @@ bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin,
     // 7 x 7 stage, run units of two images' tile blocks.)
     ConvShape g{N, H, W, Cin, 3, 3, 1, 1, H, W};
     if (!unit23 && conv32_ok(g, Cout, in, w)) return conv32_f32(g, in, w, bias, Cout, out, act, s);
-    return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    return winograd_f32(tile, in, N, H, W, Cin, w, bias, Cout, out, act, s, tile == 2 ? Upre : nullptr);
 }
 
 }  // namespace acfun

@@ -49,6 +49,10 @@ struct Layer {
     int8_t* wq = nullptr;
     float* ws = nullptr;
     I8Weights i8;        // wq prepared for the int8 GEMM once, at load
+    // fp32 3x3/s1/p1 convs: the F(2,3) filter transform, made at the first
+    // inference that routes the layer to Winograd (for plan U_plan) and reused
+    float* U = nullptr;
+    int U_plan = -1;
 };
 
 struct Raw {
@@ -140,6 +144,7 @@ void free_layers(AcfunModel* m) {
         if (L.b) hipFree(L.b);
         if (L.wq) hipFree(L.wq);
         if (L.ws) hipFree(L.ws);
+        if (L.U) hipFree(L.U);
         i8_release(L.i8);
     }
     m->layers.clear();
@@ -478,8 +483,27 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                     set_error("model: residual fusion precondition failed at layer %d", i);
                     return 0;
                 } else {
+                    // A Winograd-routed layer keeps its filter transform (the
+                    // reference rebuilds it per call, src/winograd_avx512.cpp:195-206;
+                    // the weights of a loaded model do not change).
+                    const float* U = nullptr;
+                    if (groups <= 1 && F.p[0] == 3 && F.p[1] == 3 && F.p[3] == 1 && F.p[4] == 1 &&
+                        in.H >= 3 && in.W >= 3 && in.C >= 4 && o.C >= 4) {
+                        const int plan = wino23_plan(N, in.H, in.W, in.C, o.C, x);
+                        if (plan >= 0 && F.U_plan != plan) {
+                            if (F.U) { (void)hipStreamSynchronize(s); hipFree(F.U); F.U = nullptr; }
+                            F.U_plan = -1;
+                            if (check(hipMalloc((void**)&F.U, wino23_filter_bytes(in.C, o.C)),
+                                      "hipMalloc(Winograd filter)") &&
+                                wino23_filter(F.w, in.C, o.C, plan, F.U, s))
+                                F.U_plan = plan;
+                            else
+                                return 0;
+                        }
+                        if (plan >= 0) U = F.U;
+                    }
                     ok = conv2d_route_f32(x, N, in.H, in.W, in.C, F.w, F.b, F.p[0], F.p[1], o.C,
-                                          F.p[3], F.p[4], groups > 1 ? groups : 1, y, act, s);
+                                          F.p[3], F.p[4], groups > 1 ? groups : 1, y, act, s, U);
                 }
                 break;
             }

@@ -173,18 +173,36 @@ bool round_bf16(const float* in, float* out, size_t n, hipStream_t s);
 bool gemm_bf16_dev(int M, int N, int K, const float* A, const float* B, float* C, hipStream_t s);
 
 // Winograd 3x3/s1/p1 (tile = 2 for F(2,3), 4 for F(4,3)).
+// Upre (F(2,3) only, nullable): the filter transform prepared by wino23_filter
+// for this shape's wino23_plan, instead of transforming it in the call.
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
-                  const float* bias, int Cout, float* out, int act, hipStream_t s);
+                  const float* bias, int Cout, float* out, int act, hipStream_t s,
+                  const float* Upre = nullptr);
+// The F(2,3) filter transform, prepared once for repeated calls (a model):
+// wino23_plan says which engine and filter layout a shape takes (1 or 0; -1:
+// no Winograd engine), wino23_filter writes the transform (wino23_filter_bytes).
+int wino23_plan(int N, int H, int W, int Cin, int Cout, const void* in);
+size_t wino23_filter_bytes(int Cin, int Cout);
+bool wino23_filter(const float* w, int Cin, int Cout, int plan, float* U, hipStream_t s);
 // The conv2d route's Winograd step: the route names the tile the reference
 // would use; both tiles compute the direct convolution exactly over the
 // rationals, so the faster kernel for the shape runs (within the Winograd
 // tolerance of the reference either way).
 bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
-                        const float* bias, int Cout, float* out, int act, hipStream_t s);
+                        const float* bias, int Cout, float* out, int act, hipStream_t s,
+                        const float* Upre = nullptr);
 
 // Bandwidth kernels.
 bool dwconv_f32(const float* in, int N, int H, int W, int C, const float* w, const float* bias,
                 int KH, int KW, int stride, int pad, float* out, int act, hipStream_t s);
+// Depthwise 3x3 + activation fused with a following 3x3/2 MaxPool (pool pad 0
+// or 1, post_relu): the result of dwconv_f32 then maxpool_f32, bit for bit,
+// without the depthwise output in HBM (dwconv_pool_ok says when it applies).
+bool dwconv_pool_ok(int H, int W, int C, int KH, int KW, int stride, int pad, int pool,
+                    int pstride, int ppad, const void* in, const void* w, const void* out);
+bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w,
+                     const float* bias, int stride, int pad, int act, int ppad, float* out,
+                     int post_relu, hipStream_t s);
 bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
                int KH, int KW, int Cout, int stride, int pad, int groups, float* out, int act,
                hipStream_t s);
@@ -263,9 +281,12 @@ bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8
 
 // fp32 convolution routing exactly as the reference's conv2d_impl
 // (src/layers.cpp:106-195).
+// wino_U (nullable): a prepared F(2,3) filter transform, used when the route
+// is Winograd and the shape's plan matches the one it was prepared for.
 bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float* w,
                       const float* bias, int KH, int KW, int Cout, int stride, int pad,
-                      int groups, float* out, int act, hipStream_t s);
+                      int groups, float* out, int act, hipStream_t s,
+                      const float* wino_U = nullptr);
 
 // Tile-config table (autotune).
 struct TileCfg { int bm, bn, split; };

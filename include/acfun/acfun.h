@@ -219,6 +219,16 @@ int acfun_dev_conv2d_int8_noalloc(const float* input, int N, int H, int W, int C
                                   const int8_t* wq, const float* wscale, const float* bias,
                                   int KH, int KW, int Cout, int stride, int pad, float* output,
                                   int act, void* stream);
+/* acfun_conv2d_dw (ref acfun.h:77-80, act 0/1) followed by acfun_maxpool or
+ * acfun_maxpool_relu (ref acfun.h:105-111, post_relu) on its output: the same
+ * result bit for bit, computed in one pass (3x3 depthwise with stride 1 or 2,
+ * 3x3 / stride-2 pool with padding 0 or 1, C % 4 == 0, 16-byte aligned
+ * buffers) without the depthwise output ever written; other shapes run the
+ * two kernels.  output: [N, PH, PW, C]. */
+int acfun_dev_conv2d_dw_maxpool(const float* input, int N, int H, int W, int C,
+                                const float* weight, const float* bias, int KH, int KW, int stride,
+                                int pad, int act, int pool, int pool_stride, int pool_pad,
+                                float* output, int post_relu, void* stream);
 int acfun_dev_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride,
                       int pad, float* output, int post_relu, void* stream);
 int acfun_dev_fc(const float* input, int N, int Cin, const float* weight, const float* bias,
