@@ -262,9 +262,17 @@ __global__ __launch_bounds__(320) void k_dwconv3_pool(const float4* __restrict__
                                                       const float* __restrict__ bias, int pad,
                                                       int OH, int OW, int act, int PP, int PH,
                                                       int PW, int nPHB, int nPWB, int nQG,
-                                                      float4* __restrict__ out, int post_relu) {
+                                                      int nblk, float4* __restrict__ out,
+                                                      int post_relu) {
     __shared__ float4 ys[DWP_ROWS][DWP_COLS][DWP_Q];
-    int b = blockIdx.x;
+    // XCD-ordered work: workgroup i of XCD x (blockIdx.x = 8 i + x) takes item
+    // x * per + i, so each XCD runs a contiguous range of items, and the
+    // blocks of neighbouring pool rows (which stage the same halo input rows)
+    // run on one XCD at about the same time: the second read of a halo row
+    // hits that XCD's L2 instead of going to memory again.
+    const int per = (int)(gridDim.x >> 3);
+    int b = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
+    if (b >= nblk) return;                               // uniform per workgroup
     const int qg = b % nQG;
     b /= nQG;
     const int pwb = b % nPWB;
@@ -712,19 +720,20 @@ bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w
     const int C4 = C / 4;
     const int nPHB = (PH + 1) / 2, nPWB = (PW + DWP_PWB - 1) / DWP_PWB,
               nQG = (C4 + DWP_Q - 1) / DWP_Q;
-    const long long blocks = (long long)N * nPHB * nPWB * nQG;
-    if (blocks >= (1ll << 31)) {
+    const long long items = (long long)N * nPHB * nPWB * nQG;
+    if (items >= (1ll << 30)) {
         set_error("dwconv_pool: grid too large");
         return false;
     }
+    const unsigned blocks = (unsigned)(8 * ((items + 7) / 8));   // 8 equal XCD ranges
     if (stride == 1)
-        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<1>, dim3((unsigned)blocks), dim3(320), 0, s,
+        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<1>, dim3(blocks), dim3(320), 0, s,
                      (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
-                     nPWB, nQG, (float4*)out, post_relu);
+                     nPWB, nQG, (int)items, (float4*)out, post_relu);
     else
-        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<2>, dim3((unsigned)blocks), dim3(320), 0, s,
+        ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<2>, dim3(blocks), dim3(320), 0, s,
                      (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
-                     nPWB, nQG, (float4*)out, post_relu);
+                     nPWB, nQG, (int)items, (float4*)out, post_relu);
     return check_launch("k_dwconv3_pool");
 }
 
