@@ -4,21 +4,23 @@ Headline (the JSON line's metric/value): BASELINE config 2(a) -- fp32 NHWC 3x3
 conv, stride 1, pad 1, bias + fused ReLU, N=32, 56x56, 64 -> 64 channels,
 which the reference routes to Winograd F(2,3).  One step = one
 acfun_dev_conv2d call over the whole batch, inputs resident in HBM.  value is
-TFLOPS counted as direct convolution (2*N*OH*OW*Cout*9*Cin = 7.40 GFLOP), the
-way the reference quotes conv throughput; roofline.achieved counts the FLOPs
-the MFMA units actually execute for F(2,3) (2*tiles*16*Cin*Cout) over the
-dominant kernel's time.
+the FLOP rate the MFMA units execute: F(2,3)'s 2 * tiles * 16 * Cin * Cout =
+3.288 GFLOP per step over the step time; the direct-convolution-equivalent rate
+(7.40 GFLOP per step, the way the reference quotes conv throughput) is in
+config.  roofline divides the same executed FLOPs by the dominant kernel's own
+mean duration.
 
-The other BASELINE configs are measured the same way and reported under
-"configs" (GEMM 1024^3, F(4,3), the two int8 convs, depthwise+pool, grouped,
-ResNet-50-style batch 64 fp32 and int8).  Configs 3 and 4 also report
-"ms_cold": the same step cycling over copies of its input and output whose
-total exceeds the 256 MB MALL, so the operands come from HBM ("ms" reuses one
-set, which may stay cached).
+Every other BASELINE config is measured the same way under "configs": its step
+time, the dominant kernel's time, a roofline block on the algorithmic work of
+SURVEY.md section 8(d) (FLOPs, ops or bytes, as the config is MFMA- or
+HBM-bound), and a cpu_baseline: the reference library itself (oracle/_ref,
+built from the reference's sources) timed on this host's cores on a bounded
+sample of the same workload, 3 warmups then the median (src/benchmark.cpp:98-111).
+Configs 3 and 4 also report "ms_cold": the step cycling over copies of its
+operands whose total exceeds the 256 MB MALL.
 
-cpu_baseline: the reference library itself (oracle/_ref, built from the
-reference's sources) timed on this host's cores on the headline config:
-3 warmups, then the median of the timed repetitions (src/benchmark.cpp:98-111).
+--profile CFG runs only CFG's step (5 times) and then three plain 256 MiB
+device copies, for rocprofv3 --pmc passes whose counters the copies scale.
 """
 import argparse
 import ctypes as C
@@ -33,19 +35,23 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP32 = 157.3e12     # dense fp32 MFMA, FLOP/s
 PEAK_INT8 = 5.0e15       # dense int8 MFMA, OP/s
+PEAK_BF16 = 2.5e15       # dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12        # B/s
+CPU_BUDGET_S = 5.0       # timed CPU work per configuration (after the warmups)
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
-    ap.add_argument("--traffic", action="store_true",
-                    help="for rocprofv3 --pmc runs: 5 headline steps, then 3 plain copies of "
-                         "256 MiB (the counter scale reference); prints no JSON line")
+    ap.add_argument("--profile", metavar="CFG", default=None,
+                    help="for rocprofv3 --pmc runs: 5 steps of CFG (cfg1, cfg2a, cfg2b, cfg3a, "
+                         "cfg3b, cfg3a_q, cfg3b_q, cfg4a, cfg4b), then 3 plain copies of 256 MiB "
+                         "(the counter scale reference); prints no JSON line")
+    ap.add_argument("--traffic", action="store_true", help="the same as --profile cfg2a")
     return ap.parse_args()
 
 
@@ -69,20 +75,336 @@ class Timer:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps   # ms per step
 
-    def kernel_ms(self, lib, fn, steps, kernel):
-        """Mean duration (ms) of one library kernel over `steps` more steps: the
-        library brackets each launch of it with a HIP event pair on its stream."""
+    def kernel_ms(self, lib, fn, steps, kernels):
+        """Mean duration (ms) of library kernels over `steps` more steps: the
+        library brackets each launch with a HIP event pair on its stream."""
         self.torch.cuda.synchronize()
         lib.acfun_prof_enable(1)
         for _ in range(steps):
             fn()
         self.torch.cuda.synchronize()
         lib.acfun_prof_enable(0)
-        n = C.c_int(0)
-        ms = lib.acfun_prof_kernel_ms(kernel.encode(), C.byref(n))
-        return ms if n.value > 0 and ms > 0 else None
+        out = {}
+        for k in kernels:
+            n = C.c_int(0)
+            ms = lib.acfun_prof_kernel_ms(k.encode(), C.byref(n))
+            out[k] = round(ms, 5) if n.value > 0 and ms > 0 else None
+        return out
 
 
+def read_traffic(name):
+    """HBM bytes per launch from a committed counter summary
+    (profiles/traffic_<name>.txt: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+    scaled by a plain copy of known size), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for ln in f:
+            parts = ln.split()
+            if len(parts) == 2 and not ln.startswith("#"):
+                try:
+                    vals[parts[0]] = float(parts[1])
+                except ValueError:
+                    pass
+    return vals.get("hbm_bytes_per_launch")
+
+
+def roofline(bound, work, ms, kernel, work_note, traffic_name=None):
+    """A roofline block: `work` is FLOP/op (bound mfma-fp32 / mfma-int8) or
+    bytes (bound hbm) per launch of `kernel`, `ms` its mean duration."""
+    if bound == "hbm":
+        peak, unit, scale = PEAK_HBM, "GB/s", 1e9
+    elif bound == "mfma-int8":
+        peak, unit, scale = PEAK_INT8, "TOP/s", 1e12
+    else:
+        peak, unit, scale = PEAK_FP32, "TFLOP/s", 1e12
+    ach = work / (ms * 1e-3) if ms else None
+    return {"bound": "hbm" if bound == "hbm" else "mfma",
+            "achieved": round(ach / scale, 3) if ach else None,
+            "peak": peak / scale, "unit": unit,
+            "frac": round(ach / peak, 4) if ach else None,
+            "traffic": read_traffic(traffic_name) if traffic_name else None,
+            "kernel": kernel, "kernel_ms": round(ms, 5) if ms else None, "work": work_note}
+
+
+# ------------------------------------------------------------------ the configs
+# Each builder returns (step, extras): step() runs one step on the library's
+# stream; extras carries what the report needs.
+
+def make_configs(lib, torch, dev, sp, rng, check):
+    import numpy as np
+
+    from acfun_amd import acfun0
+
+    def cuda(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    cfg = {}
+
+    # 2(a), the headline: F(2,3), N=32, 56x56, 64 -> 64
+    N, H, Cin, Cout = 32, 56, 64, 64
+    x2 = rng.uniform(0, 1, (N, H, H, Cin)).astype(np.float32)
+    w2 = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32)
+    b2 = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
+    tx2, tw2, tb2 = cuda(x2), cuda(w2), cuda(b2)
+    ty2 = torch.empty((N, H, H, Cout), device=dev)
+    cfg["cfg2a"] = dict(
+        step=lambda: check(lib.acfun_dev_conv2d(tx2.data_ptr(), N, H, H, Cin, tw2.data_ptr(),
+                                                tb2.data_ptr(), 3, 3, Cout, 1, 1, 1,
+                                                ty2.data_ptr(), 1, sp)),
+        host=(x2, w2, b2))
+
+    # 1: GEMM 1024^3
+    M = 1024
+    A1 = rng.uniform(-1, 1, (M, M)).astype(np.float32)
+    B1 = rng.uniform(-1, 1, (M, M)).astype(np.float32)
+    tA, tB = cuda(A1), cuda(B1)
+    tC = torch.empty((M, M), device=dev)
+    cfg["cfg1"] = dict(step=lambda: check(lib.acfun_dev_gemm_epi(M, M, M, tA.data_ptr(),
+                                                                  tB.data_ptr(), tC.data_ptr(),
+                                                                  None, 0, sp)),
+                       host=(A1, B1))
+    cfg["bf16"] = dict(step=lambda: check(lib.acfun_dev_gemm_bf16(M, M, M, tA.data_ptr(),
+                                                                   tB.data_ptr(), tC.data_ptr(),
+                                                                   sp)))
+
+    # 2(b): N=8, 112x112, 64 -> 64 (the reference's F(4,3) route)
+    x2b = rng.uniform(0, 1, (8, 112, 112, 64)).astype(np.float32)
+    tx2b = cuda(x2b)
+    ty2b = torch.empty((8, 112, 112, 64), device=dev)
+    cfg["cfg2b"] = dict(
+        step=lambda: check(lib.acfun_dev_conv2d(tx2b.data_ptr(), 8, 112, 112, 64, tw2.data_ptr(),
+                                                tb2.data_ptr(), 3, 3, 64, 1, 1, 1,
+                                                ty2b.data_ptr(), 1, sp)),
+        host=(x2b, w2, b2))
+
+    # 3(a) / 3(b): int8 convs, float I/O (acfun_conv2d_int8) and int8 I/O (acfun_dev_conv2d_int8_q)
+    for name, (KK, ci, co, pd) in {"cfg3a": (1, 256, 512, 0), "cfg3b": (3, 128, 128, 1)}.items():
+        q = rng.integers(-127, 128, (32, 28, 28, ci)).astype(np.int8)
+        q.reshape(-1)[0] = 127
+        while True:
+            sa = np.float32(rng.uniform(0.005, 0.05))
+            if np.float32(np.float32(127.0) * sa) / np.float32(127.0) == sa:
+                break
+        xf = (q.astype(np.float32) * sa).astype(np.float32)
+        wq = rng.integers(-127, 128, (KK * KK * ci, co)).astype(np.int8)
+        ws = rng.uniform(0.005, 0.05, co).astype(np.float32)
+        bi = (rng.standard_normal(co) * 0.01).astype(np.float32)
+        t = dict(x=cuda(xf), q=cuda(q), wq=cuda(wq), ws=cuda(ws), b=cuda(bi),
+                 y=torch.empty((32, 28, 28, co), device=dev),
+                 yq=torch.empty((32, 28, 28, co), dtype=torch.int8, device=dev),
+                 si=torch.tensor([float(sa)], device=dev), so=torch.zeros(1, device=dev))
+
+        def conv_f(xt, yt, t=t, KK=KK, ci=ci, co=co, pd=pd):
+            check(lib.acfun_dev_conv2d_int8(xt.data_ptr(), 32, 28, 28, ci, t["wq"].data_ptr(),
+                                            t["ws"].data_ptr(), t["b"].data_ptr(), KK, KK, co, 1,
+                                            pd, yt.data_ptr(), 1, sp))
+
+        def conv_q(qt, yt, t=t, KK=KK, ci=ci, co=co, pd=pd):
+            check(lib.acfun_dev_conv2d_int8_q(qt.data_ptr(), t["si"].data_ptr(), 32, 28, 28, ci,
+                                              t["wq"].data_ptr(), t["ws"].data_ptr(),
+                                              t["b"].data_ptr(), KK, KK, co, 1, pd, yt.data_ptr(),
+                                              t["so"].data_ptr(), 1, 0, sp))
+        cfg[name] = dict(step=lambda f=conv_f, t=t: f(t["x"], t["y"]), rot=(conv_f, t["x"], t["y"]),
+                         host=(xf, wq, ws, bi, KK, ci, co, pd),
+                         ops=2.0 * 32 * 28 * 28 * co * KK * KK * ci,
+                         fbytes=4.0 * 32 * 28 * 28 * (ci + co), qbytes=1.0 * 32 * 28 * 28 * (ci + co))
+        cfg[name + "_q"] = dict(step=lambda f=conv_q, t=t: f(t["q"], t["yq"]),
+                                rot=(conv_q, t["q"], t["yq"]))
+
+    # 4(a): depthwise 3x3/2 (BN folded) + ReLU, then 3x3/2 MaxPool, fused
+    C4 = 96
+    x4 = rng.uniform(0, 1, (32, 112, 112, C4)).astype(np.float32)
+    w4 = (rng.standard_normal((C4, 3, 3)) * 0.3).astype(np.float32)
+    b4 = (rng.standard_normal(C4) * 0.1).astype(np.float32)
+    tx4, tw4, tb4 = cuda(x4), cuda(w4), cuda(b4)
+    tz4 = torch.empty((32, 28, 28, C4), device=dev)
+
+    def dwpool(xt, zt):
+        check(lib.acfun_dev_conv2d_dw_maxpool(xt.data_ptr(), 32, 112, 112, C4, tw4.data_ptr(),
+                                              tb4.data_ptr(), 3, 3, 2, 1, 1, 3, 2, 1,
+                                              zt.data_ptr(), 0, sp))
+    cfg["cfg4a"] = dict(step=lambda: dwpool(tx4, tz4), rot=(dwpool, tx4, tz4),
+                        host=(x4, w4, b4), bytes=4.0 * (32 * 112 * 112 * C4 + 32 * 28 * 28 * C4))
+
+    # 4(b): grouped 3x3 g6, 24 -> 48, N=32, 14x14, then 3x3/2 MaxPool
+    x5 = rng.uniform(0, 1, (32, 14, 14, 24)).astype(np.float32)
+    w5 = (rng.standard_normal((6, 36, 8)) * 0.3).astype(np.float32)
+    b5 = (rng.standard_normal(48) * 0.1).astype(np.float32)
+    tx5, tw5, tb5 = cuda(x5), cuda(w5), cuda(b5)
+    ty5 = torch.empty((32, 14, 14, 48), device=dev)
+    tz5 = torch.empty((32, 7, 7, 48), device=dev)
+
+    def gpool(xt, zt):
+        check(lib.acfun_dev_conv2d(xt.data_ptr(), 32, 14, 14, 24, tw5.data_ptr(), tb5.data_ptr(),
+                                   3, 3, 48, 1, 1, 6, ty5.data_ptr(), 1, sp))
+        check(lib.acfun_dev_maxpool(ty5.data_ptr(), 32, 14, 14, 48, 3, 2, 1, zt.data_ptr(), 0, sp))
+    cfg["cfg4b"] = dict(step=lambda: gpool(tx5, tz5), rot=(gpool, tx5, tz5), host=(x5, w5, b5),
+                        bytes=4.0 * (32 * 14 * 14 * 24 + 2 * 32 * 14 * 14 * 48 + 32 * 7 * 7 * 48))
+
+    # 5: ResNet-50-style, batch 64
+    inC, inH, inW, recs = acfun0.resnet50(np.random.default_rng(5))
+    cfg["cfg5"] = dict(recs=(inC, inH, inW, recs))
+    return cfg
+
+
+def rotation_sets(x, y, extra=0, total=320 << 20):
+    """Copies of an input and an output tensor, enough sets that one pass over
+    them (plus `extra` bytes of fixed intermediates) exceeds the 256 MB MALL:
+    a step on set i % n then finds its operands in HBM, not in the cache."""
+    per = x.numel() * x.element_size() + y.numel() * y.element_size()
+    n = max(2, -(-(total - extra) // per))
+    return [x.clone() for _ in range(n)], [y.new_empty(y.shape) for _ in range(n)]
+
+
+def rotating(fn, xs, ys):
+    state = [0]
+
+    def step():
+        i = state[0] % len(xs)
+        state[0] += 1
+        fn(xs[i], ys[i])
+    return step
+
+
+# ------------------------------------------------------------------ CPU baselines
+def host_cpu():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_median(fn, budget=CPU_BUDGET_S, warmups=3, min_reps=5):
+    """The reference's method (src/benchmark.cpp:98-111): warmups, then the
+    median of the timed repetitions (at least min_reps, up to the budget)."""
+    import numpy as np
+    for _ in range(warmups):
+        fn()
+    times = []
+    t_end = time.time() + budget
+    while len(times) < min_reps or (time.time() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baselines(cfg, configs, line):
+    """The compiled reference on this host, per configuration."""
+    import numpy as np
+
+    import oracle
+    import oracle.model as omodel
+    from acfun_amd.capi import bind
+    ref = oracle.ref()
+    if ref is None:
+        na = {"value": None, "unit": None, "cores": 0, "kind": "reference",
+              "sample": "oracle/_ref/libacfun_ref.so not present"}
+        line["cpu_baseline"] = dict(na, unit="TFLOPS")
+        return
+    bind(ref)
+    cores = int(ref.acfun_effective_cores())
+    ref.acfun_set_threads(cores)
+    host = f"{host_cpu()}, {cores} threads (cgroup-capped, as the reference's own acfun_effective_cores)"
+    P = lambda a: C.c_void_p(a.ctypes.data)
+
+    def base(value, unit, sample):
+        return {"value": round(value, 4), "unit": unit, "cores": cores, "kind": "reference",
+                "sample": sample, "host": host}
+
+    # 2(a) headline
+    x, w, b = cfg["cfg2a"]["host"]
+    y = np.empty((32, 56, 56, 64), np.float32)
+    t, n = cpu_median(lambda: ref.acfun_conv2d_relu(P(x), 32, 56, 56, 64, P(w), P(b), 3, 3, 64, 1,
+                                                    1, P(y)))
+    line["cpu_baseline"] = base(3.288334336e9 / t / 1e12, "TFLOPS",
+                                f"full headline batch (N=32) through the reference's "
+                                f"acfun_conv2d_relu (Winograd F(2,3), AVX-512/OpenMP), median of {n} "
+                                f"runs after 3 warmups: {t * 1e3:.2f} ms/step; value counts the "
+                                f"executed F(2,3) FLOPs as the GPU value does "
+                                f"({7.398752256e9 / t / 1e12:.3f} TFLOPS direct-equivalent)")
+    if "cfg1_gemm_1024" in configs:
+        A, B = cfg["cfg1"]["host"]
+        Cm = np.empty((1024, 1024), np.float32)
+        t, n = cpu_median(lambda: ref.acfun_gemm(1024, 1024, 1024, P(A), P(B), P(Cm)))
+        configs["cfg1_gemm_1024"]["cpu_baseline"] = base(
+            2.0 * 1024 ** 3 / t / 1e12, "TFLOPS",
+            f"full size through acfun_gemm, median of {n}: {t * 1e3:.2f} ms")
+    if "cfg2b_conv3x3_f43" in configs:
+        x, w, b = cfg["cfg2b"]["host"]
+        y = np.empty(x.shape, np.float32)
+        t, n = cpu_median(lambda: ref.acfun_conv2d_relu(P(x), 8, 112, 112, 64, P(w), P(b), 3, 3,
+                                                        64, 1, 1, P(y)))
+        configs["cfg2b_conv3x3_f43"]["cpu_baseline"] = base(
+            1.849688064e9 / t / 1e12, "TFLOPS",
+            f"full size through acfun_conv2d_relu (its F(4,3) route), median of {n}: "
+            f"{t * 1e3:.2f} ms; value on the executed F(4,3) FLOPs "
+            f"({7.398752256e9 / t / 1e12:.3f} TFLOPS direct-equivalent)")
+    for name, key in (("cfg3a", "cfg3a_int8_1x1"), ("cfg3b", "cfg3b_int8_3x3")):
+        if key not in configs:
+            continue
+        xf, wq, ws, bi, KK, ci, co, pd = cfg[name]["host"]
+        y = np.empty((32, 28, 28, co), np.float32)
+        t, n = cpu_median(lambda: ref.acfun_conv2d_int8(P(xf), 32, 28, 28, ci, P(wq), P(ws), P(bi),
+                                                        KK, KK, co, 1, pd, C.c_float(0.0), P(y), 1))
+        configs[key]["cpu_baseline"] = base(
+            cfg[name]["ops"] / t / 1e12, "TOPS",
+            f"full size through acfun_conv2d_int8 (float I/O, AVX-512 VNNI), median of {n}: "
+            f"{t * 1e3:.2f} ms")
+    if "cfg4a_dw_bn_relu_pool" in configs:
+        x, w, b = cfg["cfg4a"]["host"]
+        y = np.empty((32, 56, 56, 96), np.float32)
+        z = np.empty((32, 28, 28, 96), np.float32)
+
+        def dp():
+            ref.acfun_conv2d_dw(P(x), 32, 112, 112, 96, P(w), P(b), 3, 3, 2, 1, P(y), 1)
+            ref.acfun_maxpool(P(y), 32, 56, 56, 96, 3, 2, 1, P(z))
+        t, n = cpu_median(dp)
+        configs["cfg4a_dw_bn_relu_pool"]["cpu_baseline"] = base(
+            cfg["cfg4a"]["bytes"] / t / 1e9, "GB/s",
+            f"full size through acfun_conv2d_dw + acfun_maxpool, median of {n}: {t * 1e3:.2f} ms; "
+            f"value on the same 163.8 MB as the GPU figure")
+    if "cfg4b_grouped_pool" in configs:
+        x, w, b = cfg["cfg4b"]["host"]
+        y = np.empty((32, 14, 14, 48), np.float32)
+        z = np.empty((32, 7, 7, 48), np.float32)
+
+        def gp():
+            ref.acfun_conv2d_g(P(x), 32, 14, 14, 24, P(w), P(b), 3, 3, 48, 1, 1, 6, P(y), 1)
+            ref.acfun_maxpool(P(y), 32, 14, 14, 48, 3, 2, 1, P(z))
+        t, n = cpu_median(gp)
+        configs["cfg4b_grouped_pool"]["cpu_baseline"] = base(
+            cfg["cfg4b"]["bytes"] / t / 1e9, "GB/s",
+            f"full size through acfun_conv2d_g + acfun_maxpool, median of {n}: {t * 1e3:.3f} ms")
+    # 5: the version-2 ResNet-50 through the reference's own per-op calls on a
+    # bounded sample of 8 images (its executor cannot load residual records)
+    inC, inH, inW, recs = cfg["cfg5"]["recs"]
+    from acfun_amd import acfun0
+    blob = acfun0.encode(inC, inH, inW, recs, version=2)
+    xs = np.random.default_rng(3).uniform(0, 1, (8, inH, inW, inC)).astype(np.float32)
+    for tag, int8 in (("fp32", False), ("int8", True)):
+        key = f"cfg5_resnet50_b64_{tag}"
+        if key not in configs:
+            continue
+        prep = omodel.prepare_reference(ref, blob, int8)
+        t, n = cpu_median(lambda: omodel.run_reference(ref, prep, xs), budget=CPU_BUDGET_S,
+                          warmups=1, min_reps=3)
+        configs[key]["cpu_baseline"] = base(
+            8 / t, "images/s",
+            f"8 images (a sample of the batch of 64) through the reference's per-op calls "
+            f"(acfun_conv2d(_relu)/acfun_conv2d_int8, acfun_maxpool, acfun_fc, acfun_softmax; "
+            f"numpy for the Add and global-pool records), median of {n}: {t * 1e3:.1f} ms"
+            + ("; int8 convs are acfun_conv2d_int8 on the batch" if int8 else ""))
+
+
+# ------------------------------------------------------------------ main
 def main():
     args = parse()
     if args.gpus != 1:
@@ -106,28 +428,19 @@ def main():
     T = Timer(torch, stream)
     rng = np.random.default_rng(12345 + 1)
 
-    def cuda(a):
-        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
     def check(rc):
         if rc != 0:
             raise RuntimeError(capi.last_error())
 
-    # ---------------------------------------------------------------- headline: config 2(a)
-    N, H, Cin, Cout = 32, 56, 64, 64
-    x = rng.uniform(0, 1, (N, H, H, Cin)).astype(np.float32)
-    w = (rng.standard_normal((9 * Cin, Cout)) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32)
-    b = (rng.standard_normal(Cout) * 0.01).astype(np.float32)
-    tx, tw, tb = cuda(x), cuda(w), cuda(b)
-    ty = torch.empty((N, H, H, Cout), device=dev)
-
-    def step():
-        check(lib.acfun_dev_conv2d(tx.data_ptr(), N, H, H, Cin, tw.data_ptr(), tb.data_ptr(),
-                                   3, 3, Cout, 1, 1, 1, ty.data_ptr(), 1, sp))
+    cfg = make_configs(lib, torch, dev, sp, rng, check)
 
     if args.traffic:
+        args.profile = "cfg2a"
+    if args.profile:
+        if args.profile not in cfg or "step" not in cfg[args.profile]:
+            raise SystemExit(f"bench.py: no configuration {args.profile!r}")
         for _ in range(5):
-            step()
+            cfg[args.profile]["step"]()
         src = torch.empty(64 << 20, device=dev)        # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -135,18 +448,14 @@ def main():
         torch.cuda.synchronize()
         return
 
-    ms = T.run(step, args.steps, args.warmup)
-    kms = T.kernel_ms(lib, step, args.steps, "k_wino23")
-    direct_flop = 2.0 * N * H * H * Cout * 9 * Cin
-    tiles = N * ((H + 1) // 2) ** 2
-    exec_flop = 2.0 * tiles * 16 * Cin * Cout
-    value = direct_flop / (ms * 1e-3) / 1e12
-    achieved = exec_flop / (kms * 1e-3) if kms else None
-    traffic = read_traffic(os.path.join(ROOT, "profiles", "traffic_k_wino23_cfg2a.txt"))
-
+    # ---------------------------------------------------------------- headline
+    ms = T.run(cfg["cfg2a"]["step"], args.steps, args.warmup)
+    k = T.kernel_ms(lib, cfg["cfg2a"]["step"], args.steps, ["k_wino23", "k_wino_filter_t"])
+    direct_flop = 7.398752256e9
+    exec_flop = 3.288334336e9
     line = {
         "metric": "fp32 TFLOPS & int8 TOPS (% MI355X peak); ResNet-50-style b64 images/s",
-        "value": round(value, 3),
+        "value": round(exec_flop / (ms * 1e-3) / 1e12, 3),
         "unit": "TFLOPS",
         "n_gpus": 1,
         "steps": args.steps,
@@ -159,28 +468,24 @@ def main():
         "data": "synthetic (seeded; BASELINE config-2 distributions)",
         "config": {"workload": "cfg2a fp32 NHWC conv3x3 s1 p1 +bias+ReLU, N=32, 56x56, 64->64 "
                                "(reference route: Winograd F(2,3))",
-                   "flop_count": "direct-conv equivalent 7.40 GFLOP per step",
+                   "flop_count": "executed F(2,3) MFMA FLOPs, 3.288 GFLOP per step",
+                   "TFLOPS_direct_equivalent": round(direct_flop / (ms * 1e-3) / 1e12, 3),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma",
-                     "achieved": round(achieved / 1e12, 3) if achieved else None,
-                     "peak": PEAK_FP32 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32, 4) if achieved else None,
-                     "traffic": traffic,
-                     "kernel": "k_wino23p<16,1,1>", "kernel_ms": round(kms, 5) if kms else None,
-                     "work": "executed F(2,3) MFMA FLOPs 3.288 GFLOP per launch (2 * 25088 "
-                             "tiles * 16 points * 64 * 64)"},
+        "roofline": roofline("mfma-fp32", exec_flop, k["k_wino23"], "k_wino23p<16,1,1>",
+                             "executed F(2,3) MFMA FLOPs 3.288 GFLOP per launch (2 * 25088 tiles "
+                             "* 16 points * 64 * 64)", "k_wino23_cfg2a"),
     }
+    line["roofline"]["other_kernels_ms"] = {"k_wino_filter_t": k["k_wino_filter_t"]}
 
-    # ---------------------------------------------------------------- other configs
     configs = {}
     if not args.headline_only:
-        steps = max(5, args.steps // 2)
+        steps = args.steps
 
-        # 2a through the reference-compatible host-pointer API (acfun_conv2d_relu on
-        # host buffers: H2D staging, kernels, D2H, synchronize) -- PCIe-inclusive rate
-        yh = np.empty((N, H, H, Cout), np.float32)
+        # 2(a) through the reference-compatible host-pointer API -- PCIe-inclusive rate
+        x, w, b = cfg["cfg2a"]["host"]
+        yh = np.empty((32, 56, 56, 64), np.float32)
         Ph = lambda a: C.c_void_p(a.ctypes.data)
-        hcall = lambda: lib.acfun_conv2d_relu(Ph(x), N, H, H, Cin, Ph(w), Ph(b), 3, 3, Cout, 1, 1,
+        hcall = lambda: lib.acfun_conv2d_relu(Ph(x), 32, 56, 56, 64, Ph(w), Ph(b), 3, 3, 64, 1, 1,
                                               Ph(yh))
         for _ in range(3):
             hcall()
@@ -191,139 +496,116 @@ def main():
             th.append(time.perf_counter() - t0)
         th = float(np.median(th)) * 1e3
         configs["cfg2a_host_buffers"] = {"ms": round(th, 4),
-                                         "TFLOPS_direct": round(direct_flop / (th * 1e-3) / 1e12, 3),
-                                         "note": "acfun_conv2d_relu on host memory, PCIe-inclusive, "
-                                                 "median wall time"}
+                                         "note": "acfun_conv2d_relu on host memory: H2D, kernels, "
+                                                 "D2H, synchronize (PCIe-inclusive), median wall "
+                                                 "time; never the headline value"}
 
         # 1: GEMM 1024^3
-        M = 1024
-        A = cuda(rng.uniform(-1, 1, (M, M)).astype(np.float32))
-        Bm = cuda(rng.uniform(-1, 1, (M, M)).astype(np.float32))
-        Cm = torch.empty((M, M), device=dev)
-        s1 = lambda: check(lib.acfun_dev_gemm_epi(M, M, M, A.data_ptr(), Bm.data_ptr(),
-                                                  Cm.data_ptr(), None, 0, sp))
-        t = T.run(s1, steps, 5)
-        k = T.kernel_ms(lib, s1, steps, "k_gemm_f32")
-        f = 2.0 * M ** 3 / (t * 1e-3)
-        configs["cfg1_gemm_1024"] = {"ms": round(t, 5), "TFLOPS": round(f / 1e12, 3),
-                                     "frac_fp32_peak": round(f / PEAK_FP32, 4),
-                                     "kernel_ms": {"k_gemm_f32": k}}
+        t = T.run(cfg["cfg1"]["step"], steps, args.warmup)
+        k = T.kernel_ms(lib, cfg["cfg1"]["step"], steps, ["k_gemm_f32"])
+        flop = 2.0 * 1024 ** 3
+        configs["cfg1_gemm_1024"] = {
+            "ms": round(t, 5), "TFLOPS": round(flop / (t * 1e-3) / 1e12, 3),
+            "roofline": roofline("mfma-fp32", flop, k["k_gemm_f32"], "k_gemm32",
+                                 "2*1024^3 = 2.147 GFLOP per launch", "k_gemm32_cfg1")}
 
-        # acfun_gemm_bf16 at 1024^3 on device pointers (bf16 MFMA; not a BASELINE config)
-        sb = lambda: check(lib.acfun_dev_gemm_bf16(M, M, M, A.data_ptr(), Bm.data_ptr(),
-                                                   Cm.data_ptr(), sp))
-        t = T.run(sb, steps, 5)
-        k = T.kernel_ms(lib, sb, steps, "k_bf16mm")
-        f = 2.0 * M ** 3 / (t * 1e-3)
-        configs["gemm_bf16_1024"] = {"ms": round(t, 5), "TFLOPS": round(f / 1e12, 3),
-                                     "frac_bf16_peak": round(f / 2.5e15, 4),
-                                     "kernel_ms": {"k_bf16mm": k},
-                                     "note": "step = two bf16 packing passes + k_bf16mm"}
+        # acfun_gemm_bf16 1024^3 (not a BASELINE config)
+        t = T.run(cfg["bf16"]["step"], steps, args.warmup)
+        k = T.kernel_ms(lib, cfg["bf16"]["step"], steps, ["k_bf16mm"])
+        configs["gemm_bf16_1024"] = {"ms": round(t, 5), "TFLOPS": round(flop / (t * 1e-3) / 1e12, 3),
+                                     "frac_bf16_peak_kernel": round(flop / (k["k_bf16mm"] * 1e-3) / PEAK_BF16, 4)
+                                     if k["k_bf16mm"] else None,
+                                     "kernel_ms": k, "note": "step = two bf16 packing passes + k_bf16mm"}
 
-        # 2b: F(4,3), N=8, 112x112
-        x2 = cuda(rng.uniform(0, 1, (8, 112, 112, 64)).astype(np.float32))
-        y2 = torch.empty((8, 112, 112, 64), device=dev)
-        s2 = lambda: check(lib.acfun_dev_conv2d(x2.data_ptr(), 8, 112, 112, 64, tw.data_ptr(),
-                                                tb.data_ptr(), 3, 3, 64, 1, 1, 1,
-                                                y2.data_ptr(), 1, sp))
-        # The reference routes this shape to F(4,3); the route here runs the faster
-        # of this library's two Winograd kernels for it, the F(2,3) unit kernel
-        # (k_wino23p), so executed FLOPs are counted for F(2,3).
-        t = T.run(s2, steps, 5)
-        k = T.kernel_ms(lib, s2, steps, "k_wino23")
-        f = direct_flop / (t * 1e-3)
-        ex_flop = 2.0 * 8 * 56 * 56 * 16 * 64 * 64
-        ex = ex_flop / (t * 1e-3)
-        configs["cfg2b_conv3x3_f43"] = {"ms": round(t, 5), "TFLOPS_direct": round(f / 1e12, 3),
-                                        "kernel": "k_wino23p (persistent F(2,3) unit kernel) on the F(4,3) route",
-                                        "TFLOPS_executed": round(ex / 1e12, 3),
-                                        "frac_fp32_peak_executed": round(ex / PEAK_FP32, 4),
-                                        "kernel_frac_fp32_peak": round(ex_flop / (k * 1e-3) / PEAK_FP32, 4)
-                                        if k else None,
-                                        "kernel_ms": {"k_wino23": k}}
+        # 2(b): F(4,3) route; the fraction counts section 8(d)'s F(4,3) work
+        t = T.run(cfg["cfg2b"]["step"], steps, args.warmup)
+        k = T.kernel_ms(lib, cfg["cfg2b"]["step"], steps, ["k_wino23", "k_wino_fused", "k_wino_filter_t"])
+        f43 = 1.849688064e9
+        kern = "k_wino23" if k["k_wino23"] else "k_wino_fused"
+        configs["cfg2b_conv3x3_f43"] = {
+            "ms": round(t, 5), "TFLOPS_direct_equivalent": round(direct_flop / (t * 1e-3) / 1e12, 3),
+            "TFLOPS_f43_work": round(f43 / (t * 1e-3) / 1e12, 3),
+            "roofline": roofline("mfma-fp32", f43, k[kern], kern,
+                                 "F(4,3) work of section 8(d): 2 * 6272 tiles * 36 points * 64 * "
+                                 "64 = 1.850 GFLOP per launch, whichever kernel runs it",
+                                 "k_wino_cfg2b"),
+            "kernel_ms": k}
 
-        # 3a / 3b: int8 convs with float I/O
-        for name, (KK, ci, co, pd) in {"cfg3a_int8_1x1": (1, 256, 512, 0),
-                                        "cfg3b_int8_3x3": (3, 128, 128, 1)}.items():
-            sa = np.float32(rng.uniform(0.005, 0.05))
-            xi = cuda((rng.integers(-127, 128, (32, 28, 28, ci)).astype(np.float32) * sa))
-            wq = cuda(rng.integers(-127, 128, (KK * KK * ci, co)).astype(np.int8))
-            ws = cuda(rng.uniform(0.005, 0.05, co).astype(np.float32))
-            bi = cuda((rng.standard_normal(co) * 0.01).astype(np.float32))
-            yi = torch.empty((32, 28, 28, co), device=dev)
-            def conv3(xt, yt):
-                check(lib.acfun_dev_conv2d_int8(
-                    xt.data_ptr(), 32, 28, 28, ci, wq.data_ptr(), ws.data_ptr(), bi.data_ptr(), KK, KK,
-                    co, 1, pd, yt.data_ptr(), 1, sp))
-            s3 = lambda: conv3(xi, yi)
-            t = T.run(s3, steps, 5)
-            k = T.kernel_ms(lib, s3, steps, "k_igemm_i8")
-            ops = 2.0 * 32 * 28 * 28 * co * KK * KK * ci
-            byts = 4.0 * 32 * 28 * 28 * (ci + co)
-            xs, ys = rotation_sets(xi, yi)
-            tc = T.run(rotating(conv3, xs, ys), steps, 5)
-            configs[name] = {"ms": round(t, 5), "TOPS": round(ops / (t * 1e-3) / 1e12, 3),
-                             "frac_int8_peak": round(ops / (t * 1e-3) / PEAK_INT8, 4),
-                             "float_io_GBps": round(byts / (t * 1e-3) / 1e9, 1),
-                             "ms_cold": round(tc, 5), "sets_cold": len(xs),
-                             "kernel_ms": {"k_igemm_i8": k}}
+        # 3(a) / 3(b)
+        for name, key in (("cfg3a", "cfg3a_int8_1x1"), ("cfg3b", "cfg3b_int8_3x3")):
+            c = cfg[name]
+            t = T.run(c["step"], steps, args.warmup)
+            k = T.kernel_ms(lib, c["step"], steps, ["k_i8mm"])
+            fn, xt, yt = c["rot"]
+            xs, ys = rotation_sets(xt, yt)
+            tc = T.run(rotating(fn, xs, ys), steps, args.warmup)
             del xs, ys
+            tq = T.run(cfg[name + "_q"]["step"], steps, args.warmup)
+            kq = T.kernel_ms(lib, cfg[name + "_q"]["step"], steps, ["k_i8mm_amax", "k_i8mm_q8"])
+            fn, xt, yt = cfg[name + "_q"]["rot"]
+            xs, ys = rotation_sets(xt, yt)
+            tqc = T.run(rotating(fn, xs, ys), steps, args.warmup)
+            del xs, ys
+            ops = c["ops"]
+            configs[key] = {
+                "float_io": {
+                    "ms": round(t, 5), "ms_cold": round(tc, 5),
+                    "TOPS": round(ops / (t * 1e-3) / 1e12, 3),
+                    "roofline": roofline("hbm", c["fbytes"], t, "step (absmax + quantize + k_i8mm)",
+                                         f"float I/O {c['fbytes'] / 1e6:.1f} MB per step (section "
+                                         "8(d)); the int8 fraction is TOPS/5000"),
+                    "frac_int8_peak": round(ops / (t * 1e-3) / PEAK_INT8, 4),
+                    "kernel_ms": k,
+                    "kernel_frac_int8_peak": round(ops / (k["k_i8mm"] * 1e-3) / PEAK_INT8, 4)
+                    if k["k_i8mm"] else None},
+                "int8_io": {
+                    "ms": round(tq, 5), "ms_cold": round(tqc, 5),
+                    "TOPS": round(ops / (tq * 1e-3) / 1e12, 3),
+                    "roofline": roofline("hbm" if name == "cfg3a" else "mfma-int8",
+                                         c["qbytes"] if name == "cfg3a" else ops, tq,
+                                         "step (k_i8mm max pass + k_i8mm s8 pass)",
+                                         (f"int8 I/O {c['qbytes'] / 1e6:.1f} MB per step" if name == "cfg3a"
+                                          else f"{ops / 1e9:.2f} GOP per step (MFMA-bound with int8 I/O)")
+                                         + " (acfun_dev_conv2d_int8_q)"),
+                    "frac_int8_peak": round(ops / (tq * 1e-3) / PEAK_INT8, 4),
+                    "kernel_ms": kq}}
 
-        # 4a: depthwise 3x3/2 (BN folded) + ReLU, then 3x3/2 maxpool
-        C4 = 96
-        x4 = cuda(rng.uniform(0, 1, (32, 112, 112, C4)).astype(np.float32))
-        w4 = cuda((rng.standard_normal((C4, 9)) * 0.3).astype(np.float32))
-        b4 = cuda((rng.standard_normal(C4) * 0.1).astype(np.float32))
-        y4 = torch.empty((32, 56, 56, C4), device=dev)
-        z4 = torch.empty((32, 28, 28, C4), device=dev)
-
-        def dwpool(xt, zt):
-            check(lib.acfun_dev_conv2d(xt.data_ptr(), 32, 112, 112, C4, w4.data_ptr(), b4.data_ptr(),
-                                       3, 3, C4, 2, 1, C4, y4.data_ptr(), 1, sp))
-            check(lib.acfun_dev_maxpool(y4.data_ptr(), 32, 56, 56, C4, 3, 2, 1, zt.data_ptr(), 0, sp))
-        s4 = lambda: dwpool(x4, z4)
-        t = T.run(s4, steps, 5)
-        kd = T.kernel_ms(lib, s4, steps, "k_dwconv")
-        kp = T.kernel_ms(lib, s4, steps, "k_maxpool")
-        byts = 4.0 * (32 * 112 * 112 * C4 + 2 * 32 * 56 * 56 * C4 + 32 * 28 * 28 * C4)
-        xs, zs = rotation_sets(x4, z4, extra=y4.numel() * 4)
-        tc = T.run(rotating(dwpool, xs, zs), steps, 5)
-        configs["cfg4a_dw_bn_relu_pool"] = {"ms": round(t, 5),
-                                            "GBps": round(byts / (t * 1e-3) / 1e9, 1),
-                                            "frac_hbm": round(byts / (t * 1e-3) / PEAK_HBM, 4),
-                                            "ms_cold": round(tc, 5), "sets_cold": len(xs),
-                                            "frac_hbm_cold": round(byts / (tc * 1e-3) / PEAK_HBM, 4),
-                                            "kernel_ms": {"k_dwconv": kd, "k_maxpool": kp}}
+        # 4(a): fused depthwise + BN + ReLU + MaxPool
+        c = cfg["cfg4a"]
+        t = T.run(c["step"], steps, args.warmup)
+        k = T.kernel_ms(lib, c["step"], steps, ["k_dwconv_pool"])
+        fn, xt, zt = c["rot"]
+        xs, zs = rotation_sets(xt, zt)
+        tc = T.run(rotating(fn, xs, zs), steps, args.warmup)
         del xs, zs
+        configs["cfg4a_dw_bn_relu_pool"] = {
+            "ms": round(t, 5), "ms_cold": round(tc, 5),
+            "roofline": roofline("hbm", c["bytes"], k["k_dwconv_pool"], "k_dwconv3_pool<2>",
+                                 "163.8 MB per launch: the input read and the pooled output written "
+                                 "once (section 8(d), fused)", "k_dwconv_pool_cfg4a"),
+            "frac_hbm_cold_step": round(c["bytes"] / (tc * 1e-3) / PEAK_HBM, 4)}
 
-        # 4b: grouped 3x3 g6, 24 -> 48, N=32, 14x14, then maxpool
-        x5 = cuda(rng.uniform(0, 1, (32, 14, 14, 24)).astype(np.float32))
-        w5 = cuda((rng.standard_normal((6, 36, 8)) * 0.3).astype(np.float32))
-        b5 = cuda((rng.standard_normal(48) * 0.1).astype(np.float32))
-        y5 = torch.empty((32, 14, 14, 48), device=dev)
-        z5 = torch.empty((32, 7, 7, 48), device=dev)
-
-        def gpool(xt, zt):
-            check(lib.acfun_dev_conv2d(xt.data_ptr(), 32, 14, 14, 24, w5.data_ptr(), b5.data_ptr(),
-                                       3, 3, 48, 1, 1, 6, y5.data_ptr(), 1, sp))
-            check(lib.acfun_dev_maxpool(y5.data_ptr(), 32, 14, 14, 48, 3, 2, 1, zt.data_ptr(), 0, sp))
-        s5 = lambda: gpool(x5, z5)
-        t = T.run(s5, steps, 5)
-        kg = T.kernel_ms(lib, s5, steps, "k_gconv")
-        byts = 4.0 * (32 * 14 * 14 * 24 + 2 * 32 * 14 * 14 * 48 + 32 * 7 * 7 * 48)
-        xs, zs = rotation_sets(x5, z5, extra=y5.numel() * 4)
-        tc = T.run(rotating(gpool, xs, zs), steps, 5)
-        configs["cfg4b_grouped_pool"] = {"ms": round(t, 5), "GBps": round(byts / (t * 1e-3) / 1e9, 1),
-                                         "ms_cold": round(tc, 5), "sets_cold": len(xs),
-                                         "kernel_ms": {"k_gconv": kg}}
+        # 4(b): grouped conv + MaxPool, two launches
+        c = cfg["cfg4b"]
+        t = T.run(c["step"], steps, args.warmup)
+        k = T.kernel_ms(lib, c["step"], steps, ["k_gconv", "k_maxpool"])
+        fn, xt, zt = c["rot"]
+        xs, zs = rotation_sets(xt, zt)
+        tc = T.run(rotating(fn, xs, zs), steps, args.warmup)
         del xs, zs
+        configs["cfg4b_grouped_pool"] = {
+            "ms": round(t, 5), "ms_cold": round(tc, 5),
+            "roofline": roofline("hbm", c["bytes"], t, "step (k_gconv4_3x3 + k_maxpool)",
+                                 f"{c['bytes'] / 1e6:.2f} MB per step; launch-bound at this size "
+                                 "(section 8(d))"),
+            "kernel_ms": k}
 
         # 5: ResNet-50-style, batch 64, fp32 and int8
-        inC, inH, inW, recs = acfun0.resnet50(np.random.default_rng(5))
+        inC, inH, inW, recs = cfg["cfg5"]["recs"]
         fd, path = tempfile.mkstemp(suffix=".acfun")
         os.close(fd)
         acfun0.write(path, inC, inH, inW, recs, version=2)
-        xin = cuda(rng.uniform(0, 1, (64, 224, 224, 3)).astype(np.float32))
+        xin = torch.from_numpy(rng.uniform(0, 1, (64, 224, 224, 3)).astype(np.float32)).to(dev)
         out = torch.empty((64, 1000), device=dev)
         gfl = acfun0.resnet50_flops()
         for tag, flags in (("fp32", 0), ("int8", 1)):
@@ -335,90 +617,21 @@ def main():
             def s6():
                 if lib.acfun_dev_model_infer_batch(m, 64, xin.data_ptr(), out.data_ptr(), sp) != 1000:
                     raise RuntimeError(capi.last_error())
-            t = T.run(s6, max(3, steps // 5), 2)
-            configs[f"cfg5_resnet50_b64_{tag}"] = {"ms": round(t, 3),
-                                                   "images_per_s": round(64 / (t * 1e-3), 1),
-                                                   "TFLOPS": round(64 * gfl / (t * 1e-3) / 1e12, 3)}
+            t = T.run(s6, max(3, steps // 4), 2)
+            peak = PEAK_FP32 if tag == "fp32" else PEAK_INT8
+            configs[f"cfg5_resnet50_b64_{tag}"] = {
+                "ms": round(t, 3), "images_per_s": round(64 / (t * 1e-3), 1),
+                "TFLOPS": round(64 * gfl / (t * 1e-3) / 1e12, 3),
+                "frac_peak": round(64 * gfl / (t * 1e-3) / peak, 4),
+                "work": f"{gfl / 1e9:.2f} GFLOP per image (convs and FC, direct count)"}
             lib.acfun_model_destroy(m)
         os.unlink(path)
     line["configs"] = configs
 
-    # ---------------------------------------------------------------- CPU baseline
+    # ---------------------------------------------------------------- CPU baselines
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(x, w, b, direct_flop)
+        cpu_baselines(cfg, configs, line)
     print(json.dumps(line), flush=True)
-
-
-def rotation_sets(x, y, extra=0, total=320 << 20):
-    """Copies of an input and an output tensor, enough sets that one pass over
-    them (plus `extra` bytes of fixed intermediates) exceeds the 256 MB MALL:
-    a step on set i % n then finds its operands in HBM, not in the cache."""
-    per = x.numel() * x.element_size() + y.numel() * y.element_size()
-    n = max(2, -(-(total - extra) // per))
-    xs = [x.clone() for _ in range(n)]
-    ys = [y.new_empty(y.shape) for _ in range(n)]
-    return xs, ys
-
-
-def rotating(fn, xs, ys):
-    """A step function that cycles fn over the rotation sets."""
-    state = [0]
-
-    def step():
-        i = state[0] % len(xs)
-        state[0] += 1
-        fn(xs[i], ys[i])
-    return step
-
-
-def read_traffic(path):
-    """HBM bytes per launch of the headline kernel from the committed counter
-    summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain copy of
-    known size), or None when the summary is absent."""
-    if not os.path.exists(path):
-        return None
-    vals = {}
-    with open(path) as f:
-        for ln in f:
-            parts = ln.split()
-            if len(parts) == 2 and not ln.startswith("#"):
-                try:
-                    vals[parts[0]] = float(parts[1])
-                except ValueError:
-                    pass
-    return vals.get("hbm_bytes_per_launch")
-
-
-def cpu_baseline(x, w, b, flop):
-    import numpy as np
-
-    import oracle
-    from acfun_amd.capi import bind
-    ref = oracle.ref()
-    if ref is None:
-        return {"value": None, "unit": "TFLOPS", "cores": 0, "kind": "reference",
-                "sample": "oracle/_ref/libacfun_ref.so not present"}
-    bind(ref)
-    N, H, _, Cin = x.shape
-    Cout = w.shape[1]
-    y = np.empty((N, H, H, Cout), np.float32)
-    P = lambda a: C.c_void_p(a.ctypes.data)
-    run = lambda: ref.acfun_conv2d_relu(P(x), N, H, H, Cin, P(w), P(b), 3, 3, Cout, 1, 1, P(y))
-    for _ in range(3):
-        run()
-    times = []
-    t_end = time.time() + 20.0
-    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    cores = ref.acfun_effective_cores()
-    return {"value": round(flop / med / 1e12, 4), "unit": "TFLOPS", "cores": int(cores),
-            "kind": "reference",
-            "sample": f"full headline batch (N=32) through the reference's acfun_conv2d_relu "
-                      f"(Winograd F(2,3), AVX-512/OpenMP), median of {len(times)} runs after 3 "
-                      f"warmups: {med * 1e3:.1f} ms/step"}
 
 
 if __name__ == "__main__":
