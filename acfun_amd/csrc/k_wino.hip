@@ -1557,6 +1557,13 @@ bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, co
 
 }  // namespace
 
+bool wino43_filter(const float* w, int Cin, int Cout, float* U, hipStream_t s) {
+    const int Cinp = (Cin + 15) / 16 * 16;
+    ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<4, true>), dim3((Cout + 15) / 16, Cinp / 16),
+                 dim3(256), 0, s, w, Cin, Cinp, Cout, U);
+    return check_launch("k_wino_filter_t");
+}
+
 int wino23_plan(int N, int H, int W, int Cin, int Cout, const void* in) {
     return wino23_plan_impl(N, H, W, Cin, Cout, in);
 }
@@ -1572,16 +1579,26 @@ bool wino23_filter(const float* w, int Cin, int Cout, int plan, float* U, hipStr
 bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
                   const float* bias, int Cout, float* out, int act, hipStream_t s, const float* Upre) {
     if (N <= 0 || H <= 0 || W <= 0) return true;
-    if (tile == 4) return run_fused<4, 16, 4, 8>(in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    if (tile == 4) {
+        bool done = false;
+        if (!run_wino43(in, N, H, W, Cin, w, bias, Cout, out, act, s, &done)) return false;
+        if (done) return true;
+        return run_fused<4, 16, 4, 8>(in, N, H, W, Cin, w, bias, Cout, out, act, s);
+    }
     return run_wino23(in, N, H, W, Cin, w, bias, Cout, out, act, s, Upre);
 }
 
 bool winograd_route_f32(int tile, const float* in, int N, int H, int W, int Cin, const float* w,
                         const float* bias, int Cout, float* out, int act, hipStream_t s,
                         const float* Upre) {
-    // Measured on MI355X at BASELINE config 2(b) (8 x 112^2 x 64 -> 64): the
-    // F(2,3) unit kernel (k_wino23u) takes about half the time of k_wino_fused<4>,
-    // so the F(4,3) route runs it whenever its staging conditions hold.
+    // F(4,3) runs on its unit kernel (k_wino43p) where it applies.  Elsewhere
+    // the F(2,3) unit kernels take the F(4,3) route too: measured on MI355X at
+    // BASELINE config 2(b) they take about half the time of k_wino_fused<4>.
+    if (tile == 4 && N > 0) {
+        bool done = false;
+        if (!run_wino43(in, N, H, W, Cin, w, bias, Cout, out, act, s, &done)) return false;
+        if (done) return true;
+    }
     const int tW = (W + 1) / 2, tH = (H + 1) / 2;
     const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cin >= 32;
     const bool unit23 = Cin % 4 == 0 && ((uintptr_t)in & 15u) == 0 && (tW >= 6 || small);

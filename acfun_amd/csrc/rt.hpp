@@ -184,6 +184,15 @@ bool winograd_f32(int tile, const float* in, int N, int H, int W, int Cin, const
 int wino23_plan(int N, int H, int W, int Cin, int Cout, const void* in);
 size_t wino23_filter_bytes(int Cin, int Cout);
 bool wino23_filter(const float* w, int Cin, int Cout, int plan, float* U, hipStream_t s);
+// F(4,3): the filter transform in the chunked layout U[Cinp/8][36][Cout][8]
+// (Cinp = Cin rounded up to 16, zero-padded), and the persistent unit kernel
+// (k_wino43p), which reads it.  run_wino43 sets *done when the shape suits the
+// unit kernel and it ran (Cin % 4 == 0, Cin >= 32, a 16-byte aligned input,
+// images at least 24 pixels wide, operands within 2 GB, Cout <= 4096);
+// otherwise it leaves the call to another engine.
+bool wino43_filter(const float* w, int Cin, int Cout, float* U, hipStream_t s);
+bool run_wino43(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
+                int Cout, float* out, int act, hipStream_t s, bool* done);
 // The conv2d route's Winograd step: the route names the tile the reference
 // would use; both tiles compute the direct convolution exactly over the
 // rationals, so the faster kernel for the shape runs (within the Winograd

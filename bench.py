@@ -519,9 +519,10 @@ def main():
 
         # 2(b): F(4,3) route; the fraction counts section 8(d)'s F(4,3) work
         t = T.run(cfg["cfg2b"]["step"], steps, args.warmup)
-        k = T.kernel_ms(lib, cfg["cfg2b"]["step"], steps, ["k_wino23", "k_wino_fused", "k_wino_filter_t"])
+        k = T.kernel_ms(lib, cfg["cfg2b"]["step"], steps, ["k_wino43", "k_wino23", "k_wino_fused",
+                                                             "k_wino_filter_t"])
         f43 = 1.849688064e9
-        kern = "k_wino23" if k["k_wino23"] else "k_wino_fused"
+        kern = next((n for n in ("k_wino43", "k_wino23", "k_wino_fused") if k[n]), "k_wino43")
         configs["cfg2b_conv3x3_f43"] = {
             "ms": round(t, 5), "TFLOPS_direct_equivalent": round(direct_flop / (t * 1e-3) / 1e12, 3),
             "TFLOPS_f43_work": round(f43 / (t * 1e-3) / 1e12, 3),
