@@ -19,6 +19,8 @@
 // kernel reduces in fixed split order (deterministic) before bias and ReLU.
 #include "rt.hpp"
 
+#include <memory>
+
 namespace acfun {
 namespace {
 
@@ -394,6 +396,40 @@ TileCfg default_f32_tile(int M, int N, int K, int batch) {
         if (split < 1) split = 1;
     }
     return TileCfg{64, 64, split};
+}
+
+// Tile-search candidates (kind "f32"): the four tiles x split-K 1, 2, 4, 8
+// (split s needs K >= 256 s).
+TileCfg f32_cand(int c) {
+    static const int tiles[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+    static const int splits[4] = {1, 2, 4, 8};
+    return TileCfg{tiles[c / 4][0], tiles[c / 4][1], splits[c % 4]};
+}
+
+TileCfg tuned_f32_tile(int M, int N, int K, int batch) {
+    const TileCfg d = default_f32_tile(M, N, K, batch);
+    if (batch != 1) return d;
+    const std::vector<int> key{M, N, K};
+    bool rec = false;
+    const int c = tune_lookup("f32", key, 16, &rec);
+    if (rec)
+        tune_record("f32", key, 16, [M, N, K]() -> TuneRunner {
+            const size_t ab = (size_t)M * K * 4, bb = (size_t)K * N * 4, cb = (size_t)M * N * 4;
+            if (ab + bb + cb > ((size_t)2 << 30)) return TuneRunner();
+            hipStream_t s = lib_stream();
+            auto a = std::make_shared<Scratch>(ab, s);
+            auto b = std::make_shared<Scratch>(bb, s);
+            auto cc = std::make_shared<Scratch>(cb, s);
+            if (!a->p || !b->p || !cc->p || hipMemsetD32Async((hipDeviceptr_t)a->p, kTuneFill, ab / 4, s) != hipSuccess ||
+                hipMemsetD32Async((hipDeviceptr_t)b->p, kTuneFill, bb / 4, s) != hipSuccess)
+                return TuneRunner();
+            return [=](int cand, hipStream_t st) {
+                const TileCfg t = f32_cand(cand);
+                if (t.split > 1 && K < 256 * t.split) return false;
+                return gemm_f32_cfg(M, N, K, a->as<float>(), b->as<float>(), cc->as<float>(), t, st);
+            };
+        });
+    return c >= 0 ? f32_cand(c) : d;
 }
 
 bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,

@@ -23,6 +23,7 @@
 #include "rt.hpp"
 
 #include <cstdlib>
+#include <memory>
 
 namespace acfun {
 namespace {
@@ -400,23 +401,79 @@ bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, in
     return check_launch("k_gemm32");
 }
 
+// Tile-search candidates (kind "g32"): 64 x 64 with 2 or 3 stages, 64 x 64
+// with two K groups, 128 x 64 with 2 or 3 stages, 128 x 128.
+constexpr G32Tile kG32Cand[] = {{64, 64, 2, 1}, {64, 64, 3, 1}, {64, 64, 2, 2},
+                                {128, 64, 2, 1}, {128, 64, 3, 1}, {128, 128, 2, 1}};
+constexpr int kG32NC = 6;
+
+int g32_index(const G32Tile& t) {
+    for (int i = 0; i < kG32NC; ++i)
+        if (kG32Cand[i].bm == t.bm && kG32Cand[i].bn == t.bn && kG32Cand[i].nst == t.nst &&
+            kG32Cand[i].ks == t.ks)
+            return i;
+    return 0;
+}
+// Two K groups need chunks for both (the heuristic takes them from 8 chunks).
+bool g32_admits(int c, int K) { return kG32Cand[c].ks == 1 || (K + G32_KC - 1) / G32_KC >= 4; }
+
+template <bool CONV>
+bool launch_cand(int c, int M, int N, int K, const float* A, int lda, const float* B, int ldb,
+                 float* C, int ldc, const float* bias, int act, hipStream_t s, const float* res,
+                 int ldr, const G32Conv& cv) {
+    switch (c) {
+        case 1: return launch_g32<64, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 2: return launch_g32<64, 64, 2, CONV, 2>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 3: return launch_g32<128, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 4: return launch_g32<128, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 5: return launch_g32<128, 128, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        default: return launch_g32<64, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    }
+}
+
+// The replay the tile search times for a shape: operands of the shape filled
+// with a constant
+// (A with lda = K for a GEMM, the NHWC input for a convolution), no epilogue.
+template <bool CONV>
+TuneMaker g32_maker(int M, int N, int K, const G32Conv& cv) {
+    return [=]() -> TuneRunner {
+        const size_t abytes = CONV ? (size_t)cv.bytes : (size_t)M * K * 4;
+        const size_t bbytes = (size_t)K * N * 4, cbytes = (size_t)M * N * 4;
+        if (abytes + bbytes + cbytes > ((size_t)2 << 30)) return TuneRunner();
+        hipStream_t s = lib_stream();
+        auto a = std::make_shared<Scratch>(abytes, s);
+        auto b = std::make_shared<Scratch>(bbytes, s);
+        auto c = std::make_shared<Scratch>(cbytes, s);
+        if (!a->p || !b->p || !c->p || hipMemsetD32Async((hipDeviceptr_t)a->p, kTuneFill, abytes / 4, s) != hipSuccess ||
+            hipMemsetD32Async((hipDeviceptr_t)b->p, kTuneFill, bbytes / 4, s) != hipSuccess)
+            return TuneRunner();
+        return [=](int cand, hipStream_t st) {
+            if (!g32_admits(cand, K)) return false;
+            return launch_cand<CONV>(cand, M, N, K, a->as<float>(), CONV ? cv.Cin : K, b->as<float>(), N,
+                                     c->as<float>(), N, nullptr, 0, st, nullptr, 0, cv);
+        };
+    };
+}
+
 template <bool CONV>
 bool launch_gemm32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
                    int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
                    const G32Conv& cv) {
     if (M <= 0 || N <= 0) return true;
-    const G32Tile t = pick_g32(M, N, K);
-    if (t.ks == 2)
-        return launch_g32<64, 64, 2, CONV, 2>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
-    if (t.bm == 128 && t.bn == 128)
-        return launch_g32<128, 128, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
-    if (t.bm == 128 && t.nst == 3)
-        return launch_g32<128, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
-    if (t.bm == 128)
-        return launch_g32<128, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
-    if (t.nst == 3)
-        return launch_g32<64, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
-    return launch_g32<64, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+    const std::vector<int> key = CONV ? std::vector<int>{1, M, N, K, cv.H, cv.W, cv.Cin, cv.KW, cv.stride,
+                                                         cv.pad, cv.OH, cv.OW}
+                                      : std::vector<int>{0, M, N, K};
+    bool rec = false;
+    int c = tune_lookup("g32", key, kG32NC, &rec);
+    if (rec) {
+        tune_record("g32", key, kG32NC, g32_maker<CONV>(M, N, K, cv));
+        if (autotune_wanted()) {
+            autotune_run();
+            c = tune_lookup("g32", key, kG32NC, &rec);
+        }
+    }
+    if (c < 0 || !g32_admits(c, K)) c = g32_index(pick_g32(M, N, K));
+    return launch_cand<CONV>(c, M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
 }
 }  // namespace
 
@@ -450,4 +507,13 @@ bool gemm32_ok(int M, int N, int K, const float* A, int lda, const float* B, int
            (long long)((N + 63) / 64) * ((M + 63) / 64) < 0x7fffffffll;
 }
 
+}  // namespace acfun
+
+namespace acfun {
+void gemm32_register(int M, int N, int K) {
+    const std::vector<int> key{0, M, N, K};
+    bool rec = false;
+    if (tune_lookup("g32", key, kG32NC, &rec) < 0 && rec)
+        tune_record("g32", key, kG32NC, g32_maker<false>(M, N, K, G32Conv{}));
+}
 }  // namespace acfun

@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <memory>
 #include <mutex>
 
 namespace acfun {
@@ -617,12 +618,57 @@ int i8mm_am(const I8M& p) {
     return AM_GEN;
 }
 
+// Tile-search candidates (kind "i8mm", the fp32-output kernel): 64 x 64 with 2
+// or 3 stages, 128 x 64, 64 x 128 (3 stages), 128 x 128 (2 stages).
+constexpr int kI8NC = 5;
+I8Tile i8mm_cand(int c, int per_cu) {
+    static const int t[kI8NC][3] = {{64, 64, 2}, {64, 64, 3}, {128, 64, 3}, {64, 128, 3}, {128, 128, 2}};
+    return I8Tile{t[c][0], t[c][1], t[c][2], per_cu};
+}
+
+// The replay the tile search times for an int8 conv shape: constant s8
+// activations and weights, zero scales (EPI_GEMM), fp32 output.
+TuneMaker i8mm_maker(const I8M& q, int am) {
+    I8M g = q;
+    return [g, am]() -> TuneRunner {
+        hipStream_t s = lib_stream();
+        const size_t cb = (size_t)g.M * g.N * 4;
+        if ((size_t)g.a_bytes + g.b_bytes + cb > ((size_t)2 << 30)) return TuneRunner();
+        auto a = std::make_shared<Scratch>(g.a_bytes, s);
+        auto b = std::make_shared<Scratch>(g.b_bytes, s);
+        auto c = std::make_shared<Scratch>(cb, s);
+        auto v = std::make_shared<Scratch>((size_t)(3 * g.N + 64) * 4, s);   // ws, bias, Sw, scal
+        if (!a->p || !b->p || !c->p || !v->p || hipMemsetAsync(a->p, 0x11, g.a_bytes, s) != hipSuccess ||
+            hipMemsetAsync(b->p, 0x11, g.b_bytes, s) != hipSuccess ||
+            hipMemsetAsync(v->p, 0, (size_t)(3 * g.N + 64) * 4, s) != hipSuccess)
+            return TuneRunner();
+        return [=](int cand, hipStream_t st) {
+            I8M p = g;
+            p.A = a->as<int8_t>(); p.Bt = b->as<int8_t>(); p.Cf = c->as<float>(); p.ldc = p.N;
+            float* vf = v->as<float>();
+            p.ws = vf; p.bias = vf + p.N; p.Sw = (const int*)(vf + 2 * p.N); p.scal = vf + 3 * p.N;
+            p.s_in = nullptr; p.alpha = p.beta = nullptr; p.res = nullptr; p.amax = nullptr;
+            p.epi = EPI_GEMM; p.act = 0; p.vec = 1;
+            const I8Tile t = i8mm_cand(cand, pick_i8mm_tile(p.M, p.N, p.K).per_cu);
+            return launch_i8mm_f32(p, t, am, st);
+        };
+    };
+}
+
 bool launch_i8mm(I8M& p, hipStream_t s) {
     if (p.M <= 0 || p.N <= 0) return true;
-    const I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
+    I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
     p.vec = al16(p.Cf) && p.ldc % 4 == 0 && (!p.res || (al16(p.res) && p.ldr % 4 == 0));
-    return launch_i8mm_f32(p, t, i8mm_am(p), s);
+    const int am = i8mm_am(p);
+    if (!getenv("ACFUN_I8_TILE")) {
+        const std::vector<int> key{am, p.M, p.N, p.K, p.H, p.W, p.Cinp, p.KW, p.stride, p.pad, p.OH, p.OW};
+        bool rec = false;
+        const int c = tune_lookup("i8mm", key, kI8NC, &rec);
+        if (rec) tune_record("i8mm", key, kI8NC, i8mm_maker(p, am));
+        if (c >= 0) t = i8mm_cand(c, t.per_cu);
+    }
+    return launch_i8mm_f32(p, t, am, s);
 }
 
 // A requantized s8 output: the first pass writes the per-workgroup maxima of

@@ -13,6 +13,8 @@
 // bias and ReLU, so the input is read once and the output written once.
 #include "rt.hpp"
 
+#include <memory>
+
 #include <type_traits>
 
 namespace acfun {
@@ -1460,6 +1462,54 @@ bool wino23_filter_impl(const float* w, int Cin, int Cout, int plan, float* U, h
     return check_launch("k_wino_filter_t");
 }
 
+// Tile-search candidates (kind "w23") for the unit kernels (plan 1): 0 the
+// persistent 16-wide units, 1 16-wide units one per workgroup, 2 persistent
+// 8-wide, 3 8-wide one per workgroup, 4 units of two 4 x 4-tile blocks.  The
+// 16-wide units run on images of at least 12 tile columns, the paired blocks
+// only on images of at most 4 x 4 tiles (where the heuristic takes them).
+constexpr int kW23NC = 5;
+bool w23_launch(int c, const float* in, const float* U, const float* bias, float* out, int N, int H,
+                int W, int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s,
+                bool* launched) {
+    *launched = false;
+    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
+    if ((c <= 1 && tW < 12) || (c == 4 && !small)) return true;
+    switch (c) {
+        case 0: return launch_wino23p<16>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s, launched);
+        case 2: return launch_wino23p<8>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s, launched);
+        case 4: return launch_wino23p<4, 2>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s, launched);
+        default: break;
+    }
+    *launched = true;
+    if (c == 1) return launch_wino23u<16>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
+    return launch_wino23u<8>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
+}
+
+// The replay the tile search times: input and filter transform of the shape
+// filled with a constant, no bias, no activation.
+TuneMaker w23_maker(int N, int H, int W, int Cin, int Cout) {
+    return [=]() -> TuneRunner {
+        const int Cinp = (Cin + 15) / 16 * 16, tH = (H + 1) / 2, tW = (W + 1) / 2;
+        const size_t ib = (size_t)N * H * W * Cin * 4, ub = (size_t)16 * Cout * Cinp * 4,
+                     ob = (size_t)N * H * W * Cout * 4;
+        if (ib + ub + ob > ((size_t)2 << 30)) return TuneRunner();
+        hipStream_t s = lib_stream();
+        auto x = std::make_shared<Scratch>(ib, s);
+        auto u = std::make_shared<Scratch>(ub, s);
+        auto o = std::make_shared<Scratch>(ob, s);
+        if (!x->p || !u->p || !o->p || hipMemsetD32Async((hipDeviceptr_t)x->p, kTuneFill, ib / 4, s) != hipSuccess ||
+            hipMemsetD32Async((hipDeviceptr_t)u->p, kTuneFill, ub / 4, s) != hipSuccess)
+            return TuneRunner();
+        return [=](int cand, hipStream_t st) {
+            bool launched = false;
+            if (!w23_launch(cand, x->as<float>(), u->as<float>(), nullptr, o->as<float>(), N, H, W, Cin,
+                            Cinp, Cout, tH, tW, 0, st, &launched))
+                return false;
+            return launched;
+        };
+    };
+}
+
 // Upre: the filter already transformed for this shape's plan (a model's cached
 // transform), or null to transform it here.
 bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
@@ -1477,6 +1527,17 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
     if (plan == 1) {
         if (!Upre && !wino23_filter_impl(w, Cin, Cout, 1, Uown.as<float>(), s)) return false;
+        // the tile search's choice of unit kernel for this shape, if any
+        const std::vector<int> key{N, H, W, Cin, Cout};
+        bool rec = false;
+        const int c = tune_lookup("w23", key, kW23NC, &rec);
+        if (rec) tune_record("w23", key, kW23NC, w23_maker(N, H, W, Cin, Cout));
+        if (c >= 0) {
+            bool launched = false;
+            if (!w23_launch(c, in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s, &launched))
+                return false;
+            if (launched) return true;
+        }
         bool launched = false;
         if (small) {
             if (!launch_wino23p<4, 2>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,

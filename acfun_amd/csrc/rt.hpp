@@ -8,6 +8,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <vector>
 
 namespace acfun {
@@ -297,14 +298,33 @@ bool conv2d_route_f32(const float* in, int N, int H, int W, int Cin, const float
                       int groups, float* out, int act, hipStream_t s,
                       const float* wino_U = nullptr);
 
-// Tile-config table (autotune).
+// The tile search (tune.cpp).  A kernel family (kind "g32", "i8mm", "w23",
+// "f32") asks tune_lookup for the searched candidate of a shape (key) among its
+// ncand candidates: -1 when the search has not covered (arch, kind, key,
+// ncand), and then *record is set the
+// first time the shape is seen in this process, so that the caller registers
+// it with tune_record: ncand candidates and a maker that, called by the
+// search, allocates scratch operands of the shape and returns a runner that
+// launches candidate c on them (false: the shape does not admit c).
+using TuneRunner = std::function<bool(int cand, hipStream_t s)>;
+using TuneMaker = std::function<TuneRunner()>;
+const char* device_arch();      // the current device's gfx name, e.g. "gfx950"
+int tune_lookup(const char* kind, const std::vector<int>& key, int ncand, bool* record);
+void tune_record(const char* kind, const std::vector<int>& key, int ncand, TuneMaker maker);
+bool autotune_wanted();         // ACFUN_AUTOTUNE=1: true at the first ask of a process
+// The replays fill their fp32 operands with this bit pattern (0.01f), not
+// zeros, so the MFMA units see ordinary data.
+constexpr unsigned kTuneFill = 0x3c23d70au;
+void gemm32_register(int M, int N, int K);   // a GEMM shape for the next search
+void autotune_run();
+const char* tune_status();
+
+// k_gemm_f32 tiles (the unaligned fallback).
 struct TileCfg { int bm, bn, split; };
 TileCfg default_f32_tile(int M, int N, int K, int batch = 1);
 TileCfg tuned_f32_tile(int M, int N, int K, int batch = 1);
 // Runs one fp32 GEMM with an explicit tile config (used by the tile search).
 bool gemm_f32_cfg(int M, int N, int K, const float* A, const float* B, float* C,
                   const TileCfg& cfg, hipStream_t s);
-void autotune_run();
-const char* tune_status();
 
 }  // namespace acfun

@@ -1,43 +1,60 @@
-// tune.cpp -- MFMA tile-shape search, replacing the reference's cache-blocking
-// autotune (src/autotune.cpp:29-30,148-302,336-388).
+// tune.cpp -- the tile search, replacing the reference's cache-blocking
+// autotune (src/autotune.cpp:29-30,89-142,148-302,336-388).
 //
-// The reference searches (KC, NC) cache blocks for its CPU micro-kernel and
-// caches the winner per machine.  On the GPU the free parameters are the
-// workgroup tile (BM x BN of the MFMA kernel) and the split-K factor, which
-// trade occupancy of the 256 CUs against operand reuse.  acfun_autotune()
-// times every candidate on every GEMM shape this process has run (plus the
-// shapes named in ACFUN_TUNE_SHAPES="MxNxK,..."), keeps the fastest per
-// shape, and writes them to $HOME/.cache/acfun_amd/tune_gfx950.txt, which
-// later processes read at first use.  ACFUN_AUTOTUNE=1 runs the search at the
-// first GEMM of a process.
+// The reference times (KC, NC) cache blocks for its CPU micro-kernel per
+// GEMM shape and caches the winners per machine.  Here the free parameters
+// are the launch shapes of the kernels that run:
+//   "g32"   k_gemm32 (fp32 GEMM, 1x1 and implicit-GEMM convs): tile, stages and
+//           K groups;
+//   "i8mm"  k_i8mm (int8 convs): tile and stages;
+//   "w23"   the F(2,3) unit kernels: unit width and persistent or one unit per
+//           workgroup;
+//   "f32"   k_gemm_f32 (the unaligned fallback): tile and split-K.
+// A kernel family asks tune_lookup() for its shape's choice and, the first
+// time a shape is seen in a process, registers it with tune_record() together
+// with a maker that can replay the launch on scratch operands of that shape.
+// acfun_autotune() times every candidate of every registered shape (plus the
+// GEMM shapes named in ACFUN_TUNE_SHAPES="MxNxK,..."), keeps the fastest and
+// writes the table to the cache file ($ACFUN_TUNE_CACHE, else
+// $HOME/.cache/acfun_amd/tune.txt), one line per (arch, kind, shape):
+//   <arch> <kind> <ncand> <k0>,<k1>,... <choice>
+// so one file serves several GPU types.  Later processes read it at first
+// use; ACFUN_AUTOTUNE=1 runs the search at the first GEMM of a process.
 #include <sys/stat.h>
 
 #include <algorithm>
 #include <cerrno>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
-#include <set>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "rt.hpp"
 
 namespace acfun {
 namespace {
 
-using Key = std::tuple<int, int, int>;
+using TKey = std::tuple<std::string, std::string, std::vector<int>>;   // arch, kind, shape
+struct Pending { std::string arch, kind; std::vector<int> key; int ncand; TuneMaker maker; };
+
 std::mutex g_mu;
-std::map<Key, TileCfg> g_table;
-std::set<Key> g_seen;
+std::map<TKey, std::pair<int, int>> g_table;    // (choice, candidates) per point, all arches
+std::map<TKey, size_t> g_index;                 // points registered in this process -> g_pending
+std::vector<Pending> g_pending;
 bool g_loaded = false;
 bool g_busy = false;
-std::string g_status = "default heuristic (no tile search run)";
+std::string g_status = "default heuristics (no tile search run)";
+long long g_hits = 0;                           // launches that used a searched choice
+std::string g_status_out;
 
 std::string cache_path() {
+    if (const char* p = std::getenv("ACFUN_TUNE_CACHE"); p && *p) return p;
     const char* h = std::getenv("HOME");
-    return std::string(h ? h : "/tmp") + "/.cache/acfun_amd/tune_gfx950.txt";
+    return std::string(h ? h : "/tmp") + "/.cache/acfun_amd/tune.txt";
 }
 
 void load_cache_locked() {
@@ -45,9 +62,13 @@ void load_cache_locked() {
     g_loaded = true;
     FILE* f = fopen(cache_path().c_str(), "r");
     if (!f) return;
-    int M, N, K, bm, bn, sp, n = 0;
-    while (fscanf(f, "TILE %d %d %d %d %d %d\n", &M, &N, &K, &bm, &bn, &sp) == 6) {
-        g_table[Key{M, N, K}] = TileCfg{bm, bn, sp};
+    char arch[64], kind[16], keys[512];
+    int ncand, choice, n = 0;
+    while (fscanf(f, "%63s %15s %d %511s %d", arch, kind, &ncand, keys, &choice) == 5) {
+        std::vector<int> key;
+        for (char* t = strtok(keys, ","); t; t = strtok(nullptr, ",")) key.push_back(atoi(t));
+        if (choice < 0 || choice >= ncand || key.empty()) continue;
+        g_table[TKey{arch, kind, key}] = {choice, ncand};
         ++n;
     }
     fclose(f);
@@ -65,73 +86,92 @@ bool make_dirs(const std::string& dir) {
     return stat(dir.c_str(), &st) == 0 && S_ISDIR(st.st_mode);
 }
 
-void save_cache_locked() {
-    std::string p = cache_path();
-    if (!make_dirs(p.substr(0, p.rfind('/')))) return;
+bool save_cache_locked() {
+    const std::string p = cache_path();
+    const size_t slash = p.rfind('/');
+    if (slash != std::string::npos && slash > 0 && !make_dirs(p.substr(0, slash))) return false;
     FILE* f = fopen(p.c_str(), "w");
-    if (!f) return;
-    for (auto& kv : g_table)
-        fprintf(f, "TILE %d %d %d %d %d %d\n", std::get<0>(kv.first), std::get<1>(kv.first),
-                std::get<2>(kv.first), kv.second.bm, kv.second.bn, kv.second.split);
-    fclose(f);
+    if (!f) return false;
+    for (auto& kv : g_table) {
+        const auto& [arch, kind, key] = kv.first;
+        std::string ks;
+        for (size_t i = 0; i < key.size(); ++i) ks += (i ? "," : "") + std::to_string(key[i]);
+        fprintf(f, "%s %s %d %s %d\n", arch.c_str(), kind.c_str(), kv.second.second, ks.c_str(),
+                kv.second.first);
+    }
+    return fclose(f) == 0;
 }
 
-float time_cfg(int M, int N, int K, const float* A, const float* B, float* C, const TileCfg& c,
-               hipStream_t s) {
-    hipEvent_t e0, e1;
-    hipEventCreate(&e0);
-    hipEventCreate(&e1);
-    if (!gemm_f32_cfg(M, N, K, A, B, C, c, s)) return 1e30f;  // warm
+// Mean time of one run of candidate c: one untimed run, then the best of three
+// timed batches of five; a candidate the shape does not admit returns +inf.
+float time_candidate(const TuneRunner& run, int c, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    if (!run(c, s)) return 1e30f;
     float best = 1e30f;
     for (int r = 0; r < 3; ++r) {
-        hipEventRecord(e0, s);
-        for (int i = 0; i < 5; ++i) gemm_f32_cfg(M, N, K, A, B, C, c, s);
-        hipEventRecord(e1, s);
-        hipEventSynchronize(e1);
-        float ms = 0;
-        hipEventElapsedTime(&ms, e0, e1);
-        best = std::min(best, ms / 5);
+        if (hipEventRecord(e0, s) != hipSuccess) return 1e30f;
+        for (int i = 0; i < 5; ++i)
+            if (!run(c, s)) return 1e30f;
+        if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e30f;
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e30f;
+        best = std::min(best, ms / 5.f);
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
     return best;
 }
 
 }  // namespace
 
-TileCfg tuned_f32_tile(int M, int N, int K, int batch) {
-    bool run_now = false;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        load_cache_locked();
-        if (!g_busy && batch == 1) g_seen.insert(Key{M, N, K});
-        auto it = g_table.find(Key{M, N, K});
-        if (batch == 1 && it != g_table.end()) return it->second;
-        static bool env_checked = false;
-        if (!env_checked && !g_busy) {
-            env_checked = true;
-            const char* e = std::getenv("ACFUN_AUTOTUNE");
-            run_now = e && std::atoi(e) > 0;
-        }
+const char* device_arch() {
+    static std::mutex mu;
+    static std::string names[16];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 16) return "unknown";
+    std::lock_guard<std::mutex> lk(mu);
+    if (names[d].empty()) {
+        hipDeviceProp_t pr;
+        if (hipGetDeviceProperties(&pr, d) != hipSuccess) return "unknown";
+        std::string a = pr.gcnArchName;
+        names[d] = a.substr(0, a.find(':'));
     }
-    if (run_now) {
-        autotune_run();
-        std::lock_guard<std::mutex> lk(g_mu);
-        auto it = g_table.find(Key{M, N, K});
-        if (batch == 1 && it != g_table.end()) return it->second;
+    return names[d].c_str();
+}
+
+int tune_lookup(const char* kind, const std::vector<int>& key, int ncand, bool* record) {
+    *record = false;
+    const TKey k{device_arch(), kind, key};
+    std::lock_guard<std::mutex> lk(g_mu);
+    load_cache_locked();
+    auto it = g_table.find(k);
+    // a choice searched over another candidate list (an older build) is ignored
+    if (it != g_table.end() && it->second.second == ncand) {
+        ++g_hits;
+        return it->second.first;
     }
-    return default_f32_tile(M, N, K, batch);
+    *record = !g_busy && g_index.find(k) == g_index.end();
+    return -1;
+}
+
+void tune_record(const char* kind, const std::vector<int>& key, int ncand, TuneMaker maker) {
+    TKey k{device_arch(), kind, key};
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_busy || g_index.count(k)) return;
+    g_index[k] = g_pending.size();
+    g_pending.push_back(Pending{std::get<0>(k), kind, key, ncand, std::move(maker)});
+}
+
+bool autotune_wanted() {
+    static int want = -1;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (want < 0) {
+        const char* e = std::getenv("ACFUN_AUTOTUNE");
+        want = e && std::atoi(e) > 0 ? 1 : 0;
+        return want == 1;
+    }
+    return false;
 }
 
 void autotune_run() {
-    std::set<Key> shapes;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        load_cache_locked();
-        if (g_busy) return;
-        g_busy = true;
-        shapes = g_seen;
-    }
+    // GEMM shapes named in the environment join the shapes this process ran
     if (const char* e = std::getenv("ACFUN_TUNE_SHAPES")) {
         std::string s(e);
         size_t pos = 0;
@@ -139,48 +179,63 @@ void autotune_run() {
             size_t nx = s.find(',', pos);
             std::string t = s.substr(pos, nx == std::string::npos ? std::string::npos : nx - pos);
             int M, N, K;
-            if (sscanf(t.c_str(), "%dx%dx%d", &M, &N, &K) == 3) shapes.insert(Key{M, N, K});
+            if (sscanf(t.c_str(), "%dx%dx%d", &M, &N, &K) == 3 && M > 0 && N > 0 && K > 0)
+                gemm32_register(M, N, K);
             if (nx == std::string::npos) break;
             pos = nx + 1;
         }
     }
-    if (shapes.empty()) shapes.insert(Key{1024, 1024, 1024});
-    hipStream_t s = lib_stream();
-    const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-    int tuned = 0;
-    for (const Key& k : shapes) {
-        int M = std::get<0>(k), N = std::get<1>(k), K = std::get<2>(k);
-        size_t bytes = sizeof(float) * ((size_t)M * K + (size_t)K * N + (size_t)M * N);
-        if (bytes > (size_t)4 << 30) continue;
-        Scratch a(sizeof(float) * (size_t)M * K, s), b(sizeof(float) * (size_t)K * N, s),
-            c(sizeof(float) * (size_t)M * N, s);
-        if (!a.p || !b.p || !c.p) continue;
-        hipMemsetAsync(a.p, 0, sizeof(float) * (size_t)M * K, s);
-        hipMemsetAsync(b.p, 0, sizeof(float) * (size_t)K * N, s);
-        TileCfg best = default_f32_tile(M, N, K);
-        float best_ms = time_cfg(M, N, K, a.as<float>(), b.as<float>(), c.as<float>(), best, s);
-        for (auto& cc : cand)
-            for (int sp : {1, 2, 4, 8}) {
-                if (sp > 1 && K < 256 * sp) continue;
-                TileCfg t{cc[0], cc[1], sp};
-                float ms = time_cfg(M, N, K, a.as<float>(), b.as<float>(), c.as<float>(), t, s);
-                if (ms < best_ms) { best_ms = ms; best = t; }
-            }
+    std::vector<Pending> todo;
+    {
         std::lock_guard<std::mutex> lk(g_mu);
-        g_table[k] = best;
-        ++tuned;
+        load_cache_locked();
+        if (g_busy) return;
+        g_busy = true;
+        todo.swap(g_pending);
+        g_index.clear();
     }
-    hipStreamSynchronize(s);
+    hipStream_t s = lib_stream();
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int tuned = 0;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        for (Pending& p : todo) {
+            const TKey k{p.arch, p.kind, p.key};
+            {
+                std::lock_guard<std::mutex> lk(g_mu);
+                auto it = g_table.find(k);
+                if (it != g_table.end() && it->second.second == p.ncand) continue;
+            }
+            TuneRunner run = p.maker ? p.maker() : TuneRunner();
+            if (!run) continue;
+            int best = -1;
+            float best_ms = 1e30f;
+            for (int c = 0; c < p.ncand; ++c) {
+                const float ms = time_candidate(run, c, s, e0, e1);
+                if (ms < best_ms) { best_ms = ms; best = c; }
+            }
+            (void)hipStreamSynchronize(s);
+            if (best < 0) continue;
+            std::lock_guard<std::mutex> lk(g_mu);
+            g_table[k] = {best, p.ncand};
+            ++tuned;
+        }
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    (void)hipGetLastError();     // a candidate refused by the runtime leaves no error behind
     std::lock_guard<std::mutex> lk(g_mu);
-    save_cache_locked();
+    const bool saved = save_cache_locked();
     g_busy = false;
-    g_status = "tile search: " + std::to_string(tuned) + " shapes tuned, cached at " + cache_path();
+    g_status = "tile search (" + std::string(device_arch()) + "): " + std::to_string(tuned) +
+               " shapes tuned, " + (saved ? "cached at " : "NOT cached (cannot write) ") + cache_path();
 }
 
 const char* tune_status() {
     std::lock_guard<std::mutex> lk(g_mu);
     load_cache_locked();
-    return g_status.c_str();
+    g_status_out = g_status + "; " + std::to_string(g_hits) + " launches used a searched choice";
+    return g_status_out.c_str();
 }
 
 }  // namespace acfun

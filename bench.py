@@ -52,6 +52,9 @@ def parse():
                          "cfg3b, cfg3a_q, cfg3b_q, cfg4a, cfg4b), then 3 plain copies of 256 MiB "
                          "(the counter scale reference); prints no JSON line")
     ap.add_argument("--traffic", action="store_true", help="the same as --profile cfg2a")
+    ap.add_argument("--tune", action="store_true",
+                    help="run the tile search (acfun_autotune) over every config's shapes first, as "
+                         "the reference's benchmark --tune does (src/benchmark.cpp:1164-1171)")
     return ap.parse_args()
 
 
@@ -404,6 +407,32 @@ def cpu_baselines(cfg, configs, line):
             + ("; int8 convs are acfun_conv2d_int8 on the batch" if int8 else ""))
 
 
+def tune_all(lib, torch, dev, sp, cfg, rng):
+    """One step of every config (and one batch-64 pass of each config-5 model)
+    registers their shapes; acfun_autotune() then searches and caches them."""
+    import numpy as np
+
+    from acfun_amd import acfun0
+    for k, c in cfg.items():
+        if "step" in c:
+            c["step"]()
+    inC, inH, inW, recs = cfg["cfg5"]["recs"]
+    fd, path = tempfile.mkstemp(suffix=".acfun")
+    os.close(fd)
+    acfun0.write(path, inC, inH, inW, recs, version=2)
+    xin = torch.from_numpy(rng.uniform(0, 1, (64, 224, 224, 3)).astype(np.float32)).to(dev)
+    out = torch.empty((64, 1000), device=dev)
+    for flags in (0, 1):
+        m = lib.acfun_model_load_ex(path.encode(), flags)
+        if m:
+            lib.acfun_dev_model_infer_batch(m, 64, xin.data_ptr(), out.data_ptr(), sp)
+            torch.cuda.synchronize()
+            lib.acfun_model_destroy(m)
+    os.unlink(path)
+    torch.cuda.synchronize()
+    lib.acfun_autotune()
+
+
 # ------------------------------------------------------------------ main
 def main():
     args = parse()
@@ -433,6 +462,8 @@ def main():
             raise RuntimeError(capi.last_error())
 
     cfg = make_configs(lib, torch, dev, sp, rng, check)
+    if args.tune:
+        tune_all(lib, torch, dev, sp, cfg, rng)
 
     if args.traffic:
         args.profile = "cfg2a"
@@ -628,6 +659,7 @@ def main():
             lib.acfun_model_destroy(m)
         os.unlink(path)
     line["configs"] = configs
+    line["config"]["tile_search"] = lib.acfun_tune_status().decode()
 
     # ---------------------------------------------------------------- CPU baselines
     if not args.no_cpu:
