@@ -73,6 +73,8 @@ SIGNATURES = {
                                            _p, _i, _p]),
     "acfun_dev_conv2d_dw_maxpool": (_i, [_p, _i, _i, _i, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
                                          _i, _p, _i, _p]),
+    "acfun_dev_conv2d_g_maxpool": (_i, [_p, _i, _i, _i, _i, _p, _p, _i, _i, _i, _i, _i, _i, _i,
+                                        _i, _i, _i, _p, _i, _p]),
     "acfun_dev_maxpool": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "acfun_dev_fc": (_i, [_p, _i, _i, _p, _p, _i, _p, _i, _p]),
     "acfun_dev_softmax": (_i, [_p, _i, _i, _p, _p]),

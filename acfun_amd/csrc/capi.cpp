@@ -538,6 +538,37 @@ int acfun_dev_conv2d_dw_maxpool(const float* input, int N, int H, int W, int C,
                ? 0 : -1;
 }
 
+int acfun_dev_conv2d_g_maxpool(const float* input, int N, int H, int W, int Cin,
+                               const float* weight, const float* bias, int KH, int KW, int Cout,
+                               int stride, int pad, int groups, int act, int pool, int pool_stride,
+                               int pool_pad, float* output, int post_relu, void* stream) {
+    if (!ensure_device()) return -1;
+    if (N <= 0 || stride <= 0 || pool_stride <= 0 || KH <= 0 || KW <= 0 || pool <= 0) return 0;
+    if (groups <= 0 || Cin % groups != 0 || Cout % groups != 0) {
+        set_error("acfun_dev_conv2d_g_maxpool: groups must divide Cin and Cout");
+        return -1;
+    }
+    const int OH = conv_out(H, KH, stride, pad), OW = conv_out(W, KW, stride, pad);
+    if (OH <= 0 || OW <= 0) return 0;
+    const int PH = conv_out(OH, pool, pool_stride, pool_pad),
+              PW = conv_out(OW, pool, pool_stride, pool_pad);
+    if (PH <= 0 || PW <= 0) return 0;
+    hipStream_t s = resolve(stream);
+    if (gconv_pool_ok(N, H, W, Cin, KH, KW, Cout, stride, pad, groups, pool, pool_stride, pool_pad,
+                      input, weight, output))
+        return gconv_pool_f32(input, N, H, W, Cin, weight, bias, Cout, stride, pad, groups, act,
+                              pool_pad, output, post_relu, s) ? 0 : -1;
+    // other shapes: the conv (acfun_conv2d_g's route) and the pool through a
+    // pooled intermediate
+    Scratch y((size_t)N * OH * OW * Cout * sizeof(float), s);
+    if (!y.p) return -1;
+    return conv2d_route_f32(input, N, H, W, Cin, weight, bias, KH, KW, Cout, stride, pad, groups,
+                            y.as<float>(), act, s) &&
+                   maxpool_f32(y.as<float>(), N, OH, OW, Cout, pool, pool_stride, pool_pad, output,
+                               post_relu, s)
+               ? 0 : -1;
+}
+
 int acfun_dev_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride, int pad,
                       float* output, int post_relu, void* stream) {
     if (!ensure_device()) return -1;

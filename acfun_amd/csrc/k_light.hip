@@ -539,6 +539,193 @@ __global__ __launch_bounds__(256) void k_gconv4_3x3(const float* __restrict__ in
     *(f4*)(out + (((long long)n * OH + oh) * OW + ow) * Cout + co) = s;
 }
 
+// Grouped 3x3 conv (Cin_p = 4 CINQ, the all-FMA rule) + activation fused with
+// a 3x3 / stride-2 MaxPool: a lane owns one pooled pixel x 4 channels, computes
+// the conv outputs of its pool window with k_gconv4_3x3's arithmetic (bias,
+// then one fmaf per in-range tap and input channel, in order) and reduces them
+// with k_maxpool's per-channel compare (max_ps below pvec_end), so the result
+// is bit for bit the two kernels' without the conv output in memory.  The
+// lane's 9 x CP weight quads are loaded once.
+template <int CINQ>
+__global__ __launch_bounds__(256) void k_gconv3_pool(const float* __restrict__ in, int N, int H,
+                                                     int W, int Cin, const float* __restrict__ w,
+                                                     const float* __restrict__ bias, int Cout,
+                                                     int stride, int pad, int groups, int OH,
+                                                     int OW, int act, int vec_end, int PP, int PH,
+                                                     int PW, int pvec_end,
+                                                     float* __restrict__ out, int post_relu) {
+    constexpr int CP = 4 * CINQ;
+    const int cq = Cout >> 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= N * PH * PW * cq) return;
+    const int q = idx % cq;
+    int p = idx / cq;
+    const int pw = p % PW;
+    p /= PW;
+    const int ph = p % PH;
+    const int n = p / PH;
+    const int Cout_p = Cout / groups;
+    const int co = 4 * q;
+    const int g = co / Cout_p, oc = co - g * Cout_p;
+    const float* wg = w + (long long)g * Cout_p * 9 * CP + oc;
+    const float* img = in + (long long)n * H * W * Cin + (long long)g * CP;
+    f4 wv[9][CP];
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+        for (int i = 0; i < CP; ++i) wv[t][i] = *(const f4*)(wg + (long long)(t * CP + i) * Cout_p);
+    const f4 b4 = bias ? *(const f4*)(bias + co) : f4{0.f, 0.f, 0.f, 0.f};
+    f4 m = {-1e30f, -1e30f, -1e30f, -1e30f};
+    for (int kh = 0; kh < 3; ++kh) {
+        const int oh = 2 * ph - PP + kh;
+        if ((unsigned)oh >= (unsigned)OH) continue;
+        for (int kw = 0; kw < 3; ++kw) {
+            const int ow = 2 * pw - PP + kw;
+            if ((unsigned)ow >= (unsigned)OW) continue;
+            f4 x[9][CINQ];
+            bool ok[9];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int ih = oh * stride - pad + t / 3, iw = ow * stride - pad + t % 3;
+                ok[t] = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+                const float* px = img + ((long long)(ok[t] ? ih : 0) * W + (ok[t] ? iw : 0)) * Cin;
+#pragma unroll
+                for (int c = 0; c < CINQ; ++c) x[t][c] = *(const f4*)(px + 4 * c);
+            }
+            f4 sv = b4;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                if (!ok[t]) continue;
+#pragma unroll
+                for (int i = 0; i < CP; ++i) {
+                    const float xi = x[t][i >> 2][i & 3];
+                    sv.x = fmaf(xi, wv[t][i].x, sv.x);
+                    sv.y = fmaf(xi, wv[t][i].y, sv.y);
+                    sv.z = fmaf(xi, wv[t][i].z, sv.z);
+                    sv.w = fmaf(xi, wv[t][i].w, sv.w);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float v = sv[u];
+                if (act == 1) {
+                    if (oc + u < vec_end) v = vmax(v, 0.0f);
+                    else if (v < 0.0f) v = 0.0f;
+                }
+                if (co + u < pvec_end) m[u] = vmax(m[u], v);
+                else if (v > m[u]) m[u] = v;
+            }
+        }
+    }
+    if (post_relu) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (co + u < pvec_end) m[u] = vmax(m[u], 0.0f);
+            else if (m[u] < 0.0f) m[u] = 0.0f;
+        }
+    }
+    *(f4*)(out + (((long long)n * PH + ph) * PW + pw) * Cout + co) = m;
+}
+
+// The same fused pair for a small image: one 256-thread workgroup per (image,
+// group) stages the group's input channels of the whole image in LDS, computes
+// the group's conv outputs into LDS (a thread keeps one output-channel quad's
+// 9 x CP weight quads in registers and walks the pixels) and then pools them;
+// the arithmetic per value is k_gconv3_pool's.  LDS: H*W*CP + OH*OW*Cout_p
+// floats (gconv_pool_img_lds).
+template <int CINQ>
+__global__ __launch_bounds__(256) void k_gconv3_pool_img(
+    const float* __restrict__ in, int H, int W, int Cin, const float* __restrict__ w,
+    const float* __restrict__ bias, int Cout, int stride, int pad, int groups, int OH, int OW,
+    int act, int vec_end, int PP, int PH, int PW, int pvec_end, float* __restrict__ out,
+    int post_relu) {
+    constexpr int CP = 4 * CINQ;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int n = blockIdx.x / groups, g = blockIdx.x - n * groups;
+    const int Cout_p = Cout / groups, nq = Cout_p >> 2;
+    f4* const xs = (f4*)lds;                               // [H*W][CINQ]
+    f4* const ys = xs + H * W * CINQ;                      // [OH*OW][nq]
+    const int tid = threadIdx.x;
+    const float* img = in + (long long)n * H * W * Cin + (long long)g * CP;
+    // conv: thread -> output-channel quad qo = tid % nq, pixels tid / nq, + 256 / nq, ...
+    // (its weights and bias are loaded while the image is staged)
+    const int per = 256 / nq;
+    const int qo = tid % nq, p0 = tid / nq;
+    const int oc = 4 * qo, co = g * Cout_p + oc;
+    f4 wv[9][CP];
+    {
+        const float* wg = w + (long long)g * Cout_p * 9 * CP + oc;
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+#pragma unroll
+            for (int i = 0; i < CP; ++i) wv[t][i] = *(const f4*)(wg + (long long)(t * CP + i) * Cout_p);
+    }
+    const f4 b4 = bias ? *(const f4*)(bias + co) : f4{0.f, 0.f, 0.f, 0.f};
+    for (int i = tid; i < H * W * CINQ; i += 256) {
+        const int px = i / CINQ, c = i - px * CINQ;
+        xs[i] = *(const f4*)(img + (long long)px * Cin + 4 * c);
+    }
+    __syncthreads();
+    if (p0 < per) {
+        for (int pix = p0; pix < OH * OW; pix += per) {
+            const int oh = pix / OW, ow = pix - oh * OW;
+            f4 sv = b4;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int ih = oh * stride - pad + t / 3, iw = ow * stride - pad + t % 3;
+                if ((unsigned)ih >= (unsigned)H || (unsigned)iw >= (unsigned)W) continue;
+                const f4* xp = xs + (ih * W + iw) * CINQ;
+#pragma unroll
+                for (int i = 0; i < CP; ++i) {
+                    const float xi = xp[i >> 2][i & 3];
+                    sv.x = fmaf(xi, wv[t][i].x, sv.x);
+                    sv.y = fmaf(xi, wv[t][i].y, sv.y);
+                    sv.z = fmaf(xi, wv[t][i].z, sv.z);
+                    sv.w = fmaf(xi, wv[t][i].w, sv.w);
+                }
+            }
+            if (act == 1) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (oc + u < vec_end) sv[u] = vmax(sv[u], 0.0f);
+                    else if (sv[u] < 0.0f) sv[u] = 0.0f;
+                }
+            }
+            ys[pix * nq + qo] = sv;
+        }
+    }
+    __syncthreads();
+    // pool: thread -> (pooled pixel, quad)
+    for (int i = tid; i < PH * PW * nq; i += 256) {
+        const int q = i % nq, pp = i / nq;
+        const int ph = pp / PW, pw = pp - ph * PW;
+        const int co = g * Cout_p + 4 * q;
+        f4 m = {-1e30f, -1e30f, -1e30f, -1e30f};
+        for (int kh = 0; kh < 3; ++kh) {
+            const int oh = 2 * ph - PP + kh;
+            if ((unsigned)oh >= (unsigned)OH) continue;
+            for (int kw = 0; kw < 3; ++kw) {
+                const int ow = 2 * pw - PP + kw;
+                if ((unsigned)ow >= (unsigned)OW) continue;
+                const f4 v = ys[(oh * OW + ow) * nq + q];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (co + u < pvec_end) m[u] = vmax(m[u], v[u]);
+                    else if (v[u] > m[u]) m[u] = v[u];
+                }
+            }
+        }
+        if (post_relu) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (co + u < pvec_end) m[u] = vmax(m[u], 0.0f);
+                else if (m[u] < 0.0f) m[u] = 0.0f;
+            }
+        }
+        *(f4*)(out + (((long long)n * PH + ph) * PW + pw) * Cout + co) = m;
+    }
+}
+
 // MaxPool: channels below vec_end use max_ps semantics, the rest the scalar
 // compare of src/layers.cpp:221-246 (they differ only for NaN / signed zero).
 __global__ void k_maxpool(const float* __restrict__ in, int N, int H, int W, int C, int pool,
@@ -735,6 +922,56 @@ bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w
                      (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
                      nPWB, nQG, (int)items, (float4*)out, post_relu);
     return check_launch("k_dwconv3_pool");
+}
+
+bool gconv_pool_ok(int N, int H, int W, int Cin, int KH, int KW, int Cout, int stride, int pad,
+                   int groups, int pool, int pstride, int ppad, const void* in, const void* w,
+                   const void* out) {
+    if (groups <= 1 || Cin % groups || Cout % groups || stride <= 0) return false;
+    const int Cin_p = Cin / groups, Cout_p = Cout / groups;
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH <= 0 || OW <= 0) return false;
+    const int PH = (OH + 2 * ppad - 3) / 2 + 1, PW = (OW + 2 * ppad - 3) / 2 + 1;
+    return KH == 3 && KW == 3 && (Cin_p == 4 || Cin_p == 8) && Cout_p >= 8 && Cout_p % 4 == 0 &&
+           pool == 3 && pstride == 2 && (ppad == 0 || ppad == 1) && PH > 0 && PW > 0 &&
+           (long long)N * PH * PW * (Cout / 4) < (1ll << 31) &&
+           ((((uintptr_t)in) | ((uintptr_t)w) | ((uintptr_t)out)) & 15u) == 0;
+}
+
+bool gconv_pool_f32(const float* in, int N, int H, int W, int Cin, const float* w,
+                    const float* bias, int Cout, int stride, int pad, int groups, int act, int ppad,
+                    float* out, int post_relu, hipStream_t s) {
+    const int OH = (H + 2 * pad - 3) / stride + 1, OW = (W + 2 * pad - 3) / stride + 1;
+    const int PH = (OH + 2 * ppad - 3) / 2 + 1, PW = (OW + 2 * ppad - 3) / 2 + 1;
+    if (N <= 0 || OH <= 0 || OW <= 0 || PH <= 0 || PW <= 0) return true;
+    const int Cout_p = Cout / groups, Cin_p = Cin / groups;
+    // the conv's and the pool's per-channel rules, as gconv_f32 and maxpool_f32 pick them
+    const int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
+    const int pvec_end = Cout >= 16 ? (Cout & ~15) : (Cout >= 8 ? (Cout & ~7) : 0);
+    // small images: one workgroup per (image, group) with the image in LDS
+    const size_t img_lds = ((size_t)H * W * Cin_p + (size_t)OH * OW * Cout_p) * sizeof(float);
+    if (img_lds <= 48 * 1024 && Cout_p / 4 <= 256 && (long long)N * groups < (1ll << 31)) {
+        const dim3 grid((unsigned)(N * groups));
+        if (Cin_p == 4)
+            ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool_img<1>, grid, dim3(256), img_lds, s, in, H, W, Cin,
+                         w, bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW,
+                         pvec_end, out, post_relu);
+        else
+            ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool_img<2>, grid, dim3(256), img_lds, s, in, H, W, Cin,
+                         w, bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW,
+                         pvec_end, out, post_relu);
+        return check_launch("k_gconv3_pool_img");
+    }
+    const long long total = (long long)N * PH * PW * (Cout / 4);
+    if (Cin_p == 4)
+        ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool<1>, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w,
+                     bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW, pvec_end, out,
+                     post_relu);
+    else
+        ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool<2>, grid1d(total), dim3(256), 0, s, in, N, H, W, Cin, w,
+                     bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW, pvec_end, out,
+                     post_relu);
+    return check_launch("k_gconv3_pool");
 }
 
 bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,

@@ -213,6 +213,16 @@ bool dwconv_pool_ok(int H, int W, int C, int KH, int KW, int stride, int pad, in
 bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w,
                      const float* bias, int stride, int pad, int act, int ppad, float* out,
                      int post_relu, hipStream_t s);
+// Grouped 3x3 conv + activation fused with a following 3x3/2 MaxPool (pool
+// pad 0 or 1, post_relu): gconv_f32 then maxpool_f32, bit for bit, without the
+// conv output in memory (gconv_pool_ok says when it applies: Cin/groups 4 or 8,
+// Cout/groups >= 8 and a multiple of 4, 16-byte aligned buffers).
+bool gconv_pool_ok(int N, int H, int W, int Cin, int KH, int KW, int Cout, int stride, int pad,
+                   int groups, int pool, int pstride, int ppad, const void* in, const void* w,
+                   const void* out);
+bool gconv_pool_f32(const float* in, int N, int H, int W, int Cin, const float* w,
+                    const float* bias, int Cout, int stride, int pad, int groups, int act, int ppad,
+                    float* out, int post_relu, hipStream_t s);
 bool gconv_f32(const float* in, int N, int H, int W, int Cin, const float* w, const float* bias,
                int KH, int KW, int Cout, int stride, int pad, int groups, float* out, int act,
                hipStream_t s);

@@ -229,6 +229,16 @@ int acfun_dev_conv2d_dw_maxpool(const float* input, int N, int H, int W, int C,
                                 const float* weight, const float* bias, int KH, int KW, int stride,
                                 int pad, int act, int pool, int pool_stride, int pool_pad,
                                 float* output, int post_relu, void* stream);
+/* acfun_conv2d_g (ref acfun.h:86-89, act 0/1) followed by acfun_maxpool or
+ * acfun_maxpool_relu (ref acfun.h:105-111, post_relu) on its output: the same
+ * result bit for bit in one pass for 3x3 grouped convs with 4 or 8 input
+ * channels per group and at least 8 (a multiple of 4) output channels per
+ * group, a 3x3 / stride-2 pool with padding 0 or 1 and 16-byte aligned
+ * buffers; other shapes run the conv and the pool.  output: [N, PH, PW, Cout]. */
+int acfun_dev_conv2d_g_maxpool(const float* input, int N, int H, int W, int Cin,
+                               const float* weight, const float* bias, int KH, int KW, int Cout,
+                               int stride, int pad, int groups, int act, int pool, int pool_stride,
+                               int pool_pad, float* output, int post_relu, void* stream);
 int acfun_dev_maxpool(const float* input, int N, int H, int W, int C, int pool, int stride,
                       int pad, float* output, int post_relu, void* stream);
 int acfun_dev_fc(const float* input, int N, int Cin, const float* weight, const float* bias,

@@ -1,7 +1,9 @@
 """GPU parity of the fused pairs through the C ABI: acfun_dev_conv2d_dw_maxpool
 (depthwise conv + activation, then MaxPool, in one kernel) against the
 oracle's depthwise conv followed by its maxpool -- the two reference calls
-(acfun_conv2d_dw, acfun_maxpool(_relu)), both pinned bit-exact in
+(acfun_conv2d_dw, acfun_maxpool(_relu)) -- and acfun_dev_conv2d_g_maxpool
+(grouped conv + activation, then MaxPool) against the oracle's grouped conv
+and maxpool (acfun_conv2d_g, acfun_maxpool(_relu)); all pinned bit-exact in
 tests/test_oracle_pins.py.  Bar: bit-exact, NaN propagation included."""
 import numpy as np
 import pytest
@@ -88,3 +90,61 @@ def test_config4a_fused_full_exact(gpu, rng):
     wf = wf.reshape(C, 3, 3)
     assert_bitexact(run_dwpool(gpu, x, wf, bf, 2, 1, 1, 1, 0),
                     want_dwpool(x, wf, bf, 2, 1, 1, 1, 0), "cfg4a fused")
+
+
+def run_gpool(gpu, x, w, b, Cout, stride, pad, groups, act, ppad, post_relu):
+    import torch
+    N, H, W, Cin = x.shape
+    OH, OW = oracle.out_hw(H, W, 3, 3, stride, pad)
+    PH, PW = oracle.out_hw(OH, OW, 3, 3, 2, ppad)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dx, dw = torch.from_numpy(x).cuda(), torch.from_numpy(np.ascontiguousarray(w)).cuda()
+        db = torch.from_numpy(b).cuda()
+        dy = torch.full((N, PH, PW, Cout), 7.0, device="cuda")
+        rc = gpu.acfun_dev_conv2d_g_maxpool(dx.data_ptr(), N, H, W, Cin, dw.data_ptr(), db.data_ptr(),
+                                            3, 3, Cout, stride, pad, groups, act, 3, 2, ppad,
+                                            dy.data_ptr(), post_relu, s.cuda_stream)
+        out = dy.cpu().numpy()
+    s.synchronize()
+    assert rc == 0, capi.last_error()
+    return out
+
+
+def want_gpool(x, w, b, Cout, stride, pad, groups, act, ppad, post_relu):
+    y = oracle.conv2d_grouped(x, w, b, 3, 3, Cout, stride, pad, groups, act)
+    return oracle.maxpool(y, 3, 2, ppad, post_relu)
+
+
+# (N, H, W, Cin, Cout, groups, stride, pad, act, pool pad, post_relu)
+GCASES = [
+    (32, 14, 14, 24, 48, 6, 1, 1, 1, 1, 0),     # config 4(b)
+    (2, 15, 13, 32, 64, 4, 1, 1, 1, 0, 1),      # 8 input channels per group, pool pad 0
+    (3, 11, 12, 12, 36, 3, 2, 1, 1, 1, 0),      # stride 2, 12 output channels per group
+    (2, 9, 9, 16, 128, 4, 1, 1, 0, 1, 1),       # 32 output channels per group, no activation
+    (1, 10, 10, 12, 12, 3, 1, 1, 1, 1, 0),      # 4 output channels per group: the two-kernel path
+    (1, 60, 58, 16, 64, 2, 1, 1, 1, 1, 1),      # image too large for LDS: one lane per pooled quad
+    (2, 41, 40, 24, 48, 6, 2, 1, 1, 0, 0),      # the same, stride 2, pool pad 0
+]
+
+
+@pytest.mark.parametrize("shape", GCASES)
+def test_g_maxpool_exact(gpu, rng, shape):
+    N, H, W, Cin, Cout, g, st, pd, act, ppad, pr = shape
+    print("gconv+pool case", shape, flush=True)
+    x = rng.standard_normal((N, H, W, Cin)).astype(np.float32)
+    w = (rng.standard_normal((g, 9 * (Cin // g), Cout // g)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.1).astype(np.float32)
+    assert_bitexact(run_gpool(gpu, x, w, b, Cout, st, pd, g, act, ppad, pr),
+                    want_gpool(x, w, b, Cout, st, pd, g, act, ppad, pr), f"gconv+pool {shape}")
+
+
+def test_g_maxpool_nan(gpu, rng):
+    x = rng.standard_normal((1, 12, 12, 24)).astype(np.float32)
+    x[0, 2, 3, 1] = np.nan
+    x[0, 11, 0, 17] = np.nan
+    w = (rng.standard_normal((6, 36, 8)) * 0.3).astype(np.float32)
+    b = np.zeros(48, np.float32)
+    for act, pr in ((0, 0), (1, 1)):
+        assert_bitexact(run_gpool(gpu, x, w, b, 48, 1, 1, 6, act, 1, pr),
+                        want_gpool(x, w, b, 48, 1, 1, 6, act, 1, pr), f"gconv NaN act={act}")
