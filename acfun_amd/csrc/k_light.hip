@@ -262,8 +262,8 @@ __global__ __launch_bounds__(320) void k_dwconv3_pool(const float4* __restrict__
                                                       const float* __restrict__ bias, int pad,
                                                       int OH, int OW, int act, int PP, int PH,
                                                       int PW, int nPHB, int nPWB, int nQG,
-                                                      int nblk, float4* __restrict__ out,
-                                                      int post_relu) {
+                                                      int nblk, int pvec_end,
+                                                      float4* __restrict__ out, int post_relu) {
     __shared__ float4 ys[DWP_ROWS][DWP_COLS][DWP_Q];
     // XCD-ordered work: workgroup i of XCD x (blockIdx.x = 8 i + x) takes item
     // x * per + i, so each XCD runs a contiguous range of items, and the
@@ -353,6 +353,9 @@ __global__ __launch_bounds__(320) void k_dwconv3_pool(const float4* __restrict__
         const int q = tid & 7, pc = (tid >> 3) % DWP_PWB, pr = (tid >> 3) / DWP_PWB;
         const int ph = ph0 + pr, pw = pw0 + pc, c4 = qg * DWP_Q + q;
         if (ph < PH && pw < PW && c4 < C4) {
+            // k_maxpool's per-channel compare: max_ps below pvec_end, else "v > m"
+            const bool pv = 4 * c4 < pvec_end;          // pvec_end is a multiple of 8
+            auto mx = [pv](float a, float v) { return pv ? vmax(a, v) : (v > a ? v : a); };
             float4 m = make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
 #pragma unroll
             for (int kh = 0; kh < 3; ++kh) {
@@ -363,11 +366,12 @@ __global__ __launch_bounds__(320) void k_dwconv3_pool(const float4* __restrict__
                     const int yc = 2 * pw - PP + kw;
                     if ((unsigned)yc >= (unsigned)OW) continue;
                     const float4 v = ys[yr - y0][yc - x0][q];
-                    m.x = vmax(m.x, v.x); m.y = vmax(m.y, v.y); m.z = vmax(m.z, v.z); m.w = vmax(m.w, v.w);
+                    m.x = mx(m.x, v.x); m.y = mx(m.y, v.y); m.z = mx(m.z, v.z); m.w = mx(m.w, v.w);
                 }
             }
             if (post_relu) {
-                m.x = vmax(m.x, 0.f); m.y = vmax(m.y, 0.f); m.z = vmax(m.z, 0.f); m.w = vmax(m.w, 0.f);
+                auto rl = [pv](float a) { return pv ? vmax(a, 0.f) : (a < 0.f ? 0.f : a); };
+                m.x = rl(m.x); m.y = rl(m.y); m.z = rl(m.z); m.w = rl(m.w);
             }
             out[(((size_t)n * PH + ph) * PW + pw) * C4 + c4] = m;
         }
@@ -537,6 +541,148 @@ __global__ __launch_bounds__(256) void k_gconv4_3x3(const float* __restrict__ in
         }
     }
     *(f4*)(out + (((long long)n * OH + oh) * OW + ow) * Cout + co) = s;
+}
+
+// Depthwise 3x3 / stride 2 + activation + 3x3 / stride-2 MaxPool, row-streaming
+// form: a lane owns 4 channels of one pooled column and walks a strip of RP
+// pooled rows down the image.  Per depthwise row y it loads the two new input
+// rows (7 columns: those of depthwise columns 2 pw - pp .. 2 pw - pp + 2), and
+// keeps only running sums: the depthwise accumulators of row y + 1 started
+// from the row the two share, and the maxima of the (at most two) pool rows
+// row y belongs to.  Every value is folded in the reference's order (bias, then
+// one fmaf per in-range tap kh-major; pool taps kh-major, max_ps from -1e30),
+// out-of-range taps skipped by selects, so the result is bit for bit
+// k_dwconv3_blk then k_maxpool3s2_row.  No LDS, no barriers: lanes stream
+// independently, and workgroups are XCD-ordered so the strips that share
+// input rows read them through one L2.
+constexpr int DWR_RP = 4;                               // pooled rows per strip
+__global__ __launch_bounds__(256) void k_dwconv3_pool_rs(
+    const float* __restrict__ in, int H, int W, int C4, const float* __restrict__ w,
+    const float* __restrict__ bias, int pad, int OH, int OW, int act, int PP, int PH, int PW,
+    int nstrip, int items, int in_bytes, int pvec_end, float4* __restrict__ out, int post_relu) {
+    constexpr unsigned kOOB = 0x80000000u;
+    const int per = (int)(gridDim.x >> 3);
+    const int blk = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
+    const int idx = blk * 256 + (int)threadIdx.x;
+    if (idx >= items) return;
+    const int q = idx % C4;
+    int t = idx / C4;
+    const int pw = t % PW;
+    t /= PW;
+    const int st = t % nstrip;
+    const int n = t / nstrip;
+    const int ph0 = st * DWR_RP, ph1 = ph0 + DWR_RP < PH ? ph0 + DWR_RP : PH;
+    const int c = 4 * q;
+    float wk[4][9];
+    {
+        const float4* w4 = (const float4*)(w + (size_t)c * 9);   // 36 floats, 16-byte aligned
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const float4 v = w4[i];
+            wk[(4 * i + 0) / 9][(4 * i + 0) % 9] = v.x;
+            wk[(4 * i + 1) / 9][(4 * i + 1) % 9] = v.y;
+            wk[(4 * i + 2) / 9][(4 * i + 2) % 9] = v.z;
+            wk[(4 * i + 3) / 9][(4 * i + 3) % 9] = v.w;
+        }
+    }
+    const f4 b4 = bias ? f4{bias[c], bias[c + 1], bias[c + 2], bias[c + 3]} : f4{0.f, 0.f, 0.f, 0.f};
+    // depthwise columns x_j = 2 pw - PP + j; their input columns cb + l, l < 7
+    const int x0 = 2 * pw - PP, cb = 2 * x0 - pad;
+    bool xok[3], cok[7];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) xok[j] = (unsigned)(x0 + j) < (unsigned)OW;
+#pragma unroll
+    for (int l = 0; l < 7; ++l) cok[l] = (unsigned)(cb + l) < (unsigned)W;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)in, (short)0, in_bytes, 0x00020000);
+    auto ldrow = [&](int r, f4* v) {                     // input row r, the 7 columns
+        const bool rok = (unsigned)r < (unsigned)H;
+        const int base = ((n * H + r) * W + cb) * C4 + q;
+#pragma unroll
+        for (int l = 0; l < 7; ++l) {
+            const unsigned off = rok && cok[l] ? (unsigned)((base + l * C4) * 16) : kOOB;
+            v[l] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        }
+        return rok;
+    };
+    // acc[j] += row's taps kh of depthwise column j, in kw order (in-range only)
+    auto fold = [&](f4* acc, const f4* v, bool rok, int kh) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const bool ok = rok && cok[2 * j + kw];
+                const f4 x = v[2 * j + kw];
+                const int tp = kh * 3 + kw;
+                acc[j].x = ok ? fmaf(x.x, wk[0][tp], acc[j].x) : acc[j].x;
+                acc[j].y = ok ? fmaf(x.y, wk[1][tp], acc[j].y) : acc[j].y;
+                acc[j].z = ok ? fmaf(x.z, wk[2][tp], acc[j].z) : acc[j].z;
+                acc[j].w = ok ? fmaf(x.w, wk[3][tp], acc[j].w) : acc[j].w;
+            }
+    };
+    // k_maxpool's per-channel compare: max_ps below pvec_end, else "v > m"
+    bool pv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = c + e < pvec_end;
+    auto pmax = [&](f4& m, const f4* d, bool yok) {      // the row's 3 taps, kw order
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const bool ok = yok && xok[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = d[j][e];
+                const float r = pv[e] ? vmax(m[e], v) : (v > m[e] ? v : m[e]);
+                m[e] = ok ? r : m[e];
+            }
+        }
+    };
+    const f4 lo = {-1e30f, -1e30f, -1e30f, -1e30f};
+    // depthwise rows yA .. yB feed pool rows ph0 .. ph1 - 1
+    const int yA = 2 * ph0 - PP, yB = 2 * (ph1 - 1) - PP + 2;
+    f4 part[3], rowa[7], rowb[7];
+    {
+        f4 acc0[3] = {b4, b4, b4};
+        const bool ok0 = ldrow(2 * yA - pad, rowb);
+        fold(acc0, rowb, ok0, 0);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) part[j] = acc0[j];
+    }
+    f4 mA = lo, mB = lo;                                  // pool rows ph, ph + 1
+    int ph = ph0;
+    for (int y = yA; y <= yB; ++y) {
+        const bool oka = ldrow(2 * y - pad + 1, rowa);
+        const bool okb = ldrow(2 * y - pad + 2, rowb);
+        f4 d[3] = {part[0], part[1], part[2]};
+        fold(d, rowa, oka, 1);
+        fold(d, rowb, okb, 2);
+        // the next row's accumulators start from the shared input row
+        part[0] = part[1] = part[2] = b4;
+        fold(part, rowb, okb, 0);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            d[j].x = act_apply(d[j].x, act); d[j].y = act_apply(d[j].y, act);
+            d[j].z = act_apply(d[j].z, act); d[j].w = act_apply(d[j].w, act);
+        }
+        const bool yok = (unsigned)y < (unsigned)OH;
+        // row y is tap kh = y - (2 ph - PP) of pool row ph and, when that is 2,
+        // tap 0 of pool row ph + 1
+        const int kh = y - (2 * ph - PP);
+        pmax(mA, d, yok);
+        if (kh == 2) {
+            pmax(mB, d, yok);
+            if (ph < PH) {
+                f4 m = mA;
+                if (post_relu) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) m[e] = pv[e] ? vmax(m[e], 0.f) : (m[e] < 0.f ? 0.f : m[e]);
+                }
+                out[(((size_t)n * PH + ph) * PW + pw) * C4 + q] = float4{m.x, m.y, m.z, m.w};
+            }
+            mA = mB;
+            mB = lo;
+            ++ph;
+        }
+    }
 }
 
 // Grouped 3x3 conv (Cin_p = 4 CINQ, the all-FMA rule) + activation fused with
@@ -912,15 +1058,29 @@ bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w
         set_error("dwconv_pool: grid too large");
         return false;
     }
+    // maxpool_f32's per-channel rule (max_ps below pvec_end)
+    const int pvec_end = C >= 16 ? (C & ~15) : (C >= 8 ? (C & ~7) : 0);
+    const long long in_bytes = (long long)N * H * W * C * 4;
+    if (stride == 2 && in_bytes < (1ll << 31)) {
+        const int nstrip = (PH + DWR_RP - 1) / DWR_RP;
+        const long long lanes = (long long)N * nstrip * PW * C4;
+        const long long wgs = (lanes + 255) / 256;
+        if (lanes < (1ll << 30)) {
+            ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool_rs, dim3((unsigned)(8 * ((wgs + 7) / 8))), dim3(256),
+                         0, s, in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nstrip, (int)lanes,
+                         (int)in_bytes, pvec_end, (float4*)out, post_relu);
+            return check_launch("k_dwconv3_pool_rs");
+        }
+    }
     const unsigned blocks = (unsigned)(8 * ((items + 7) / 8));   // 8 equal XCD ranges
     if (stride == 1)
         ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<1>, dim3(blocks), dim3(320), 0, s,
                      (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
-                     nPWB, nQG, (int)items, (float4*)out, post_relu);
+                     nPWB, nQG, (int)items, pvec_end, (float4*)out, post_relu);
     else
         ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool<2>, dim3(blocks), dim3(320), 0, s,
                      (const float4*)in, H, W, C4, w, bias, pad, OH, OW, act, ppad, PH, PW, nPHB,
-                     nPWB, nQG, (int)items, (float4*)out, post_relu);
+                     nPWB, nQG, (int)items, pvec_end, (float4*)out, post_relu);
     return check_launch("k_dwconv3_pool");
 }
 

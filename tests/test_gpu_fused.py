@@ -78,6 +78,21 @@ def test_dw_maxpool_nan(gpu, rng):
         assert_bitexact(got, want, f"NaN act={act}")
 
 
+@pytest.mark.parametrize("st", [1, 2])
+def test_dw_maxpool_nan_partial_vec(gpu, rng, st):
+    """C = 20: the pool compares channels 16..19 with the scalar rule (v > m),
+    not max_ps; with NaNs the two differ, and the fused kernels keep both."""
+    x = rng.standard_normal((2, 14, 15, 20)).astype(np.float32)
+    x[0, 3, 4, 17] = np.nan
+    x[1, 7, 8, 18] = np.nan
+    x[0, 9, 9, 2] = np.nan
+    w = (rng.standard_normal((20, 3, 3)) * 0.3).astype(np.float32)
+    b = np.zeros(20, np.float32)
+    for act, pr in ((0, 0), (0, 1)):
+        assert_bitexact(run_dwpool(gpu, x, w, b, st, 1, act, 1, pr),
+                        want_dwpool(x, w, b, st, 1, act, 1, pr), f"C=20 NaN s{st} act={act} pr={pr}")
+
+
 def test_config4a_fused_full_exact(gpu, rng):
     """Config 4(a) at full size: depthwise 3x3/2 (BN folded) + ReLU, then
     MaxPool 3x3/2 pad 1 -- one kernel, bit-exact against the two reference ops."""
