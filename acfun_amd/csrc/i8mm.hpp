@@ -87,20 +87,29 @@ enum { AM_GEN = 0, AM_C128 = 1, AM_C64 = 2 };
 
 __device__ __forceinline__ int i8swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// floor(a / b) for 0 <= a < 2^24, b >= 1 via a float reciprocal, corrected.
+// floor(a / b) for 0 <= a < 2^24, 1 <= b < 2^24 via a float reciprocal, corrected
+// by one step either way; q*b <= a + b < 2^25, so a 24-bit multiply forms it.
 __device__ __forceinline__ int udiv_small(int a, int b, float rb) {
-    int q = (int)((float)a * rb);
-    q -= (q * b > a);
-    q += ((q + 1) * b <= a);
-    return q;
+    const int q = (int)((float)a * rb);
+    const int qb = (int)__umul24((unsigned)q, (unsigned)b);
+    return q - (qb > a) + (qb + b <= a);
+}
+
+// Calls f(std::integral_constant<int, act>) for the wave-uniform activation
+// code (0, 1 or 2), so each epilogue loop is compiled for one fixed form.
+template <class F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+    if (act == 1) f(std::integral_constant<int, 1>{});
+    else if (act == 2) f(std::integral_constant<int, 2>{});
+    else f(std::integral_constant<int, 0>{});
 }
 
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-// LDS of k_i8mm: NST operand stages, then NST slots of the per-channel
+// LDS of k_i8mm: NST operand stages, then NST + 1 slots of the per-channel
 // epilogue parameters of a tile (three arrays of BN words each).
 constexpr size_t i8mm_lds(int BM, int BN, int NST) {
-    return (size_t)NST * (BM + BN) * 128 + (size_t)NST * 3 * BN * 4;
+    return (size_t)NST * (BM + BN) * 128 + (size_t)(NST + 1) * 3 * BN * 4;
 }
 
 template <int BM, int BN, int NST, int AM, int EPI, int OUT>
@@ -147,13 +156,15 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     const __amdgpu_buffer_rsrc_t bres =
         __builtin_amdgcn_make_buffer_rsrc((void*)p.Bt, (short)0, (int)p.b_bytes, 0x00020000);
     // The tile's per-channel epilogue parameters travel by the same LDS DMA as
-    // the operands (issued just before the items of the tile's last chunk, so
-    // the wait for that chunk covers them), into slot (tile index mod NST):
-    // array 0 alpha (or the weight scales), 1 beta (or the bias), 2 the weight
-    // column sums.  A missing array is a zero-length buffer and reads as 0.
-    // No vector load of the loop then has a register result, which would
-    // make the compiler wait for every DMA in flight.
-    constexpr int PSLOT = 3 * BN * 4;
+    // the operands (issued just before the items of the tile's first chunk, so
+    // the wait for any chunk of the tile covers them), into slot (tile index
+    // mod NST + 1): array 0 alpha (or the weight scales), 1 beta (or the
+    // bias), 2 the weight column sums.  A missing array is a zero-length
+    // buffer and reads as 0.  The issue cursor runs at most NST chunks, so at
+    // most NST tiles, ahead of the tile whose epilogue reads its slot: NST + 1
+    // slots keep them apart.  No vector load of the loop then has a register
+    // result, which would make the compiler wait for every DMA in flight.
+    constexpr int PSLOT = 3 * BN * 4, NPS = NST + 1;
     int8_t* const prm = sm8 + NST * STG;
     const float* pa0 = p.alpha ? p.alpha : p.ws;
     const float* pa1 = (EPI == EPI_GEMM && p.alpha) ? p.beta : p.bias;
@@ -193,6 +204,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         return hi > lo ? (1u << hi) - (1u << lo) : 0u;
     };
     int ik = 0;                                       // the issue cursor's tile (index in this workgroup)
+    int ic = 0;                                       // and its chunk in that tile
     int itn = 0;                                      // column block of the issue cursor's tile
     auto setup = [&](int k) {
         const int L = t0 + k * tstr;
@@ -201,21 +213,29 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
 #pragma unroll
         for (int t = 0; t < AIT; ++t) {
             const int m = tm * BM + 8 * (wave + 4 * t) + rl;
+            if (AM != AM_GEN && gemm1) {
+                // pixel m at its only tap (bit 0); past M no tap is in range
+                abase[t] = m < p.M ? m * p.Cinp + (AM == AM_C64 ? 16 * (aq[t] & 3) : 16 * aq[t]) : 0;
+                amask[t] = m < p.M ? 1 : 0;
+                continue;
+            }
             int pix = 0, ih0 = -(1 << 28), iw0 = 0;
             if (m < p.M) {
                 if (gemm1) {
                     pix = m;
                     ih0 = iw0 = 0;
                 } else {
-                    int n, oh;
-                    if (small_m) {
+                    int n, oh, ow;
+                    if (small_m) {            // (products below m < 2^24: 24-bit multiplies)
                         n = udiv_small(m, ohw, rohw);
-                        oh = udiv_small(m - n * ohw, p.OW, row_);
+                        const int rem = m - __mul24(n, ohw);
+                        oh = udiv_small(rem, p.OW, row_);
+                        ow = rem - __mul24(oh, p.OW);
                     } else {
                         n = m / ohw;
                         oh = (m - n * ohw) / p.OW;
+                        ow = m - n * ohw - oh * p.OW;
                     }
-                    const int ow = m - n * ohw - oh * p.OW;
                     pix = n * p.H * p.W;
                     ih0 = oh * p.stride - p.pad;
                     iw0 = ow * p.stride - p.pad;
@@ -244,24 +264,30 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         }
     };
     // issue-side per-chunk state (wave-uniform): fast modes track the tap of
-    // the chunk's first quad (kh, kw) and its channel offset ic0
-    int ikh = 0, ikw = 0, iic = 0;
+    // the chunk's first quad (kh, kw) and its channel offset ic0; AM_C128 also
+    // keeps the chunk's byte offset from the tap-(0, 0) pixel and its mask bit
+    int ikh = 0, ikw = 0, iic = 0, aoff = 0, abit = 0;
+    int islot = 0;                                    // parameter slot of the issue cursor's tile
     const float rcinp = 1.0f / (float)p.Cinp, rkw = 1.0f / (float)p.KW;
     const int taps = p.K / p.Cinp;
     auto tap_off = [&](int kh, int kw) { return (kh * p.W + kw) * p.Cinp; };
-    auto issue = [&](int t, int c, int8_t* st) {      // DMA item t of chunk c into stage st
-        if (t == 0 && c == nch - 1 && wave < 3) {     // the tile's epilogue parameters
-            if (lane < BN / 4) {
-                const unsigned off = (unsigned)((itn * BN + 4 * lane) * 4);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    prs, (lds_void*)(prm + (ik % NST) * PSLOT + wave * BN * 4), 16, off, 0, 0, 0);
-            }
+    auto issue_params = [&]() {                       // the issue cursor's tile's epilogue parameters
+        if (wave < 3 && lane < BN / 4) {
+            const unsigned off = (unsigned)((itn * BN + 4 * lane) * 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                prs, (lds_void*)(prm + islot * PSLOT + wave * BN * 4), 16, off, 0, 0, 0);
         }
+    };
+    // DMA item t of chunk c into stage st.  A chunk past the end (live false)
+    // is issued all out of range: it writes zeros to a stage no chunk reads
+    // again and keeps the number of loads per iteration fixed, so every wait
+    // of the loop is the same.
+    auto issue = [&](int t, int c, int8_t* st, bool live) {
         if (t < AIT) {
             unsigned v = kOOB;
             if (AM == AM_GEN) {
                 const int k = (c << 7) + 16 * aq[t];
-                if (k < p.K) {
+                if (live && k < p.K) {
                     const int tap = udiv_small(k, p.Cinp, rcinp);
                     const int ic = k - tap * p.Cinp;
                     const int kh = udiv_small(tap, p.KW, rkw);
@@ -271,8 +297,8 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                         v = (unsigned)((apix[t] + ih * p.W + iw) * p.Cinp + ic);
                 }
             } else if (AM == AM_C128) {
-                const bool ok = (amask[t] >> (ikh * 8 + ikw)) & 1;
-                v = ok ? (unsigned)(abase[t] + tap_off(ikh, ikw) + iic) : kOOB;
+                const bool ok = live && ((amask[t] >> abit) & 1);
+                v = ok ? (unsigned)(abase[t] + aoff) : kOOB;
             } else {
                 // two taps per chunk: quads 0-3 at (ikh, ikw), quads 4-7 at the next tap
                 int kh = ikh, kw = ikw + 1;
@@ -280,7 +306,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                 const bool second = aq[t] >= 4;
                 const bool inK = !second || (2 * c + 1 < taps);
                 const int th = second ? kh : ikh, tw = second ? kw : ikw;
-                const bool ok = inK && ((amask[t] >> (th * 8 + tw)) & 1);
+                const bool ok = live && inK && ((amask[t] >> (th * 8 + tw)) & 1);
                 v = ok ? (unsigned)(abase[t] + tap_off(th, tw)) : kOOB;
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -289,18 +315,35 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
             const int tt = t - AIT;
             // (a local, not the captured array element, as the builtin's operand:
             // with the latter clang drops the kernel's host-side stub)
-            const unsigned v = bv[tt] + (unsigned)(c << 7);
+            const unsigned v = live ? bv[tt] + (unsigned)(c << 7) : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 bres, (lds_void*)(st + SA + (wave + 4 * tt) * 1024), 16, v, 0, 0, 0);
         }
     };
-    auto advance = [&]() {                             // the issue cursor's next chunk
+    // the issue cursor's next chunk; at the end of a tile, the next tile (its
+    // rows, then its parameters)
+    auto advance = [&]() {
         if (AM == AM_C128) {
             iic += 128;
-            if (iic == p.Cinp) { iic = 0; if (++ikw == p.KW) { ikw = 0; ++ikh; } }
+            aoff += 128;
+            if (iic == p.Cinp) {
+                iic = 0;
+                if (++ikw == p.KW) { ikw = 0; ++ikh; }
+                aoff = tap_off(ikh, ikw);
+                abit = ikh * 8 + ikw;
+            }
         } else if (AM == AM_C64) {
             ikw += 2;
             while (ikw >= p.KW) { ikw -= p.KW; ++ikh; }
+        }
+        if (++ic == nch) {
+            ic = 0;
+            ikh = ikw = iic = aoff = abit = 0;
+            if (++ik < cnt) {
+                setup(ik);
+                islot = islot == NPS - 1 ? 0 : islot + 1;
+                issue_params();
+            }
         }
     };
 
@@ -341,20 +384,16 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     }
 
     // ---- prologue: the first AHEAD chunks of the item stream (tile, chunk)
-    int ic = 0;                                 // issue cursor: chunk of tile ik
-    if (nit > 0) setup(0);
+    if (nit > 0) {
+        setup(0);
+        issue_params();
+    }
 #pragma unroll
     for (int a = 0; a < AHEAD; ++a) {
-        if (a < nit) {
+        const bool live = a < nit;
 #pragma unroll
-            for (int t = 0; t < ITEMS; ++t) issue(t, ic, sm8 + a * STG);
-            advance();
-            if (++ic == nch) {
-                ic = 0;
-                ikh = ikw = iic = 0;
-                if (++ik < cnt) setup(ik);
-            }
-        }
+        for (int t = 0; t < ITEMS; ++t) issue(t, ic, sm8 + a * STG, live);
+        if (live) advance();
     }
 
     const float sa = p.s_in ? p.s_in[0] : (p.scal ? p.scal[1] : 0.0f);
@@ -387,20 +426,18 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         reduce_qparts();
     }
-    int st = 0, ck = 0, cc = 0;                 // compute cursor
+    int st = 0, ck = 0, cc = 0, cslot = 0;     // compute cursor
     float amx = 0.0f;                           // max|stored value| of this lane
     for (int g = 0; g < nit; ++g) {
-        // Chunk g.  Loads (DMA and parameters) complete in issue order, so the
-        // chunks issued after it may stay in flight.  A previous tile's
-        // epilogue stores may sit in the counter's queue after some of those
-        // loads: a wait that leaves only the later chunks' loads outstanding
-        // still proves chunk g landed (a store completing early cannot stand
-        // in for an older load, since the loads complete in order).  The
-        // stores are inline asm, so the compiler's own waits see loads only.
-        const int later = nit - 1 - g < AHEAD - 1 ? nit - 1 - g : AHEAD - 1;
-        if (later <= 0) __builtin_amdgcn_s_waitcnt(vmcnt_enc(0));
-        else if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * ITEMS));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_enc(ITEMS));
+        // Chunk g.  Every iteration issues ITEMS loads (chunk g + AHEAD, real or
+        // out of range), so the AHEAD - 1 chunks issued after chunk g account
+        // for (AHEAD - 1) * ITEMS loads, plus at most a parameter load or the
+        // stores of an epilogue queued after them.  Loads complete in issue
+        // order, so leaving that many outstanding proves chunk g (and all
+        // parameters issued before it) landed; anything extra queued after
+        // chunk g only makes the wait longer.  The stores are inline asm, so
+        // the compiler's own waits see loads only.
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc((AHEAD - 1) * ITEMS));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         // (before this iteration's DMA reuses the stage the partials came into)
         if (OUT == OUT_Q8 && g == 0) reduce_qparts();
@@ -429,19 +466,10 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
-            if (more) {
 #pragma unroll
-                for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, ic, NA);
-            }
+            for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, ic, NA, more);
         }
-        if (more) {
-            advance();
-            if (++ic == nch) {
-                ic = 0;
-                ikh = ikw = iic = 0;
-                if (++ik < cnt) setup(ik);
-            }
-        }
+        if (more) advance();
         st = st == NST - 1 ? 0 : st + 1;
         if (++cc < nch) continue;
         // ---- epilogue of tile ck: lane l, register e of block (i, j) <->
@@ -450,7 +478,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         float pv0[FN], pv1[FN];
         int pv2[FN];
         {
-            const int8_t* ps = prm + (ck % NST) * PSLOT;
+            const int8_t* ps = prm + cslot * PSLOT;
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const int col = wn * (BN / 2) + 32 * j + r32;
@@ -479,37 +507,46 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                 al[j] = p.alpha ? pv0[j] : __fmul_rn(__fmul_rn(sa, 0.25f), pv0[j]);
                 be[j] = pv1[j];
             }
+            // An all-zero input gives 0 without the bias (src/conv_int8.cpp:78).
+            // Zero factors give exactly +0 below: the product of a finite value
+            // and 0 is a signed zero, and adding +0 to it gives +0.
+            al[j] = zero ? 0.0f : al[j];
+            be[j] = zero ? 0.0f : be[j];
         }
         // The route's formula on one accumulator.  GEMM routes: fl(fl(acc_u *
         // alpha) + beta); Winograd route: fmaf(4*acc_s, alpha_w, bias), with
-        // (float)(4a) = 4*(float)a exactly.  An all-zero input gives 0 without
-        // the bias (src/conv_int8.cpp:78).
+        // (float)(4a) = 4*(float)a exactly.
         auto epi = [&](int a, int j) -> float {
-            float u;
             if (EPI == EPI_GEMM)
-                u = __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr[j]), al[j]), be[j]);
-            else
-                u = fmaf(4.0f * (float)a, al[j], be[j]);
-            return zero ? 0.0f : u;
+                return __fadd_rn(__fmul_rn((float)(int)((unsigned)a + (unsigned)corr[j]), al[j]), be[j]);
+            return fmaf(4.0f * (float)a, al[j], be[j]);
         };
         // Lane l, register e of block (i, j) <-> row m0 + wm*BM/2 + 32i + 8(e/4) +
         // 4(l/32) + e%4, column n0 + wn*BN/2 + 32j + l%32.
         const int mb = m0 + wm * (BM / 2) + 4 * hq, nb = n0 + wn * (BN / 2) + r32;
         if (OUT == OUT_AMAX) {
-            // first pass of a requantized output: the tile's max|v|, nothing stored
+            // first pass of a requantized output: the tile's max|v|, nothing stored;
+            // one loop per activation form and per full or edge tile
+            with_act(p.act, [&](auto actc) {
+                constexpr int ACT = decltype(actc)::value;
+                auto tile_max = [&](auto fullc) {
+                    constexpr bool FULL = decltype(fullc)::value;
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+                    for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
+                        for (int i = 0; i < FM; ++i)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3), n = nb + 32 * j;
-                        const float v = act_select(epi(acc[i][j][e], j), relu1, relu2);
-                        acc[i][j][e] = 0;
-                        // (a select, not a branch per element)
-                        const float av = (full || (m < p.M && n < p.N)) ? fabsf(v) : 0.0f;
-                        amx = av > amx ? av : amx;           // NaN never wins
-                    }
+                            for (int e = 0; e < 16; ++e) {
+                                const int m = mb + 32 * i + 8 * (e >> 2) + (e & 3), n = nb + 32 * j;
+                                const float v = act_apply(epi(acc[i][j][e], j), ACT);
+                                acc[i][j][e] = 0;
+                                const float av = (FULL || (m < p.M && n < p.N)) ? fabsf(v) : 0.0f;
+                                amx = av > amx ? av : amx;           // NaN never wins
+                            }
+                };
+                if (full) tile_max(std::true_type{});
+                else tile_max(std::false_type{});
+            });
         } else if (STAGED) {
             // (1) every wave is done reading the last chunk's stage; (2) each wave
             // writes its 32 x 32 block of pre-activation values there, row-major,
@@ -526,71 +563,100 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
             }
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (OUT == OUT_F32) {
-                // thread t: quad t%16 of rows t/16 + 16i
+                // thread t: quad t%16 of rows t/16 + 16i; one loop per activation
+                // form, with or without the workgroup maximum (I8M::amax)
                 const int q = tid & 15;
+                const bool fast = full && p.vec;
+                auto rows = [&](auto actc, auto trackc, auto fastc) {
+                    constexpr int ACT = decltype(actc)::value;
+                    constexpr bool TRACK = decltype(trackc)::value, FAST = decltype(fastc)::value;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = (tid >> 4) + 16 * i;
-                    const int m = m0 + r, n = n0 + 4 * q;
-                    f4v v = *(const f4v*)&stg[sidx(r, 4 * q)];
-                    float* dst = p.Cf + (long long)m * p.ldc + n;
-                    if (p.vec && m < p.M && n + 4 <= p.N) {
-                        if (p.res) {
-                            const f4v rv = *(const f4v*)(p.res + (long long)m * p.ldr + n);
-                            v = v + rv;          // fl(v + res) per lane, as a separate Add
-                        }
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = (tid >> 4) + 16 * i;
+                        const int m = m0 + r, n = n0 + 4 * q;
+                        f4v v = *(const f4v*)&stg[sidx(r, 4 * q)];
+                        float* dst = p.Cf + (long long)m * p.ldc + n;
+                        if (FAST || (p.vec && m < p.M && n + 4 <= p.N)) {
+                            if (p.res) {
+                                const f4v rv = *(const f4v*)(p.res + (long long)m * p.ldr + n);
+                                v = v + rv;          // fl(v + res) per lane, as a separate Add
+                            }
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            v[k] = act_select(v[k], relu1, relu2);
-                            const float av = fabsf(v[k]);
-                            amx = av > amx ? av : amx;
-                        }
-                        // s_nop: a VALU write to the data registers of a store of
-                        // more than 8 bytes needs a wait state after it
-                        asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(dst), "v"(v)
-                                     : "memory");
-                    } else if (m < p.M) {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            if (n + k >= p.N) continue;
-                            float w = v[k];
-                            if (p.res) w = __fadd_rn(w, p.res[(long long)m * p.ldr + n + k]);
-                            w = act_select(w, relu1, relu2);
-                            const float av = fabsf(w);
-                            amx = av > amx ? av : amx;
-                            asm volatile("global_store_dword %0, %1, off" ::"v"(dst + k), "v"(w)
+                            for (int k = 0; k < 4; ++k) {
+                                v[k] = act_apply(v[k], ACT);
+                                if (TRACK) {
+                                    const float av = fabsf(v[k]);
+                                    amx = av > amx ? av : amx;
+                                }
+                            }
+                            // s_nop: a VALU write to the data registers of a store of
+                            // more than 8 bytes needs a wait state after it
+                            asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(dst), "v"(v)
                                          : "memory");
+                        } else if (!FAST && m < p.M) {
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                if (n + k >= p.N) continue;
+                                float w = v[k];
+                                if (p.res) w = __fadd_rn(w, p.res[(long long)m * p.ldr + n + k]);
+                                w = act_apply(w, ACT);
+                                if (TRACK) {
+                                    const float av = fabsf(w);
+                                    amx = av > amx ? av : amx;
+                                }
+                                asm volatile("global_store_dword %0, %1, off" ::"v"(dst + k), "v"(w)
+                                             : "memory");
+                            }
                         }
                     }
-                }
+                };
+                // (full tiles with 16-byte rows: no bounds test per quad)
+                with_act(p.act, [&](auto actc) {
+                    if (fast) {
+                        if (p.amax) rows(actc, std::true_type{}, std::true_type{});
+                        else rows(actc, std::false_type{}, std::true_type{});
+                    } else {
+                        if (p.amax) rows(actc, std::true_type{}, std::false_type{});
+                        else rows(actc, std::false_type{}, std::false_type{});
+                    }
+                });
             } else {
                 // OUT_Q8: thread t: 16 columns 16*(t%4).. of row t/4, one 16-byte store;
                 // columns N..ldq-1 (the channel padding of the s8 layout) are 0
                 const int r = tid >> 2, c0 = 16 * (tid & 3);
                 const int m = m0 + r, n = n0 + c0;
                 if (m < p.M && n < p.ldq) {
-                    // straight-line per element: all three rounding forms are
-                    // formed and selected (rule 0: RNE; rule 1: the add-then-
-                    // truncate rule below N & ~15, lroundf's half-away above),
-                    // then clamped; padding columns and an all-zero output give 0
-                    const int cvec = p.N & ~15;
-                    const bool rne = p.rule == 0;
+                    // Rounding form 0: RNE (rule 0).  Rule 1 (the Winograd route's
+                    // input rule): add-then-truncate below N & ~15 (form 1), lroundf's
+                    // half-away above (form 2); a thread's 16 columns start at a
+                    // multiple of 16, so they share one form.  Then the clamp; padding
+                    // columns and an all-zero output give 0.
+                    const int form = p.rule == 0 ? 0 : (n < (p.N & ~15) ? 1 : 2);
                     unsigned w4[4] = {0u, 0u, 0u, 0u};
+                    auto quant = [&](auto actc, auto formc) {
+                        constexpr int ACT = decltype(actc)::value, FORM = decltype(formc)::value;
 #pragma unroll
-                    for (int k4 = 0; k4 < 4; ++k4) {
-                        const f4v v = *(const f4v*)&stg[sidx(r, c0 + 4 * k4)];
+                        for (int k4 = 0; k4 < 4; ++k4) {
+                            const f4v v = *(const f4v*)&stg[sidx(r, c0 + 4 * k4)];
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const int c = n + 4 * k4 + k;
-                            const float t = __fmul_rn(act_select(v[k], relu1, relu2), qinv);
-                            const float r_even = rintf(t);
-                            const float r_away = roundf(t);
-                            const float r_add = truncf(__fadd_rn(t, copysignf(0.5f, t)));
-                            float rq = rne ? r_even : (c < cvec ? r_add : r_away);
-                            rq = fminf(fmaxf(rq, -128.0f), 127.0f);
-                            const int qv = (c < p.N && !qzero) ? (int)rq : 0;
-                            w4[k4] |= ((unsigned)qv & 0xffu) << (8 * k);
+                            for (int k = 0; k < 4; ++k) {
+                                const int c = n + 4 * k4 + k;
+                                const float t = __fmul_rn(act_apply(v[k], ACT), qinv);
+                                float rq = FORM == 0 ? rintf(t)
+                                         : FORM == 1 ? truncf(__fadd_rn(t, copysignf(0.5f, t)))
+                                                     : roundf(t);
+                                rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+                                const int qv = c < p.N ? (int)rq : 0;
+                                w4[k4] |= ((unsigned)qv & 0xffu) << (8 * k);
+                            }
                         }
+                    };
+                    if (!qzero) {
+                        with_act(p.act, [&](auto actc) {
+                            if (form == 0) quant(actc, std::integral_constant<int, 0>{});
+                            else if (form == 1) quant(actc, std::integral_constant<int, 1>{});
+                            else quant(actc, std::integral_constant<int, 2>{});
+                        });
                     }
                     const i4 pk = {(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
                     int8_t* dq = p.Cq + (long long)m * p.ldq + n;
@@ -645,6 +711,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
         }
         cc = 0;
         ++ck;
+        cslot = cslot == NPS - 1 ? 0 : cslot + 1;
     }
     // this workgroup's max|v| of the output tensor, a partial of the next
     // layer's absmax (the reference's max|x| of its input, src/conv_int8.cpp:77)

@@ -619,7 +619,7 @@ def main():
         del xs, zs
         configs["cfg4a_dw_bn_relu_pool"] = {
             "ms": round(t, 5), "ms_cold": round(tc, 5),
-            "roofline": roofline("hbm", c["bytes"], k["k_dwconv_pool"], "k_dwconv3_pool<2>",
+            "roofline": roofline("hbm", c["bytes"], k["k_dwconv_pool"], "k_dwconv3_pool_rs",
                                  "163.8 MB per launch: the input read and the pooled output written "
                                  "once (section 8(d), fused)", "k_dwconv_pool_cfg4a"),
             "frac_hbm_cold_step": round(c["bytes"] / (tc * 1e-3) / PEAK_HBM, 4)}
