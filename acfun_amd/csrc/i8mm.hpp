@@ -73,7 +73,22 @@ struct I8M {
     const float* qparts;
     int nqparts;
     float* s_out;        // max/127 (0: all-zero output), written by workgroup 0
+    // set by i8mm_prepare: the grid in tiles (gm, gn above) and the float
+    // reciprocals of the divisors of the pixel and tap decode
+    float r_ohw, r_ow, r_cinp, r_kw;
 };
+
+// Fills the launch-derived fields of p for BM x BN tiles.  The reciprocals are
+// correctly rounded (host division), which udiv_small's one-step correction
+// relies on.
+inline void i8mm_prepare(I8M& p, int BM, int BN) {
+    p.gm = (p.M + BM - 1) / BM;
+    p.gn = (p.N + BN - 1) / BN;
+    p.r_ohw = 1.0f / (float)(p.OH * p.OW > 0 ? p.OH * p.OW : 1);
+    p.r_ow = 1.0f / (float)(p.OW > 0 ? p.OW : 1);
+    p.r_cinp = 1.0f / (float)(p.Cinp > 0 ? p.Cinp : 1);
+    p.r_kw = 1.0f / (float)(p.KW > 0 ? p.KW : 1);
+}
 
 // Output modes of k_i8mm: fp32 (the reference's float output), the maximum
 // |value| only (first pass of a requantized output), s8 requantized (second pass).
@@ -196,7 +211,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                        p.OW == p.W;
     const bool small_m = p.M < (1 << 24);
     const int ohw = p.OH * p.OW;
-    const float rohw = 1.0f / (float)ohw, row_ = 1.0f / (float)p.OW;
+    const float rohw = p.r_ohw, row_ = p.r_ow;
     // bits [lo, hi) of 8
     auto span8 = [](int lo, int hi) -> unsigned {
         lo = lo > 0 ? lo : 0;
@@ -268,7 +283,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
     // keeps the chunk's byte offset from the tap-(0, 0) pixel and its mask bit
     int ikh = 0, ikw = 0, iic = 0, aoff = 0, abit = 0;
     int islot = 0;                                    // parameter slot of the issue cursor's tile
-    const float rcinp = 1.0f / (float)p.Cinp, rkw = 1.0f / (float)p.KW;
+    const float rcinp = p.r_cinp, rkw = p.r_kw;
     const int taps = p.K / p.Cinp;
     auto tap_off = [&](int kh, int kw) { return (kh * p.W + kw) * p.Cinp; };
     auto issue_params = [&]() {                       // the issue cursor's tile's epilogue parameters

@@ -19,8 +19,7 @@ bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
         (void)hipFuncSetAttribute((const void*)k_i8mm<BM, BN, NST, AM, EPI, OUT_F32>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
-    p.gm = (p.M + BM - 1) / BM;
-    p.gn = (p.N + BN - 1) / BN;
+    i8mm_prepare(p, BM, BN);
     dim3 grid((unsigned)i8mm_grid(p, t));
     ACFUN_LAUNCH("k_i8mm", (k_i8mm<BM, BN, NST, AM, EPI, OUT_F32>), grid, dim3(256), lds, s, p);
     return check_launch("k_i8mm");

@@ -17,8 +17,7 @@ bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
         (void)hipFuncSetAttribute((const void*)k_i8mm<64, 64, NST, AM, EPI, OUT>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
-    p.gm = (p.M + 63) / 64;
-    p.gn = (p.N + 63) / 64;
+    i8mm_prepare(p, 64, 64);
     dim3 grid((unsigned)i8mm_grid(p, t));
     if (OUT == OUT_AMAX)
         ACFUN_LAUNCH("k_i8mm_amax", (k_i8mm<64, 64, NST, AM, EPI, OUT>), grid, dim3(256), lds, s, p);
