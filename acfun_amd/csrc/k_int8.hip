@@ -592,13 +592,13 @@ I8Tile pick_i8mm_tile(int M, int N, int K) {
         t = ft;
     } else {
         // Measured on configs 3a/3b and the ResNet-50 int8 model: 64 x 64 tiles
-        // in three persistent workgroups per CU (each runs its tiles back to
-        // back, the next tile's chunks loading during the current one's)
-        // beat larger tiles and one tile per workgroup: the short K loops
-        // leave a one-tile workgroup too little work to cover its launch,
-        // its first loads and its epilogue.
-        (void)M; (void)N;
-        t = I8Tile{64, 64, (K + 127) / 128 > 2 ? 3 : 2, 0};
+        // with three stages in three persistent workgroups per CU (each runs
+        // its tiles back to back, the next tile's chunks loading during the
+        // current one's) beat larger tiles, two stages and one tile per
+        // workgroup: the short K loops leave a one-tile workgroup too little
+        // work to cover its launch, its first loads and its epilogue.
+        (void)M; (void)N; (void)K;
+        t = I8Tile{64, 64, 3, 0};
     }
     t.per_cu = grid_cap;
     return t;
