@@ -657,9 +657,12 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                             for (int k = 0; k < 4; ++k) {
                                 const int c = n + 4 * k4 + k;
                                 const float t = __fmul_rn(act_apply(v[k], ACT), qinv);
+                                // (|t| <= 127 up to rounding: the reference's conversions
+                                // differ from a float clamp only at NaN, which the RNE and
+                                // add-then-truncate forms send to -128, lroundf to 0)
                                 float rq = FORM == 0 ? rintf(t)
                                          : FORM == 1 ? truncf(__fadd_rn(t, copysignf(0.5f, t)))
-                                                     : roundf(t);
+                                                     : (t != t ? 0.0f : roundf(t));
                                 rq = fminf(fmaxf(rq, -128.0f), 127.0f);
                                 const int qv = c < p.N ? (int)rq : 0;
                                 w4[k4] |= ((unsigned)qv & 0xffu) << (8 * k);

@@ -360,12 +360,10 @@ __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, lo
                 if (c < Cin) {
                     const float t = __fmul_rn(v[k], inv_s);
                     int r;
-                    if (mode == 0) r = (int)rintf(t);
-                    else if (c < cvec) r = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
-                    else r = (int)roundf(t);
-                    int u = r + 128;
-                    u = u < 0 ? 0 : (u > 255 ? 255 : u);
-                    out = u - 128;
+                    if (mode == 0) r = x86_cvt(rintf(t));
+                    else if (c < cvec) r = x86_cvt(truncf(__fadd_rn(t, copysignf(0.5f, t))));
+                    else r = x86_lround(t);
+                    out = x86_u8(r, 128) - 128;
                 }
                 w[k >> 2] |= ((unsigned)out & 0xffu) << (8 * (k & 3));
             }
@@ -418,12 +416,10 @@ __global__ void k_quant_act(const float* __restrict__ x, long long pix, int Cin,
     if (c < Cin && scal[2] == 0.0f) {
         float t = __fmul_rn(x[p * Cin + c], scal[0]);
         int r;
-        if (mode == 0) r = (int)rintf(t);
-        else if (c < cvec) r = (int)truncf(__fadd_rn(t, copysignf(0.5f, t)));
-        else r = (int)roundf(t);
-        int v = r + 128;
-        v = v < 0 ? 0 : (v > 255 ? 255 : v);
-        out = (int8_t)(v - 128);
+        if (mode == 0) r = x86_cvt(rintf(t));
+        else if (c < cvec) r = x86_cvt(truncf(__fadd_rn(t, copysignf(0.5f, t))));
+        else r = x86_lround(t);
+        out = (int8_t)(x86_u8(r, 128) - 128);
     }
     q[i] = out;
 }
@@ -438,10 +434,8 @@ __global__ void k_quant_act_inv(const float* __restrict__ x, long long pix, int 
     int8_t out = 0;
     if (c < Cin) {
         float t = __fmul_rn(x[p * Cin + c], inv_s);
-        int r = (c < cvec) ? (int)truncf(__fadd_rn(t, copysignf(0.5f, t))) : (int)roundf(t);
-        int v = r + 128;
-        v = v < 0 ? 0 : (v > 255 ? 255 : v);
-        out = (int8_t)(v - 128);
+        int r = (c < cvec) ? x86_cvt(truncf(__fadd_rn(t, copysignf(0.5f, t)))) : x86_lround(t);
+        out = (int8_t)(x86_u8(r, 128) - 128);
     }
     q[i] = out;
 }
@@ -519,8 +513,9 @@ __global__ void k_quant_weights(const float* __restrict__ w, int K, int N, float
     if (s <= 0.0f) s = 1.0f;
     sc[j] = s;
     for (int k = 0; k < K; ++k) {
-        float r = roundf(w[(long long)k * N + j] / s);
-        int v = r > 127.0f ? 127 : (r < -128.0f ? -128 : (int)r);
+        // ((int)lroundf, then the clamp: |w / s| <= 127 apart from NaN, which gives 0)
+        int v = x86_lround(w[(long long)k * N + j] / s);
+        v = v > 127 ? 127 : (v < -128 ? -128 : v);
         wq[(long long)k * N + j] = (int8_t)v;
     }
 }
@@ -531,8 +526,7 @@ __global__ void k_quant_u8(const float* __restrict__ x, uint8_t* __restrict__ ou
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float t = __fmul_rn(x[i], inv_s);
-    int v = (int)rintf(t) + zp;
-    out[i] = (uint8_t)(v < 0 ? 0 : (v > 255 ? 255 : v));
+    out[i] = (uint8_t)x86_u8(x86_cvt(rintf(t)), zp);
 }
 
 inline dim3 g1(long long n) { return dim3((unsigned)((n + 255) / 256)); }

@@ -787,7 +787,11 @@ __global__ __launch_bounds__(256) void k_gconv3_pool_img(
     int post_relu) {
     constexpr int CP = 4 * CINQ;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    const int n = blockIdx.x / groups, g = blockIdx.x - n * groups;
+    // workgroup -> (image, group), XCD-ordered (workgroup id mod 8 picks the XCD):
+    // the groups of one image share its pixels' cache lines, so they run on one L2
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    const int L = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+    const int n = L / groups, g = L - n * groups;
     const int Cout_p = Cout / groups, nq = Cout_p >> 2;
     f4* const xs = (f4*)lds;                               // [H*W][CINQ]
     f4* const ys = xs + H * W * CINQ;                      // [OH*OW][nq]

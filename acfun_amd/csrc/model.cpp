@@ -118,7 +118,7 @@ void quantize_cols(const std::vector<float>& w, int K, int N, std::vector<float>
         if (s <= 0.0f) s = 1.0f;
         sc[j] = s;
         for (int k = 0; k < K; ++k) {
-            long v = std::lroundf(w[(size_t)k * N + j] / s);
+            int v = (int)std::lroundf(w[(size_t)k * N + j] / s);   // int first, as the reference
             if (v > 127) v = 127;
             else if (v < -128) v = -128;
             q[(size_t)k * N + j] = (int8_t)v;

@@ -57,6 +57,29 @@ __device__ __forceinline__ float act_select(float v, bool relu1, bool relu2) {
     return relu1 ? r1 : r;
 }
 
+// ----------------------------------------------------------------- quantization
+// The reference's float -> int conversions as its x86 code performs them, so
+// that the GPU quantizers agree on every input, NaN included:
+// _mm512_cvtps_epi32 / _mm512_cvttps_epi32 (src/int8_quantize_avx512.cpp:15-20,
+// src/winograd_int8.cpp:306-319) give the integer indefinite INT_MIN for NaN
+// and for |x| >= 2^31; (int)std::lroundf (src/int8_quantize.cpp:33,
+// src/winograd_int8.cpp:322) keeps the low 32 bits of glibc's long result,
+// which is LONG_MIN (low bits 0) for NaN and |x| >= 2^63.
+// x86_cvt(r) takes an already rounded float (rintf / truncf of the value).
+__device__ __forceinline__ int x86_cvt(float r) {
+    return (r != r || fabsf(r) >= 2147483648.0f) ? (int)0x80000000 : (int)r;
+}
+__device__ __forceinline__ int x86_lround(float t) {
+    if (!(fabsf(t) < 9.2233720368547758e18f)) return 0;
+    if (fabsf(t) < 2147483648.0f) return (int)roundf(t);
+    return (int)(unsigned)(unsigned long long)(long long)t;   // integral here: the low 32 bits
+}
+// clamp(r + zp, 0, 255) with the reference's wrapping 32-bit add (_mm512_add_epi32)
+__device__ __forceinline__ int x86_u8(int r, int zp) {
+    const int v = (int)((unsigned)r + (unsigned)zp);
+    return v < 0 ? 0 : (v > 255 ? 255 : v);
+}
+
 // ----------------------------------------------------------------- device
 // Initializes the current device once (verifies it is gfx950, creates the
 // library stream).  Returns false (and sets the error) when no usable GPU.

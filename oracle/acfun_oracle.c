@@ -389,7 +389,7 @@ EXPORT void oracle_quantize_weights(const float* w, int K, int N, float* scales,
         if (s <= 0.0f) s = 1.0f;
         scales[j] = s;
         for (int k = 0; k < K; ++k) {
-            long v = lroundf(w[(size_t)k * N + j] / s);
+            int v = (int)lroundf(w[(size_t)k * N + j] / s);    /* as the reference: int first */
             if (v > 127) v = 127; else if (v < -128) v = -128;
             wq[(size_t)k * N + j] = (int8_t)v;
         }

@@ -65,6 +65,23 @@ def test_conv2d_int8_q_exact(gpu, rng, shape, act, rule):
     assert np.max(np.abs(got.astype(np.int32))) == 127      # the max maps to +-127
 
 
+@pytest.mark.parametrize("shape", [(2, 9, 9, 20, 3, 3, 19, 1, 1), (2, 14, 14, 32, 1, 1, 40, 1, 0)])
+@pytest.mark.parametrize("rule", [0, 1])
+def test_conv2d_int8_q_nan_outputs(gpu, rng, shape, rule):
+    """NaN biases (no activation) make whole output channels NaN: the output
+    maximum skips them, and the requantization converts them as the reference's
+    x86 code does (-128 by the RNE and add-then-truncate forms, 0 by lroundf's
+    on the channels past N & ~15 under rule 1)."""
+    N, H, W, Cin, KH, KW, Cout, st, pd = shape
+    q, s_in, _, wq, ws, b = int8_q_inputs(rng, N, H, W, Cin, KH, KW, Cout)
+    b[0] = np.nan
+    b[Cout - 2] = np.nan                           # past Cout & ~15 for the 19-channel case
+    got, so = run_q(gpu, q, s_in, wq, ws, b, KH, KW, Cout, st, pd, 0, rule)
+    want, sw = oracle.conv2d_int8_q(q, s_in, wq, ws, b, KH, KW, Cout, st, pd, 0, rule)
+    assert_bitexact(got, want, f"int8_q NaN {shape} rule {rule}")
+    assert so == sw, (so, sw)
+
+
 @pytest.mark.parametrize("KK,ci,co,pd", [(1, 256, 512, 0), (3, 128, 128, 1)])
 def test_config3_int8_io_full_exact(gpu, rng, KK, ci, co, pd):
     """Configs 3a / 3b with int8 I/O at full size (N=32, 28x28): bit-exact."""

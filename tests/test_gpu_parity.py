@@ -279,6 +279,30 @@ def test_quantize_u8_exact(gpu, rng):
         assert_bitexact(got, oracle.quantize_u8(x, inv_s, 128, 0), "quantize_u8")
 
 
+# NaN, infinities and values whose scaled form leaves int32 (the reference's x86
+# conversions, pinned in tests/test_oracle_pins.py)
+SPECIAL = np.array([np.nan, -np.nan, np.inf, -np.inf, 3e9, -3e9, 2147483648.0, -2147483648.0,
+                    2147483520.0, 1e20, -1e20, 127.5, -128.5], np.float32)
+
+
+def test_quantize_u8_special_values(gpu):
+    for inv_s, zp in ((np.float32(1.0), 128), (np.float32(0.5), 3), (np.float32(2.0), 300)):
+        got = np.zeros(SPECIAL.size, np.uint8)
+        gpu.acfun_quantize_u8(P(SPECIAL), P(got), SPECIAL.size, inv_s, zp)
+        assert_bitexact(got, oracle.quantize_u8(SPECIAL, inv_s, zp, 0), "quantize_u8 specials")
+
+
+def test_quantize_weights_special_values(gpu, rng):
+    w = (rng.standard_normal((40, 6)) * 0.2).astype(np.float32)
+    w[3, 0], w[7, 1] = np.nan, np.inf
+    w[:, 2] = np.nan
+    sw, qw = np.zeros(6, np.float32), np.zeros((40, 6), np.int8)
+    gpu.acfun_quantize_weights(P(w), 40, 6, P(sw), P(qw))
+    so, qo = oracle.quantize_weights(w)
+    assert_bitexact(sw, so, "scales")
+    assert_bitexact(qw, qo, "wq")
+
+
 def test_quantize_weights_exact(gpu, rng):
     w = (rng.standard_normal((300, 37)) * 0.2).astype(np.float32)
     w[:, 5] = 0.0
@@ -320,6 +344,24 @@ def test_conv2d_int8_exact(gpu, rng, shape, act):
     gpu.acfun_conv2d_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), KH, KW, Cout, st, pd,
                           np.float32(0.5), P(got), act)
     assert_bitexact(got, oracle.conv2d_int8(x, wq, ws, b, KH, KW, Cout, st, pd, act), "conv2d_int8")
+
+
+@pytest.mark.parametrize("shape", ROUTE_CASES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv2d_int8_nan_input(gpu, rng, shape, act):
+    """NaN activations on every route: max|x| skips them and each route's
+    quantizer converts them as the reference's x86 code does."""
+    N, H, W, Cin, KH, KW, Cout, st, pd = shape
+    x, wq, ws, b = int8_conv_inputs(rng, N, H, W, Cin, KH, KW, Cout, bias=(act == 1))
+    flat = x.reshape(-1)
+    flat[rng.choice(flat.size, max(3, flat.size // 50), replace=False)] = np.nan
+    flat[-1] = np.nan
+    OH, OW = oracle.out_hw(H, W, KH, KW, st, pd)
+    got = np.full((N, OH, OW, Cout), 7.0, np.float32)
+    gpu.acfun_conv2d_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), KH, KW, Cout, st, pd,
+                          np.float32(0.5), P(got), act)
+    assert_bitexact(got, oracle.conv2d_int8(x, wq, ws, b, KH, KW, Cout, st, pd, act),
+                    f"conv2d_int8 NaN input {shape}")
 
 
 def test_conv2d_int8_zero_input(gpu):

@@ -136,6 +136,49 @@ def test_conv2d_int8_zero_input(ref):
     assert np.all(got == 0.0)   # bias is not added (src/conv_int8.cpp:78)
 
 
+# NaN, infinities and values whose scaled form leaves int32: the reference's x86
+# conversions (integer indefinite for cvtps/cvttps, lroundf's long cut to int)
+SPECIAL = np.array([np.nan, -np.nan, np.inf, -np.inf, 3e9, -3e9, 2147483648.0, -2147483648.0,
+                    2147483520.0, 1e20, -1e20, 127.5, -128.5], np.float32)
+
+
+def test_quantize_u8_special_values(ref):
+    for inv_s, zp in ((np.float32(1.0), 128), (np.float32(0.5), 3), (np.float32(2.0), 300)):
+        want = np.empty(SPECIAL.size, np.uint8)
+        ref.acfun_quantize_u8(P(SPECIAL), P(want), SPECIAL.size, inv_s, zp)
+        assert_bitexact(oracle.quantize_u8(SPECIAL, inv_s, zp, 0), want, "quantize_u8 specials")
+
+
+def test_quantize_weights_special_values(ref, rng):
+    w = (rng.standard_normal((40, 6)) * 0.2).astype(np.float32)
+    w[3, 0] = np.nan                               # NaN among finite weights
+    w[7, 1] = np.inf                               # max|w| = inf: every w/s is 0 or NaN
+    w[:, 2] = np.nan                               # an all-NaN column: scale 1
+    sw, qw = np.empty(6, np.float32), np.empty((40, 6), np.int8)
+    ref.acfun_quantize_weights(P(w), 40, 6, P(sw), P(qw))
+    so, qo = oracle.quantize_weights(w)
+    assert_bitexact(so, sw, "scales")
+    assert_bitexact(qo, qw, "wq")
+
+
+@pytest.mark.parametrize("shape,route", ROUTE_CASES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_conv2d_int8_nan_input(ref, rng, shape, route, act):
+    """NaN activations: max|x| skips them, and each route's quantizer converts
+    them as the reference's x86 code does."""
+    N, H, W, Cin, KH, KW, Cout, st, pd = shape
+    x, wq, ws, b = int8_conv_inputs(rng, N, H, W, Cin, KH, KW, Cout, bias=(act == 1))
+    flat = x.reshape(-1)
+    flat[rng.choice(flat.size, max(3, flat.size // 50), replace=False)] = np.nan
+    flat[-1] = np.nan                              # the last channel: a route's scalar tail
+    OH, OW = oracle.out_hw(H, W, KH, KW, st, pd)
+    want = np.empty((N, OH, OW, Cout), np.float32)
+    ref.acfun_conv2d_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), KH, KW, Cout, st, pd,
+                          np.float32(0.123), P(want), act)
+    got = oracle.conv2d_int8(x, wq, ws, b, KH, KW, Cout, st, pd, act)
+    assert_bitexact(got, want, f"conv2d_int8 route {route} with NaN input")
+
+
 def test_quantize_weights_exact(ref, rng):
     w = (rng.standard_normal((300, 37)) * 0.2).astype(np.float32)
     w[:, 5] = 0.0                                  # all-zero column -> scale 1
