@@ -76,6 +76,7 @@ struct I8M {
     // set by i8mm_prepare: the grid in tiles (gm, gn above) and the float
     // reciprocals of the divisors of the pixel and tap decode
     float r_ohw, r_ow, r_cinp, r_kw;
+    int grid;            // set by the launcher: the launch's workgroups (= partials of amax)
 };
 
 // Fills the launch-derived fields of p for BM x BN tiles.  The reciprocals are

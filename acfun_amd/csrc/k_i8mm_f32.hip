@@ -21,6 +21,7 @@ bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
     }
     i8mm_prepare(p, BM, BN);
     dim3 grid((unsigned)i8mm_grid(p, t));
+    p.grid = (int)grid.x;
     ACFUN_LAUNCH("k_i8mm", (k_i8mm<BM, BN, NST, AM, EPI, OUT_F32>), grid, dim3(256), lds, s, p);
     return check_launch("k_i8mm");
 }

@@ -19,6 +19,7 @@ bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
     }
     i8mm_prepare(p, 64, 64);
     dim3 grid((unsigned)i8mm_grid(p, t));
+    p.grid = (int)grid.x;
     if (OUT == OUT_AMAX)
         ACFUN_LAUNCH("k_i8mm_amax", (k_i8mm<64, 64, NST, AM, EPI, OUT>), grid, dim3(256), lds, s, p);
     else

@@ -529,6 +529,75 @@ __global__ void k_quant_u8(const float* __restrict__ x, uint8_t* __restrict__ ou
     out[i] = (uint8_t)x86_u8(x86_cvt(rintf(t)), zp);
 }
 
+// The s8 requantization of y [M][N], the fp32 output (activation applied) of a
+// k_i8mm pass that also wrote its per-workgroup maxima of |y| (parts): the
+// values and forms of k_i8mm's s8 pass, so the same result bit for bit.
+// max from the partials, q = clamp(form(y * 127/max)) per 16 columns (rule 0:
+// RNE; rule 1: add-then-truncate below N & ~15, lroundf's half-away above,
+// NaN converted as the reference's x86 code does), columns N..ldq-1 and an
+// all-zero y give 0, s_out = max/127 (0 for an all-zero y).  Bounded grid.
+__global__ __launch_bounds__(256) void k_requant_s8(const float* __restrict__ y, int M, int N,
+                                                    int8_t* __restrict__ q, int ldq,
+                                                    const float* __restrict__ parts, int nparts,
+                                                    float* __restrict__ s_out, int rule) {
+    const int groups = ldq >> 4, cvec = N & ~15;
+    const bool vec = (N & 3) == 0;
+    const long long total = (long long)M * groups, stride = (long long)gridDim.x * 256;
+    auto load = [&](long long gi, float* v) {
+        const long long r = gi / groups;
+        const int c0 = (int)(gi - r * groups) * 16;
+        const float* src = y + r * N + c0;
+        if (vec && c0 + 16 <= N) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 f = ((const float4*)src)[k];
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = c0 + k < N ? src[k] : 0.0f;
+        }
+    };
+    // the first group's values load while the partials are reduced
+    long long gi = (long long)blockIdx.x * 256 + threadIdx.x;
+    float v[16];
+    if (gi < total) load(gi, v);
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += 256) { const float a = parts[i]; m = a > m ? a : m; }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float maxa = red[0];
+    for (int k = 1; k < 4; ++k) maxa = red[k] > maxa ? red[k] : maxa;
+    const bool qzero = maxa < 1e-12f;            // as src/conv_int8.cpp:78 for the consumer
+    const float qinv = 127.0f / maxa;
+    if (blockIdx.x == 0 && threadIdx.x == 0) s_out[0] = qzero ? 0.0f : maxa / 127.0f;
+    for (; gi < total; gi += stride) {
+        const long long r = gi / groups;
+        const int c0 = (int)(gi - r * groups) * 16;
+        unsigned w[4] = {0u, 0u, 0u, 0u};
+        if (!qzero) {
+            const int form = rule == 0 ? 0 : (c0 < cvec ? 1 : 2);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float t = __fmul_rn(v[k], qinv);
+                float rq = form == 0 ? rintf(t)
+                         : form == 1 ? truncf(__fadd_rn(t, copysignf(0.5f, t)))
+                                     : (t != t ? 0.0f : roundf(t));
+                rq = fminf(fmaxf(rq, -128.0f), 127.0f);
+                const int qv = c0 + k < N ? (int)rq : 0;
+                w[k >> 2] |= ((unsigned)qv & 0xffu) << (8 * (k & 3));
+            }
+        }
+        *(uint4*)(q + r * ldq + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+        if (gi + stride < total) load(gi + stride, v);
+    }
+}
+
 inline dim3 g1(long long n) { return dim3((unsigned)((n + 255) / 256)); }
 inline int rup(int x, int a) { return (x + a - 1) / a * a; }
 
@@ -665,11 +734,30 @@ bool launch_i8mm(I8M& p, hipStream_t s) {
     return launch_i8mm_f32(p, t, am, s);
 }
 
-// A requantized s8 output: the first pass writes the per-workgroup maxima of
-// the float output into parts (kAmaxParts floats), the second recomputes the
-// tile and stores clamp(rule(v * 127/max)) with s_out = max/127.
-bool launch_i8mm_rq(I8M& p, float* parts, hipStream_t s) {
+// A requantized s8 output.  Without ybuf: the first pass writes the
+// per-workgroup maxima of the float output into parts (kAmaxParts floats), the
+// second recomputes the tile and stores clamp(rule(v * 127/max)) with s_out =
+// max/127.  With ybuf (M x N floats): one fp32 pass into ybuf with the maxima,
+// then k_requant_s8.
+bool launch_i8mm_rq(I8M& p, float* parts, float* ybuf, hipStream_t s) {
     if (p.M <= 0 || p.N <= 0) return true;
+    if (ybuf) {
+        // One pass: the fp32 output (activation applied) and its per-workgroup
+        // maxima, then k_requant_s8 over it.  The values requantized are the ones
+        // the s8 pass would form, so the result is the same bit for bit.
+        I8M f = p;
+        f.Cf = ybuf;
+        f.ldc = p.N;
+        f.res = nullptr;
+        f.amax = parts;
+        f.Cq = nullptr;
+        if (!launch_i8mm(f, s)) return false;
+        const long long groups = (long long)p.M * (p.ldq / 16);
+        const long long blocks = std::min((groups + 255) / 256, 8ll * num_cus());
+        ACFUN_LAUNCH("k_requant_s8", k_requant_s8, dim3((unsigned)blocks), dim3(256), 0, s, ybuf, p.M,
+                     p.N, p.Cq, p.ldq, parts, f.grid, p.s_out, p.rule);
+        return check_launch("k_requant_s8");
+    }
     I8Tile t = pick_i8mm_tile(p.M, p.N, p.K);
     t.bm = t.bn = 64;                           // the s8 epilogue stages 64 x 64 tiles
     if (t.per_cu <= 0) t.per_cu = 3;
@@ -1011,7 +1099,14 @@ bool conv2d_int8_q8_dev(const int8_t* q, int ldq_in, const float* s_in, const Co
     p.Cq = out; p.ldq = ldo; p.rule = rule; p.s_out = s_out;
     if (wino) p.epi = EPI_WINO;
     else { p.epi = EPI_GEMM; p.Sw = sw; }
-    return launch_i8mm_rq(p, parts, s);
+    // Long K: store the fp32 output once and requantize it (a pass over 9 bytes
+    // per output) rather than recompute every tile in a second pass.
+    float* ybuf = nullptr;
+    if (p.K >= 512) {
+        ybuf = (float*)ar.get((size_t)p.M * p.N * sizeof(float));
+        if (!ybuf) return false;
+    }
+    return launch_i8mm_rq(p, parts, ybuf, s);
 }
 
 bool conv2d_int8_q8_api(const int8_t* in, const float* s_in, const ConvShape& g,

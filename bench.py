@@ -580,7 +580,8 @@ def main():
             tc = T.run(rotating(fn, xs, ys), steps, args.warmup)
             del xs, ys
             tq = T.run(cfg[name + "_q"]["step"], steps, args.warmup)
-            kq = T.kernel_ms(lib, cfg[name + "_q"]["step"], steps, ["k_i8mm_amax", "k_i8mm_q8"])
+            kq = T.kernel_ms(lib, cfg[name + "_q"]["step"], steps,
+                             ["k_i8mm_amax", "k_i8mm_q8", "k_i8mm", "k_requant_s8"])
             fn, xt, yt = cfg[name + "_q"]["rot"]
             xs, ys = rotation_sets(xt, yt)
             tqc = T.run(rotating(fn, xs, ys), steps, args.warmup)
@@ -602,7 +603,8 @@ def main():
                     "TOPS": round(ops / (tq * 1e-3) / 1e12, 3),
                     "roofline": roofline("hbm" if name == "cfg3a" else "mfma-int8",
                                          c["qbytes"] if name == "cfg3a" else ops, tq,
-                                         "step (k_i8mm max pass + k_i8mm s8 pass)",
+                                         "step (k_i8mm max pass + s8 pass, or for K >= 512 "
+                                         "k_i8mm fp32 pass + k_requant_s8)",
                                          (f"int8 I/O {c['qbytes'] / 1e6:.1f} MB per step" if name == "cfg3a"
                                           else f"{ops / 1e9:.2f} GOP per step (MFMA-bound with int8 I/O)")
                                          + " (acfun_dev_conv2d_int8_q)"),

@@ -65,7 +65,8 @@ def test_conv2d_int8_q_exact(gpu, rng, shape, act, rule):
     assert np.max(np.abs(got.astype(np.int32))) == 127      # the max maps to +-127
 
 
-@pytest.mark.parametrize("shape", [(2, 9, 9, 20, 3, 3, 19, 1, 1), (2, 14, 14, 32, 1, 1, 40, 1, 0)])
+@pytest.mark.parametrize("shape", [(2, 9, 9, 20, 3, 3, 19, 1, 1), (2, 14, 14, 32, 1, 1, 40, 1, 0),
+                                   (2, 9, 9, 64, 3, 3, 19, 1, 1)])   # (K = 576: the one-pass path)
 @pytest.mark.parametrize("rule", [0, 1])
 def test_conv2d_int8_q_nan_outputs(gpu, rng, shape, rule):
     """NaN biases (no activation) make whole output channels NaN: the output
