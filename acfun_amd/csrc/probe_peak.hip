@@ -8,6 +8,11 @@
 // one MFMA shape busy for `iters` x 32 instructions; FLOPs = waves x MFMAs x
 // the instruction's 2*M*N*K.  s_memtime / s_memrealtime (100 MHz) give the
 // shader clock over the run.
+// fp32 MFMA beside VALU work: whether v_mfma_f32_32x32x2f32 and v_fma_f32
+// share the SIMD's time (the transforms of a Winograd kernel are fp32 VALU
+// work next to its fp32 MFMAs).  Per iteration 8 MFMAs (independent
+// accumulators) and/or 8 x V fmas (16 independent chains), either in one
+// wave interleaved MFMA, V fmas, MFMA, ... or in two waves of one SIMD.
 // HBM: a grid-stride float4 read (sum) and copy over buffers of 4 GiB, far
 // beyond the 256 MB last-level cache, timed after one untimed pass.
 #include <hip/hip_runtime.h>
@@ -88,6 +93,48 @@ __global__ __launch_bounds__(256) void k_peak(float* out, int iters, unsigned lo
   }
 }
 
+// MODE 0: MFMA only, 1: fma only, 2: both in each wave, 3: waves 0-3 MFMA and
+// waves 4-7 fma (512 threads: two waves per SIMD); MODE 0-2 use waves 0-3
+template <int MODE, int V>
+__global__ __launch_bounds__(512, 1) void k_overlap(float* out, int iters) {
+  const int w = threadIdx.x >> 6;
+  const bool mf = MODE == 0 || MODE == 2 || (MODE == 3 && w < 4);
+  const bool va = MODE == 1 || MODE == 2 || (MODE == 3 && w >= 4);
+  if (MODE != 3 && w >= 4) return;
+  f16v acc[8];
+  for (int k = 0; k < 8; ++k)
+    for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
+  float x[16];
+  for (int i = 0; i < 16; ++i) x[i] = threadIdx.x * 1e-3f + i;
+  const float a = threadIdx.x * 0.5f, b = 1.0f / (threadIdx.x + 1);
+  for (int it = 0; it < iters; ++it) {
+    if (mf && va) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[k], 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[(k * V + v) & 15] = fmaf(x[(k * V + v) & 15], 1.0001f, 0.5f);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+      }
+    } else if (mf) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[k], 0, 0, 0);
+    } else if (va) {
+#pragma unroll
+      for (int k = 0; k < 8 * V; ++k) x[k & 15] = fmaf(x[k & 15], 1.0001f, 0.5f);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float r = 0.f;
+  for (int k = 0; k < 8; ++k) r += acc[k][0] + acc[k][15];
+  for (int i = 0; i < 16; ++i) r += x[i];
+  out[blockIdx.x * 512 + threadIdx.x] = r;
+}
+
 // grid-stride float4 sum: one partial per thread, so the loads cannot be elided
 __global__ __launch_bounds__(256) void k_read(const float4* __restrict__ a, size_t n4,
                                               float* __restrict__ part) {
@@ -150,6 +197,41 @@ int main() {
                   names[kind], bpc, ms, rate, rate / published[kind], published[kind],
                   (double)h[0] / ((double)h[1] * 10.0));
     }
+  }
+
+  {
+    // fp32 MFMA beside fp32 VALU: one workgroup per CU, MFMA work on four waves
+    const int it2 = 20000;
+    auto timed = [&](auto launch) {
+      launch(10);
+      CHECK(hipGetLastError());
+      CHECK(hipDeviceSynchronize());
+      CHECK(hipEventRecord(e0, 0));
+      launch(it2);
+      CHECK(hipEventRecord(e1, 0));
+      CHECK(hipEventSynchronize(e1));
+      float ms;
+      CHECK(hipEventElapsedTime(&ms, e0, e1));
+      return ms;
+    };
+#define ACFUN_OVL(MODE, V)                                                                        \
+  timed([&](int n) { hipLaunchKernelGGL((k_overlap<MODE, V>), dim3(cus), dim3(512), 0, 0, out2, n); })
+    float* out2;
+    CHECK(hipMalloc(&out2, (size_t)cus * 512 * sizeof(float)));
+    const float m0 = ACFUN_OVL(0, 8);
+    std::printf("fp32 MFMA / VALU overlap, %d iterations of 8 MFMAs and/or 8 x V v_fma_f32 per wave:\n", it2);
+    std::printf("  MFMA only            %7.3f ms\n", m0);
+    const float v4 = ACFUN_OVL(1, 4), v8 = ACFUN_OVL(1, 8), v15 = ACFUN_OVL(1, 15);
+    const float b4 = ACFUN_OVL(2, 4), b8 = ACFUN_OVL(2, 8), b15 = ACFUN_OVL(2, 15);
+    const float w4 = ACFUN_OVL(3, 4), w8 = ACFUN_OVL(3, 8), w15 = ACFUN_OVL(3, 15);
+#undef ACFUN_OVL
+    const float vs[3] = {v4, v8, v15}, bs[3] = {b4, b8, b15}, ws[3] = {w4, w8, w15};
+    const int Vs[3] = {4, 8, 15};
+    for (int i = 0; i < 3; ++i)
+      std::printf("  V=%2d: fma only %7.3f ms | one wave, interleaved %7.3f ms | MFMA wave + fma wave "
+                  "%7.3f ms | sum %7.3f, max %7.3f\n",
+                  Vs[i], vs[i], bs[i], ws[i], m0 + vs[i], m0 > vs[i] ? m0 : vs[i]);
+    CHECK(hipFree(out2));
   }
 
   const size_t bytes = (size_t)4 << 30;
