@@ -93,6 +93,23 @@ def test_dw_maxpool_nan_partial_vec(gpu, rng, st):
                         want_dwpool(x, w, b, st, 1, act, 1, pr), f"C=20 NaN s{st} act={act} pr={pr}")
 
 
+@pytest.mark.parametrize("C", [16, 20])
+def test_dw_maxpool_nan_strips(gpu, rng, C):
+    """Stride 2 over 3 strips of 4 pooled rows (the row-streaming kernel's
+    unit): NaNs in each strip, at strip boundaries and in the halo rows the
+    strips share, with full (C = 16) and partial (C = 20) max_ps channel
+    groups."""
+    x = rng.standard_normal((2, 41, 22, C)).astype(np.float32)
+    for (n, r, c, ch) in ((0, 3, 4, 1), (0, 15, 7, 2), (0, 16, 8, C - 1), (1, 17, 9, 3),
+                          (1, 24, 20, C - 2), (0, 31, 0, 0), (1, 33, 21, C - 3), (0, 40, 5, 5)):
+        x[n, r, c, ch] = np.nan
+    w = (rng.standard_normal((C, 3, 3)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    for act, pr in ((0, 0), (1, 0), (0, 1)):
+        assert_bitexact(run_dwpool(gpu, x, w, b, 2, 1, act, 1, pr),
+                        want_dwpool(x, w, b, 2, 1, act, 1, pr), f"strips C={C} act={act} pr={pr}")
+
+
 def test_config4a_fused_full_exact(gpu, rng):
     """Config 4(a) at full size: depthwise 3x3/2 (BN folded) + ReLU, then
     MaxPool 3x3/2 pad 1 -- one kernel, bit-exact against the two reference ops."""
