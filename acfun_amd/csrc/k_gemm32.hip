@@ -221,7 +221,10 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     }
 
     // Software pipeline per chunk c (operands in registers):
-    //   MFMAs of k-steps 0..27 (the DMA of chunk c+AHEAD issued between them);
+    //   the DMA of chunk c+AHEAD, all of it up front (issued between the first
+    //   k-steps' MFMAs it measured 4 % slower at 1024^3: the last loads had
+    //   only the deferred k-steps to land in);
+    //   MFMAs of k-steps 0..27;
     //   the last four k-steps' operands set aside;
     //   wait for chunk c+1's DMA, LDS-only barrier, LDS reads of all of chunk
     //   c+1's operands;
@@ -267,10 +270,9 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], bb[j][s],
                                                                      acc[i][j], 0, 0, 0);
-            if (more) {
+            if (more && s == 0) {                  // its stage was read before this chunk
 #pragma unroll
-                for (int t = s * ITEMS / (32 - DEFER); t < (s + 1) * ITEMS / (32 - DEFER); ++t)
-                    issue(t, c + AHEAD, NA);
+                for (int t = 0; t < ITEMS; ++t) issue(t, c + AHEAD, NA);
             }
         }
         f4g al[FM];
