@@ -192,11 +192,8 @@ __global__ void k_wino_filter_t(const float* __restrict__ w, int Cin, int Cinp, 
 // Filter transform as a tiled transpose: a 256-lane block owns 16 output x 16
 // input channels.  Lane (o = l%16, c = l/16) reads its 9 taps with output
 // channels fastest (64-byte runs of w), transforms them, and the block writes
-// through LDS with input channels fastest: U[a][Cout][Cinp] (64-byte runs), or
-// with CHUNK8 the chunked layout U[Cinp/8][a][Cout][8], in which the filter
-// slice one 8-channel chunk of a kernel needs for one point and 32 output
-// channels is a single contiguous kilobyte.
-template <int TILE, bool CHUNK8>
+// through LDS with input channels fastest: U[a][Cout][Cinp] (64-byte runs).
+template <int TILE>
 __global__ __launch_bounds__(256) void k_wino_filter_tt(const float* __restrict__ w, int Cin,
                                                          int Cinp, int Cout, float* __restrict__ U) {
     constexpr int A = Wino<TILE>::A, AA = A * A;
@@ -228,15 +225,42 @@ __global__ __launch_bounds__(256) void k_wino_filter_tt(const float* __restrict_
     const long long plane = (long long)Cout * Cinp;
     if (o0 + wo < Cout && c0 + wc < Cinp) {
         const int c = c0 + wc;
-        if (CHUNK8) {
-            const long long base = (long long)(c >> 3) * AA * Cout * 8 + (long long)(o0 + wo) * 8 + (c & 7);
 #pragma unroll
-            for (int a = 0; a < AA; ++a) U[base + (long long)a * Cout * 8] = tr[a][wo][wc];
-        } else {
-#pragma unroll
-            for (int a = 0; a < AA; ++a) U[a * plane + (long long)(o0 + wo) * Cinp + c] = tr[a][wo][wc];
-        }
+        for (int a = 0; a < AA; ++a) U[a * plane + (long long)(o0 + wo) * Cinp + c] = tr[a][wo][wc];
     }
+}
+
+// The chunked layout U[Cinp/8][a][Cout][8], in which the filter slice one
+// 8-channel chunk of a unit kernel needs for one point and 32 output channels
+// is a single contiguous kilobyte, written directly: lane (c % 8, o)
+// of a 64-thread block transforms one filter and writes its AA points, and
+// the 64 lanes of one point store 8 output channels x 8 input channels, 256
+// contiguous bytes, without an LDS transpose.  The arithmetic is
+// k_wino_filter_tt's (the same f_tf).
+template <int TILE>
+__global__ __launch_bounds__(64) void k_wino_filter_c8(const float* __restrict__ w, int Cin, int Cout,
+                                                      float* __restrict__ U) {
+    constexpr int A = Wino<TILE>::A, AA = A * A;
+    const int l = threadIdx.x;
+    const int c = blockIdx.y * 8 + (l & 7), o = blockIdx.x * 8 + (l >> 3);
+    if (o >= Cout) return;
+    float gh[A][A];
+    if (c < Cin) {
+        float g[3][3];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) g[kh][kw] = w[((long long)(kh * 3 + kw) * Cin + c) * Cout + o];
+        Wino<TILE>::f_tf(g, gh);
+    } else {
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < A; ++j) gh[i][j] = 0.f;
+    }
+    const long long base = (long long)blockIdx.y * AA * Cout * 8 + (long long)o * 8 + (l & 7);
+#pragma unroll
+    for (int a = 0; a < AA; ++a) U[base + (long long)a * Cout * 8] = gh[a / A][a % A];
 }
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -1454,10 +1478,10 @@ int wino23_plan_impl(int N, int H, int W, int Cin, int Cout, const void* in) {
 bool wino23_filter_impl(const float* w, int Cin, int Cout, int plan, float* U, hipStream_t s) {
     const int Cinp = (Cin + 15) / 16 * 16;
     if (plan == 1)
-        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, true>), dim3((Cout + 15) / 16, Cinp / 16),
-                     dim3(256), 0, s, w, Cin, Cinp, Cout, U);
+        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_c8<2>), dim3((Cout + 7) / 8, Cinp / 8), dim3(64), 0, s,
+                     w, Cin, Cout, U);
     else
-        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2, false>), dim3((Cout + 15) / 16, Cinp / 16),
+        ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<2>), dim3((Cout + 15) / 16, Cinp / 16),
                      dim3(256), 0, s, w, Cin, Cinp, Cout, U);
     return check_launch("k_wino_filter_t");
 }
@@ -1620,8 +1644,8 @@ bool run_fused(const float* in, int N, int H, int W, int Cin, const float* w, co
 
 bool wino43_filter(const float* w, int Cin, int Cout, float* U, hipStream_t s) {
     const int Cinp = (Cin + 15) / 16 * 16;
-    ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_tt<4, true>), dim3((Cout + 15) / 16, Cinp / 16),
-                 dim3(256), 0, s, w, Cin, Cinp, Cout, U);
+    ACFUN_LAUNCH("k_wino_filter_t", (k_wino_filter_c8<4>), dim3((Cout + 7) / 8, Cinp / 8), dim3(64), 0, s, w,
+                 Cin, Cout, U);
     return check_launch("k_wino_filter_t");
 }
 
