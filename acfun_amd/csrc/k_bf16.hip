@@ -6,13 +6,15 @@
 // so the result differs from the reference only by the fp32 accumulation
 // order.
 //
-// Two packing kernels write the rounded operands k-contiguous -- A as
-// [M][Kp], B transposed as [N][Kp], Kp = K rounded up to 64, zeros beyond K --
-// and k_bf16mm multiplies them on v_mfma_f32_32x32x16_bf16.  Its staging is
-// the int8 kernel's: 64 x 64 tiles, 2 x 2 waves, K in chunks of 128 bytes
-// (64 bf16) DMA'd into LDS by buffer_load_dwordx4 ... lds, quad q of row r at
-// slot r*8 + (q ^ swz(r)), three stages.  In k-step s lane half h reads quad
-// 2s+h of its A row and its B row: eight bf16 each, the MFMA's 16 k per step.
+// One packing launch writes the rounded operands k-contiguous -- A as
+// [M][Kp], B transposed as [N][Kp], Kp = K rounded up to 128, zeros beyond K
+// -- and k_bf16mm multiplies them on v_mfma_f32_32x32x16_bf16: 64 x 64 tiles,
+// 2 x 2 waves, K in chunks of 256 bytes (128 bf16) DMA'd into LDS by
+// buffer_load_dwordx4 ... lds, quad q of row r at slot r*16 + (q ^ (r % 16)),
+// four stages (three chunks ahead).  In k-step s lane half h reads quad 2s+h
+// of its A row and its B row: eight bf16 each, the MFMA's 16 k per step.  At
+// 1024^3 the grid is one tile per CU and the K loop is bound by the DMA round
+// trip, so the chunks are large and many are in flight.
 #include "rt.hpp"
 
 namespace acfun {
@@ -33,11 +35,9 @@ __device__ __forceinline__ unsigned bf16_bits(float f) {
 }
 
 // One lane: 8 consecutive k of one row of A -> one 16-byte store.
-__global__ __launch_bounds__(256) void k_pack_a_bf16(const float* __restrict__ A, int M, int K,
-                                                     int lda, unsigned short* __restrict__ Ab,
-                                                     int Kp) {
+__device__ __forceinline__ void pack_a_bf16(long long t, const float* __restrict__ A, int M, int K,
+                                            int lda, unsigned short* __restrict__ Ab, int Kp) {
     const int kq = Kp >> 3;
-    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
     if (t >= (long long)M * kq) return;
     const int m = (int)(t / kq), k0 = (int)(t - (long long)m * kq) * 8;
     const float* src = A + (long long)m * lda + k0;
@@ -54,10 +54,8 @@ __global__ __launch_bounds__(256) void k_pack_a_bf16(const float* __restrict__ A
 
 // One lane: column n, 8 consecutive k of B -> one 16-byte store into Bt[n][k0..].
 // Lanes run n fastest, so each of the 8 loads is a coalesced row segment.
-__global__ __launch_bounds__(256) void k_pack_bt_bf16(const float* __restrict__ B, int K, int N,
-                                                      int ldb, unsigned short* __restrict__ Bt,
-                                                      int Kp) {
-    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void pack_bt_bf16(long long t, const float* __restrict__ B, int K, int N,
+                                             int ldb, unsigned short* __restrict__ Bt, int Kp) {
     if (t >= (long long)N * (Kp >> 3)) return;
     const int kb = (int)(t / N), n = (int)(t - (long long)kb * N);
     const int k0 = kb * 8;
@@ -72,16 +70,27 @@ __global__ __launch_bounds__(256) void k_pack_bt_bf16(const float* __restrict__ 
     *(i4v*)(Bt + (long long)n * Kp + k0) = i4v{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
 
-__device__ __forceinline__ int bswz(int r) { return (r ^ (r >> 3)) & 7; }
+// Both operands in one launch: blocks [0, nba) pack A, the rest B.
+__global__ __launch_bounds__(256) void k_pack_bf16(const float* __restrict__ A, const float* __restrict__ B,
+                                                   int M, int N, int K, int lda, int ldb, int Kp, int nba,
+                                                   unsigned short* __restrict__ Ab,
+                                                   unsigned short* __restrict__ Bt) {
+    const int b = (int)blockIdx.x;
+    if (b < nba) pack_a_bf16((long long)b * 256 + threadIdx.x, A, M, K, lda, Ab, Kp);
+    else pack_bt_bf16((long long)(b - nba) * 256 + threadIdx.x, B, K, N, ldb, Bt, Kp);
+}
 
-constexpr int BF_BM = 64, BF_BN = 64, BF_NST = 3;
-constexpr int BF_SA = BF_BM * 128, BF_STG = (BF_BM + BF_BN) * 128;
+constexpr int BF_BM = 64, BF_BN = 64, BF_NST = 4, BF_KB = 256;   // K chunk: 256 bytes, 128 bf16
+constexpr int BF_SA = BF_BM * BF_KB, BF_STG = (BF_BM + BF_BN) * BF_KB;
+static_assert(BF_NST == 4, "the waits below leave at most two chunks in flight");
+// s_waitcnt vmcnt(n), n < 64
+constexpr int bf_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict__ Ab,
                                                 const unsigned short* __restrict__ Bt,
                                                 float* __restrict__ C, int M, int N, int Kp,
                                                 int ldc, unsigned a_bytes, unsigned b_bytes) {
-    constexpr int AIT = BF_BM / 32, BIT = BF_BN / 32, ITEMS = AIT + BIT;
+    constexpr int AIT = BF_BM / 16, BIT = BF_BN / 16, ITEMS = AIT + BIT;   // 1 KB (4 rows) per item
     constexpr int AHEAD = BF_NST - 1;
     constexpr unsigned kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) char smb[];
@@ -93,32 +102,33 @@ __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict
     int L = blockIdx.x;
     if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
     const int m0 = (L / gn) * BF_BM, n0 = (L % gn) * BF_BN;
-    const int nch = Kp >> 6;
+    const int nch = Kp >> 7;
     const __amdgpu_buffer_rsrc_t ares =
         __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, (int)a_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t bres =
         __builtin_amdgcn_make_buffer_rsrc((void*)Bt, (short)0, (int)b_bytes, 0x00020000);
-    // DMA rows of this lane: row 8*(wave + 4t) + lane/8, quad slot lane%8
-    const int sl = lane & 7, rl = lane >> 3;
+    // DMA rows of this lane: row 4*(wave + 4t) + lane/16, slot lane%16 holding
+    // quad (lane%16) ^ (row%16)
+    const int sl = lane & 15, rl = lane >> 4;
     unsigned av[AIT], bv[BIT];
 #pragma unroll
     for (int t = 0; t < AIT; ++t) {
-        const int row = 8 * (wave + 4 * t) + rl, q = sl ^ bswz(row);
+        const int row = 4 * (wave + 4 * t) + rl, q = sl ^ (row & 15);
         av[t] = m0 + row < M ? (unsigned)((m0 + row) * Kp * 2 + 16 * q) : kOOB;
     }
 #pragma unroll
     for (int t = 0; t < BIT; ++t) {
-        const int row = 8 * (wave + 4 * t) + rl, q = sl ^ bswz(row);
+        const int row = 4 * (wave + 4 * t) + rl, q = sl ^ (row & 15);
         bv[t] = n0 + row < N ? (unsigned)((n0 + row) * Kp * 2 + 16 * q) : kOOB;
     }
     auto issue = [&](int t, int c, char* st) {
         if (t < AIT) {
-            const unsigned v = av[t] + (unsigned)(c << 7);   // kOOB + k stays out of range
+            const unsigned v = av[t] + (unsigned)(c << 8);   // kOOB + k stays out of range
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(st + (wave + 4 * t) * 1024), 16,
                                                      v, 0, 0, 0);
         } else {
             const int tt = t - AIT;
-            const unsigned v = bv[tt] + (unsigned)(c << 7);
+            const unsigned v = bv[tt] + (unsigned)(c << 8);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(st + BF_SA + (wave + 4 * tt) * 1024),
                                                      16, v, 0, 0, 0);
         }
@@ -126,11 +136,11 @@ __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict
     // LDS read offsets (bytes within a stage) per k-step
     const int r32 = lane & 31, hq = lane >> 5;
     const int ra = wm * 32 + r32, rb = wn * 32 + r32;
-    int rda[4], rdb[4];
+    int rda[8], rdb[8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        rda[s] = ra * 128 + 16 * ((2 * s + hq) ^ bswz(ra));
-        rdb[s] = BF_SA + rb * 128 + 16 * ((2 * s + hq) ^ bswz(rb));
+    for (int s = 0; s < 8; ++s) {
+        rda[s] = ra * BF_KB + 16 * ((2 * s + hq) ^ (ra & 15));
+        rdb[s] = BF_SA + rb * BF_KB + 16 * ((2 * s + hq) ^ (rb & 15));
     }
     f16v acc;
 #pragma unroll
@@ -144,27 +154,29 @@ __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict
         }
     int st = 0;
     for (int c = 0; c < nch; ++c) {
-        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt((ITEMS & 15) | 0x0F70);   // vmcnt(ITEMS)
-        else __builtin_amdgcn_s_waitcnt(0x0F70);                               // vmcnt(0)
+        // chunk c landed: the chunks after it (at most AHEAD - 1) stay in flight
+        const int later = nch - 1 - c < AHEAD - 1 ? nch - 1 - c : AHEAD - 1;
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(bf_vmcnt(2 * ITEMS));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(bf_vmcnt(ITEMS));
+        else __builtin_amdgcn_s_waitcnt(bf_vmcnt(0));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const char* S = smb + st * BF_STG;
-        char* NA = smb + (st == 0 ? BF_NST - 1 : st - 1) * BF_STG;
+        char* NA = smb + (st == 0 ? BF_NST - 1 : st - 1) * BF_STG;   // (c + AHEAD) % NST: chunk c - 1's
         const bool more = c + AHEAD < nch;
-        i4v fa[4], fb[4];
+        i4v fa[8], fb[8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < 8; ++s) {
             fa[s] = *(const i4v*)(S + rda[s]);
             fb[s] = *(const i4v*)(S + rdb[s]);
         }
+        if (more) {                                      // its stage was read before this chunk
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+            for (int t = 0; t < ITEMS; ++t) issue(t, c + AHEAD, NA);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, fa[s]),
                                                           __builtin_bit_cast(bf8, fb[s]), acc, 0, 0, 0);
-            if (more) {
-#pragma unroll
-                for (int t = s * ITEMS / 4; t < (s + 1) * ITEMS / 4; ++t) issue(t, c + AHEAD, NA);
-            }
-        }
         st = st == BF_NST - 1 ? 0 : st + 1;
     }
     // epilogue: lane l, register e <-> row m0 + 32wm + 8(e/4) + 4(l/32) + e%4, column n0 + 32wn + l%32
@@ -180,7 +192,7 @@ __global__ __launch_bounds__(256) void k_bf16mm(const unsigned short* __restrict
 // C[0:M, 0:N] (row stride ldb = ldc) = bf16(A[0:M, :]) x bf16(B[:, 0:N]) on bf16 MFMA
 bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, float* C,
                  hipStream_t s) {
-    const int Kp = (K + 63) / 64 * 64;
+    const int Kp = (K + 127) / 128 * 128;
     if ((long long)M * Kp * 2 >= 0x7fffffffll || (long long)N * Kp * 2 >= 0x7fffffffll) {
         set_error("acfun_gemm_bf16: operands beyond 2 GB");
         return false;
@@ -188,12 +200,14 @@ bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, f
     Scratch ab((size_t)M * Kp * 2, s), bt((size_t)N * Kp * 2, s);
     if (!ab.p || !bt.p) return false;
     const long long na = (long long)M * (Kp / 8), nb = (long long)N * (Kp / 8);
-    hipLaunchKernelGGL(k_pack_a_bf16, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, A, M, K, K,
-                       ab.as<unsigned short>(), Kp);
-    if (!check_launch("k_pack_a_bf16")) return false;
-    hipLaunchKernelGGL(k_pack_bt_bf16, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, B, K, N, ldb,
-                       bt.as<unsigned short>(), Kp);
-    if (!check_launch("k_pack_bt_bf16")) return false;
+    const long long nba = (na + 255) / 256, nbb = (nb + 255) / 256;
+    if (nba + nbb >= (1ll << 31)) {
+        set_error("acfun_gemm_bf16: operands too large");
+        return false;
+    }
+    hipLaunchKernelGGL(k_pack_bf16, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, A, B, M, N, K, K, ldb, Kp,
+                       (int)nba, ab.as<unsigned short>(), bt.as<unsigned short>());
+    if (!check_launch("k_pack_bf16")) return false;
     static bool attr = false;
     constexpr int lds = BF_NST * BF_STG;
     if (!attr) {

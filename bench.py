@@ -553,7 +553,7 @@ def main():
         configs["gemm_bf16_1024"] = {"ms": round(t, 5), "TFLOPS": round(flop / (t * 1e-3) / 1e12, 3),
                                      "frac_bf16_peak_kernel": round(flop / (k["k_bf16mm"] * 1e-3) / PEAK_BF16, 4)
                                      if k["k_bf16mm"] else None,
-                                     "kernel_ms": k, "note": "step = two bf16 packing passes + k_bf16mm"}
+                                     "kernel_ms": k, "note": "step = one bf16 packing launch (A and B) + k_bf16mm"}
 
         # 2(b): F(4,3) route; the fraction counts section 8(d)'s F(4,3) work
         t = T.run(cfg["cfg2b"]["step"], steps, args.warmup)
