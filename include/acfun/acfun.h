@@ -261,7 +261,10 @@ AcfunModel* acfun_model_load_ex(const char* path, int flags);
  * its input with one scale for the whole batch, so an image's result depends
  * on the other images of its batch; with N = 1 it is acfun_model_infer's. */
 int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* output);
-/* The same on device pointers, queued on `stream` (not synchronized). */
+/* The same on device pointers, queued on `stream` (not synchronized).  A model
+ * holds per-layer device state (Winograd filter transforms made at first use),
+ * so one model runs one inference at a time: calls on the same model from
+ * different streams must not overlap. */
 int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float* output,
                                 void* stream);
 

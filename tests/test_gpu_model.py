@@ -10,6 +10,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+import oracle
 import oracle.model as omodel
 from acfun_amd import acfun0, capi
 from tests import models
@@ -184,3 +185,27 @@ def test_resnet50_headless_batch8(gpu, rng, tmp_path, int8):
         assert_bitexact(got, want, "int8 ResNet-50 body, batch 8")
     else:
         assert rel_err(got, want) < TOL, rel_err(got, want)
+
+
+def test_model_winograd_cache_repeats(gpu, rng, tmp_path):
+    """A 3x3 conv whose model keeps its F(2,3) filter transform from the first
+    inference, at config 2(a)'s size (32 x 56 x 56 x 64, more units than the
+    persistent unit kernel has workgroups): three inferences in a row give the
+    entry point's bits on the same weights."""
+    C, HW, N = 64, 56, 32
+    w = acfun0.conv_weight(rng, 3, 3, C, C)
+    b = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    path = _write(tmp_path, "wino.acfun", C, HW, HW, [("conv", 3, 3, C, 1, 1, w, b)], 1)
+    x = rng.uniform(0, 1, (N, HW, HW, C)).astype(np.float32)
+    want = np.full((N, HW, HW, C), np.nan, np.float32)
+    gpu.acfun_conv2d(P(x), N, HW, HW, C, P(w.reshape(9 * C, C)), P(b), 3, 3, C, 1, 1, P(want))
+    assert rel_err(want[:1], oracle.conv2d_f64(np.ascontiguousarray(x[:1]), w.reshape(9 * C, C), b, 3, 3, C, 1, 1)) < TOL
+    m = _load(gpu, path)
+    try:
+        for i in range(3):
+            got = np.full((N, HW, HW, C), np.nan, np.float32)
+            assert gpu.acfun_model_infer_batch(m, N, P(x), P(got)) == HW * HW * C, capi.last_error()
+            assert_bitexact(got, want, f"model inference {i} vs acfun_conv2d")
+    finally:
+        gpu.acfun_model_destroy(m)
+
