@@ -11,9 +11,9 @@ config.  roofline divides the same executed FLOPs by the dominant kernel's own
 mean duration.
 
 Every other BASELINE config is measured the same way under "configs": its step
-time, the dominant kernel's time, a roofline block on the algorithmic work of
-SURVEY.md section 8(d) (FLOPs, ops or bytes, as the config is MFMA- or
-HBM-bound), and a cpu_baseline: the reference library itself (oracle/_ref,
+time, the dominant kernel's time, a roofline block on the config's algorithmic
+work (FLOPs, ops or bytes: the ones the computation needs, not padding or
+re-reads, as the config is MFMA- or HBM-bound), and a cpu_baseline: the reference library itself (oracle/_ref,
 built from the reference's sources) timed on this host's cores on a bounded
 sample of the same workload, 3 warmups then the median (src/benchmark.cpp:98-111).
 Configs 3 and 4 also report "ms_cold": the step cycling over copies of its
@@ -555,7 +555,7 @@ def main():
                                      if k["k_bf16mm"] else None,
                                      "kernel_ms": k, "note": "step = one bf16 packing launch (A and B) + k_bf16mm"}
 
-        # 2(b): F(4,3) route; the fraction counts section 8(d)'s F(4,3) work
+        # 2(b): F(4,3) route; the fraction counts the F(4,3) work the route needs
         t = T.run(cfg["cfg2b"]["step"], steps, args.warmup)
         k = T.kernel_ms(lib, cfg["cfg2b"]["step"], steps, ["k_wino43", "k_wino23", "k_wino_fused",
                                                              "k_wino_filter_t"])
@@ -565,7 +565,7 @@ def main():
             "ms": round(t, 5), "TFLOPS_direct_equivalent": round(direct_flop / (t * 1e-3) / 1e12, 3),
             "TFLOPS_f43_work": round(f43 / (t * 1e-3) / 1e12, 3),
             "roofline": roofline("mfma-fp32", f43, k[kern], kern,
-                                 "F(4,3) work of section 8(d): 2 * 6272 tiles * 36 points * 64 * "
+                                 "F(4,3) work: 2 * 6272 tiles * 36 points * 64 * "
                                  "64 = 1.850 GFLOP per launch, whichever kernel runs it",
                                  "k_wino_cfg2b"),
             "kernel_ms": k}
@@ -592,8 +592,8 @@ def main():
                     "ms": round(t, 5), "ms_cold": round(tc, 5),
                     "TOPS": round(ops / (t * 1e-3) / 1e12, 3),
                     "roofline": roofline("hbm", c["fbytes"], t, "step (absmax + quantize + k_i8mm)",
-                                         f"float I/O {c['fbytes'] / 1e6:.1f} MB per step (section "
-                                         "8(d)); the int8 fraction is TOPS/5000"),
+                                         f"float I/O {c['fbytes'] / 1e6:.1f} MB per step (fp32 input "
+                                         "read, fp32 output written); the int8 fraction is TOPS/5000"),
                     "frac_int8_peak": round(ops / (t * 1e-3) / PEAK_INT8, 4),
                     "kernel_ms": k,
                     "kernel_frac_int8_peak": round(ops / (k["k_i8mm"] * 1e-3) / PEAK_INT8, 4)
@@ -623,7 +623,7 @@ def main():
             "ms": round(t, 5), "ms_cold": round(tc, 5),
             "roofline": roofline("hbm", c["bytes"], k["k_dwconv_pool"], "k_dwconv3_pool_rs",
                                  "163.8 MB per launch: the input read and the pooled output written "
-                                 "once (section 8(d), fused)", "k_dwconv_pool_cfg4a"),
+                                 "once (fused)", "k_dwconv_pool_cfg4a"),
             "frac_hbm_cold_step": round(c["bytes"] / (tc * 1e-3) / PEAK_HBM, 4)}
 
         # 4(b): grouped conv + ReLU + MaxPool fused; the two-launch path beside
@@ -648,7 +648,7 @@ def main():
             "ms_two_launches": round(t2, 5),
             "roofline": roofline("hbm", c["bytes"], k["k_gconv_pool"], "k_gconv3_pool_img<1>",
                                  f"{c['bytes'] / 1e6:.2f} MB per launch (input once, pooled output "
-                                 "once); launch-bound at this size (section 8(d))"),
+                                 "once); launch-bound at this size"),
             "kernel_ms": k}
 
         # 5: ResNet-50-style, batch 64, fp32 and int8
