@@ -83,6 +83,7 @@ SIGNATURES = {
     "acfun_dev_model_infer_batch": (_i, [_p, _i, _p, _p, _p]),
     "acfun_prof_enable": (None, [_i]),
     "acfun_prof_kernel_ms": (C.c_double, [_s, C.POINTER(_i)]),
+    "acfun_prof_report": (_i, [C.c_char_p, _i]),
 }
 
 
@@ -125,6 +126,28 @@ def lib():
                               "`python -c 'import __graft_entry__ as g; g.build()'`")
         _lib = bind(C.CDLL(LIB_PATH), required=SIGNATURES.keys())
     return _lib
+
+
+def prof_report():
+    """acfun_prof_report as (kernels, layers): kernels maps (tag, name) to
+    (launches, total ms); layers is a list of per-layer dicts."""
+    L = lib()
+    n = L.acfun_prof_report(None, 0)
+    if n < 0:
+        raise RuntimeError(last_error())
+    buf = C.create_string_buffer(n)
+    if L.acfun_prof_report(buf, n) < 0:
+        raise RuntimeError(last_error())
+    kernels, layers = {}, []
+    keys = ("i", "type", "N", "H", "W", "C", "OH", "OW", "OC", "KH", "KW", "stride", "pad",
+            "groups", "int8", "fused_into", "act", "residual")
+    for ln in buf.value.decode().splitlines():
+        f = ln.split("\t")
+        if f[0] == "K":
+            kernels[(int(f[1]), f[2])] = (int(f[3]), float(f[4]))
+        elif f[0] == "L":
+            layers.append(dict(zip(keys, map(int, f[1:]))))
+    return kernels, layers
 
 
 def last_error():

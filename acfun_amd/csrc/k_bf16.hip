@@ -205,7 +205,7 @@ bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, f
         set_error("acfun_gemm_bf16: operands too large");
         return false;
     }
-    hipLaunchKernelGGL(k_pack_bf16, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, A, B, M, N, K, K, ldb, Kp,
+    ACFUN_LAUNCH("k_pack_bf16", k_pack_bf16, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, A, B, M, N, K, K, ldb, Kp,
                        (int)nba, ab.as<unsigned short>(), bt.as<unsigned short>());
     if (!check_launch("k_pack_bf16")) return false;
     static bool attr = false;

@@ -370,7 +370,7 @@ bool run(GemmP p, int batch, bool va, bool vb, hipStream_t s, const TileCfg* for
     p.act = 0;
     if (!launch_cfg<CONV>(p, 1, va, vb, c, s)) return false;
     long long total = plane;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+    ACFUN_LAUNCH("k_splitk_reduce", k_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                        ws.as<float>(), splits, plane, p.M, p.N, C, ldc, bias, act);
     return check_launch("k_splitk_reduce");
 }
@@ -486,7 +486,7 @@ bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const f
 
 bool round_bf16(const float* in, float* out, size_t n, hipStream_t s) {
     if (!n) return true;
-    hipLaunchKernelGGL(k_round_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
+    ACFUN_LAUNCH("k_round_bf16", k_round_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
     return check_launch("k_round_bf16");
 }
 

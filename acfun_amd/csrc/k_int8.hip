@@ -796,7 +796,7 @@ bool alloc_weights(int taps, int Cinp, int N, hipStream_t s, PrepW& w) {
 }
 bool prep_weights(const int8_t* wq, int taps, int Cin, int Cinp, int N, hipStream_t s, PrepW& w) {
     if (!alloc_weights(taps, Cinp, N, s, w)) return false;
-    hipLaunchKernelGGL(k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N,
+    ACFUN_LAUNCH("k_prep_weights", k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N,
                        w.bt.as<int8_t>(), w.ldb, w.sw.as<int>());
     return check_launch("k_prep_weights");
 }
@@ -805,13 +805,13 @@ bool prep_weights(const int8_t* wq, int taps, int Cin, int Cinp, int N, hipStrea
 
 bool quantize_weights_dev(const float* w, int K, int N, float* scales, int8_t* wq, hipStream_t s) {
     if (K <= 0 || N <= 0) return true;
-    hipLaunchKernelGGL(k_quant_weights, g1(N), dim3(256), 0, s, w, K, N, scales, wq);
+    ACFUN_LAUNCH("k_quant_weights", k_quant_weights, g1(N), dim3(256), 0, s, w, K, N, scales, wq);
     return check_launch("k_quant_weights");
 }
 
 bool quantize_u8_dev(const float* in, uint8_t* out, size_t n, float inv_s, int zp, hipStream_t s) {
     if (!n) return true;
-    hipLaunchKernelGGL(k_quant_u8, g1((long long)n), dim3(256), 0, s, in, out, n, inv_s, zp);
+    ACFUN_LAUNCH("k_quant_u8", k_quant_u8, g1((long long)n), dim3(256), 0, s, in, out, n, inv_s, zp);
     return check_launch("k_quant_u8");
 }
 
@@ -842,7 +842,7 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
     long long pix = (long long)g.N * g.H * g.W;
     Scratch q((size_t)pix * Cinp, s);
     if (!q.p) return false;
-    hipLaunchKernelGGL(k_u8_to_s8, g1(pix * Cinp), dim3(256), 0, s, inQ, pix, g.Cin, Cinp, q.as<int8_t>());
+    ACFUN_LAUNCH("k_u8_to_s8", k_u8_to_s8, g1(pix * Cinp), dim3(256), 0, s, inQ, pix, g.Cin, Cinp, q.as<int8_t>());
     if (!check_launch("k_u8_to_s8")) return false;
     PrepW w;
     if (!prep_weights(wq, g.KH * g.KW, g.Cin, Cinp, Cout, s, w)) return false;
@@ -904,13 +904,13 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         int nb = amax_in ? 0 : (int)((n4 + 1023) / 1024);
         if (!amax_in) nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
         if (nb + (prepared ? 0 : Cout) > 0) {
-            hipLaunchKernelGGL(k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
+            ACFUN_LAUNCH("k_absmax_prep", k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
                                inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, nbt, ldb, nsw);
             if (!check_launch("k_absmax_prep")) return false;
         }
         const long long groups = pix * (Cinp / 16);
         const long long qb = std::min((groups + 255) / 256, 8ll * num_cus());
-        hipLaunchKernelGGL(k_quant16, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin, Cinp,
+        ACFUN_LAUNCH("k_quant16", k_quant16, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin, Cinp,
                            q, amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
                            scal, wino ? 2 : 0, g.Cin & ~15);
         if (!check_launch("k_quant16")) return false;
@@ -934,7 +934,7 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         return false;
     }
     if (!prepared) {
-        hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
+        ACFUN_LAUNCH("k_prep_weights", k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
                            Cinp, Cout, nbt, ldb, nsw);
         if (!check_launch("k_prep_weights")) return false;
     }
@@ -946,16 +946,16 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
     float* alpha = scal + 8;
     float* beta = alpha + Cout;
     float* alpha_w = beta + Cout;
-    hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, s, bits, 1, 0u);
+    ACFUN_LAUNCH("k_fill_u32", k_fill_u32, dim3(1), dim3(64), 0, s, bits, 1, 0u);
     if (!check_launch("k_fill_u32")) return false;
     int nb = (int)((inN / 4 + 255) / 256);
     nb = nb < 1 ? 1 : (nb > 4 * num_cus() ? 4 * num_cus() : nb);
-    hipLaunchKernelGGL(k_absmax, dim3(nb), dim3(256), 0, s, in, inN, bits);
+    ACFUN_LAUNCH("k_absmax", k_absmax, dim3(nb), dim3(256), 0, s, in, inN, bits);
     if (!check_launch("k_absmax")) return false;
-    hipLaunchKernelGGL(k_int8_params, g1(Cout), dim3(256), 0, s, bits, ws, bias, sw,
+    ACFUN_LAUNCH("k_int8_params", k_int8_params, g1(Cout), dim3(256), 0, s, bits, ws, bias, sw,
                        Cout, alpha, beta, alpha_w, scal);
     if (!check_launch("k_int8_params")) return false;
-    hipLaunchKernelGGL(k_quant_act, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp,
+    ACFUN_LAUNCH("k_quant_act", k_quant_act, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp,
                        q, scal, wino ? 2 : 0, g.Cin & ~15);
     if (!check_launch("k_quant_act")) return false;
     I8P p{};
@@ -973,7 +973,7 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         const size_t outN = (size_t)g.N * g.OH * g.OW * Cout;
         int nbo = (int)((outN / 4 + 1023) / 1024);
         nbo = nbo < 1 ? 1 : (nbo > kAmaxParts ? kAmaxParts : nbo);
-        hipLaunchKernelGGL(k_absmax_part, dim3(nbo), dim3(256), 0, s, out, outN, amax_out);
+        ACFUN_LAUNCH("k_absmax_part", k_absmax_part, dim3(nbo), dim3(256), 0, s, out, outN, amax_out);
         if (!check_launch("k_absmax_part")) return false;
     }
     return true;
@@ -1081,7 +1081,7 @@ bool conv2d_int8_q8_dev(const int8_t* q, int ldq_in, const float* s_in, const Co
         int8_t* nbt = (int8_t*)ar.get((size_t)Cout * ldb);
         int* nsw = (int*)ar.get((size_t)Cout * sizeof(int));
         if (!nbt || !nsw) return false;
-        hipLaunchKernelGGL(k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
+        ACFUN_LAUNCH("k_prep_weights", k_prep_weights, dim3(Cout), dim3(256), 0, s, wq, g.KH * g.KW, g.Cin,
                            Cinp, Cout, nbt, ldb, nsw);
         if (!check_launch("k_prep_weights")) return false;
         bt = nbt; sw = nsw;
@@ -1124,7 +1124,7 @@ bool conv2d_int8_q8_api(const int8_t* in, const float* s_in, const ConvShape& g,
     if (g.Cin != Cinp || ((uintptr_t)in & 15u)) {
         int8_t* t = (int8_t*)ar.get((size_t)pix * Cinp);
         if (!t) return false;
-        hipLaunchKernelGGL(k_s8_repad, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp, t);
+        ACFUN_LAUNCH("k_s8_repad", k_s8_repad, g1(pix * Cinp), dim3(256), 0, s, in, pix, g.Cin, Cinp, t);
         if (!check_launch("k_s8_repad")) return false;
         qin = t;
     }
@@ -1138,7 +1138,7 @@ bool conv2d_int8_q8_api(const int8_t* in, const float* s_in, const ConvShape& g,
                             s, nullptr))
         return false;
     if (!direct) {
-        hipLaunchKernelGGL(k_s8_repad, g1(pixo * Cout), dim3(256), 0, s, qo, pixo, Coutp, Cout, out);
+        ACFUN_LAUNCH("k_s8_repad", k_s8_repad, g1(pixo * Cout), dim3(256), 0, s, qo, pixo, Coutp, Cout, out);
         if (!check_launch("k_s8_repad")) return false;
     }
     return true;
@@ -1153,10 +1153,10 @@ bool winograd_int8_dev(const float* in, int N, int H, int W, int Cin, const int8
     Scratch q((size_t)pix * Cinp, s);
     Scratch aw((size_t)Cout * sizeof(float), s);
     if (!q.p || !aw.p) return false;
-    hipLaunchKernelGGL(k_quant_act_inv, g1(pix * Cinp), dim3(256), 0, s, in, pix, Cin, Cinp,
+    ACFUN_LAUNCH("k_quant_act_inv", k_quant_act_inv, g1(pix * Cinp), dim3(256), 0, s, in, pix, Cin, Cinp,
                        q.as<int8_t>(), inv_s, Cin & ~15);
     if (!check_launch("k_quant_act_inv")) return false;
-    hipLaunchKernelGGL(k_alpha_w, g1(Cout), dim3(256), 0, s, ws, s_in, Cout, aw.as<float>());
+    ACFUN_LAUNCH("k_alpha_w", k_alpha_w, g1(Cout), dim3(256), 0, s, ws, s_in, Cout, aw.as<float>());
     if (!check_launch("k_alpha_w")) return false;
     PrepW w;
     if (!prep_weights(wq, 9, Cin, Cinp, Cout, s, w)) return false;
@@ -1185,7 +1185,7 @@ bool i8_prepare(const int8_t* wq, int taps, int Cin, int N, I8Weights& w, hipStr
         return false;
     }
     w.taps = taps; w.Cin = Cin; w.N = N;
-    hipLaunchKernelGGL(k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N, w.bt,
+    ACFUN_LAUNCH("k_prep_weights", k_prep_weights, dim3(N), dim3(256), 0, s, wq, taps, Cin, Cinp, N, w.bt,
                        w.ldb, w.sw);
     return check_launch("k_prep_weights");
 }

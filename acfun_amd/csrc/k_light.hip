@@ -1198,31 +1198,31 @@ bool maxpool_f32(const float* in, int N, int H, int W, int C, int pool, int stri
 
 bool relu_f32(float* d, size_t n, int six, hipStream_t s) {
     if (!n) return true;
-    hipLaunchKernelGGL(k_relu, grid1d((long long)n), dim3(256), 0, s, d, n, six);
+    ACFUN_LAUNCH("k_relu", k_relu, grid1d((long long)n), dim3(256), 0, s, d, n, six);
     return check_launch("k_relu");
 }
 
 bool fill_f32(float* d, size_t n, float v, hipStream_t s) {
     if (!n) return true;
-    hipLaunchKernelGGL(k_fill, grid1d((long long)n), dim3(256), 0, s, d, n, v);
+    ACFUN_LAUNCH("k_fill", k_fill, grid1d((long long)n), dim3(256), 0, s, d, n, v);
     return check_launch("k_fill");
 }
 
 bool add_relu_f32(const float* a, const float* b, float* y, size_t n, int act, hipStream_t s) {
     if (!n) return true;
-    hipLaunchKernelGGL(k_add_relu, grid1d((long long)n), dim3(256), 0, s, a, b, y, n, act);
+    ACFUN_LAUNCH("k_add_relu", k_add_relu, grid1d((long long)n), dim3(256), 0, s, a, b, y, n, act);
     return check_launch("k_add_relu");
 }
 
 bool gap_f32(const float* x, int N, int HW, int C, float* y, hipStream_t s) {
     if (N <= 0 || C <= 0 || HW <= 0) return true;
-    hipLaunchKernelGGL(k_gap, grid1d((long long)N * C), dim3(256), 0, s, x, N, HW, C, y);
+    ACFUN_LAUNCH("k_gap", k_gap, grid1d((long long)N * C), dim3(256), 0, s, x, N, HW, C, y);
     return check_launch("k_gap");
 }
 
 bool softmax_f32(const float* in, int rows, int cols, float* out, hipStream_t s) {
     if (rows <= 0 || cols <= 0) return true;
-    hipLaunchKernelGGL(k_softmax, dim3(rows), dim3(256), 0, s, in, cols, out);
+    ACFUN_LAUNCH("k_softmax", k_softmax, dim3(rows), dim3(256), 0, s, in, cols, out);
     return check_launch("k_softmax");
 }
 
@@ -1230,7 +1230,7 @@ bool batchnorm_f32(float* d, int size, int channels, const float* mean, const fl
                    const float* gamma, const float* beta, float eps, hipStream_t s) {
     if (size <= 0 || channels <= 0) return true;
     long long total = (long long)(size / channels) * channels;
-    hipLaunchKernelGGL(k_batchnorm, grid1d(total), dim3(256), 0, s, d, total, channels, mean, var,
+    ACFUN_LAUNCH("k_batchnorm", k_batchnorm, grid1d(total), dim3(256), 0, s, d, total, channels, mean, var,
                        gamma, beta, eps);
     return check_launch("k_batchnorm");
 }
@@ -1239,7 +1239,7 @@ bool group_split_copy(const float* src, int pix, int srcC, int off, int cnt, flo
                       int dstOff, hipStream_t s) {
     long long total = (long long)pix * cnt;
     if (!total) return true;
-    hipLaunchKernelGGL(k_chan_copy, grid1d(total), dim3(256), 0, s, src, pix, srcC, off, cnt, dst,
+    ACFUN_LAUNCH("k_chan_copy", k_chan_copy, grid1d(total), dim3(256), 0, s, src, pix, srcC, off, cnt, dst,
                        dstC, dstOff);
     return check_launch("k_chan_copy");
 }

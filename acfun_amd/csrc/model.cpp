@@ -331,6 +331,7 @@ struct Dims { int H, W, C; };
 
 // Runs the fused layers on N images resident in HBM.
 int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s) {
+    struct TagReset { ~TagReset() { prof_tag(-1); } } tag_reset;   // launches after the layers are untagged
     const int L = (int)m->layers.size();
     // Shapes and last uses (liveness) of every fused output.
     std::vector<Dims> out(L);
@@ -427,12 +428,26 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
     cur = Dims{m->inH, m->inW, m->inC};
     const float* x = din;
     int xi = -1;
+    const bool prof = prof_on();
     for (int i = 0; i < L; ++i) {
         Layer& F = m->layers[i];
         Dims in = cur;
         if (F.type == 10) { x = tensor_of(F.from); xi = F.from; in = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from]; }
         Dims o = out[i];
         size_t cap = (size_t)N * o.H * o.W * o.C;
+        if (prof) {
+            // i type N H W C -> OH OW OC, kernel, stride, pad, groups, int8, fused-into, act, residual
+            char rec[192];
+            const bool conv = F.type == 1 || F.type == 7;
+            snprintf(rec, sizeof(rec), "%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d\t%d",
+                     i, F.type, N, in.H, in.W, in.C, o.H, o.W, o.C, conv ? F.p[0] : 0,
+                     conv ? F.p[1] : 0, conv ? F.p[3] : 0, conv ? F.p[4] : 0,
+                     F.type == 7 ? F.p[5] : 1, (m->int8 && F.type == 1 && F.wq) ? 1 : 0,
+                     alias[i] != -2 && F.type != 10 ? alias[i] : -2,
+                     act_of[i] >= 0 ? act_of[i] : F.act, res_of[i] != -3 ? 1 : 0);
+            prof_layer(rec);
+            prof_tag(i);
+        }
         if (alias[i] != -2) {                        // fused into the previous layer, or an Input
             buf[i] = const_cast<float*>(tensor_of(alias[i]));
             if (alias[i] >= 0) amax_of[i] = amax_of[alias[i]];
@@ -544,6 +559,7 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         x = y;
         xi = i;
     }
+    prof_tag(-1);
     size_t per = (size_t)cur.H * cur.W * cur.C;
     if (L == 0) per = (size_t)m->inH * m->inW * m->inC;
     if (!check(hipMemcpyAsync(dout, x, (size_t)N * per * sizeof(float), hipMemcpyDeviceToDevice, s), "D2D out"))

@@ -28,6 +28,12 @@ bool check_launch(const char* kernel);
 // the time from the later of its start and the previous timed kernel's stop
 // on the same stream to its stop.  Disabled: a plain launch.
 bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_t* stop);
+// Tag for the launches that follow (a model executor sets its layer index;
+// -1 outside a model), and one text record per executed model layer; both
+// are reported by acfun_prof_report while timing is enabled.
+void prof_tag(int tag);
+bool prof_on();
+void prof_layer(const char* record);
 #define ACFUN_LAUNCH(NAME, KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                               \
     do {                                                                                        \
         hipEvent_t acfun_ev0_, acfun_ev1_;                                                      \
@@ -90,11 +96,14 @@ int num_cus();
 inline hipStream_t resolve(void* s) { return s ? (hipStream_t)s : lib_stream(); }
 
 // ----------------------------------------------------------------- memory
-// Stream-ordered caching pool: a block returned with pool_free(p, s) is only
-// handed out again for work queued on the same stream s, so reuse is ordered
-// after every kernel that used it.
+// Stream-ordered caching pool (policy in pool.hpp): a block returned with
+// pool_free(p, s) is handed out again for work on s (ordered after every
+// kernel that used it); blocks cached on other streams, including streams
+// the caller has since destroyed, are reclaimed for any stream by one device
+// synchronization once they add up to 64 MiB.
 void* pool_alloc(size_t bytes, hipStream_t s);
 void pool_free(void* p, hipStream_t s);
+size_t pool_cached_bytes();   // bytes held in the free lists
 
 // RAII scratch buffer from the pool.
 struct Scratch {

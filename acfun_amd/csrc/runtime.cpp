@@ -1,9 +1,11 @@
 // runtime.cpp -- device bring-up, library stream, caching pool, staging of
 // host buffers for the synchronous API, and the error string.
 #include "rt.hpp"
+#include "pool.hpp"
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -36,6 +38,7 @@ namespace {
 struct ProfLaunch {
     hipEvent_t start, stop;
     hipEvent_t prev;     // stop event of the previous timed launch on the stream (or null)
+    int tag;             // prof_tag() at the launch (a model's layer index; -1 outside models)
 };
 struct ProfKernel {
     std::vector<ProfLaunch> ev;                           // events created on demand, reused
@@ -43,9 +46,36 @@ struct ProfKernel {
 };
 std::map<hipStream_t, hipEvent_t> g_prof_last;            // last timed stop event per stream
 bool g_prof_on = false;
+int g_prof_tag = -1;
 std::map<std::string, ProfKernel> g_prof;
 std::mutex g_prof_mu;
+std::string g_prof_layers;                                // model layer records (prof_layer)
+
+// Duration of one recorded launch in ms (see acfun_prof_kernel_ms), -1 on error.
+double launch_ms(const ProfLaunch& e) {
+    if (hipEventSynchronize(e.stop) != hipSuccess) return -1.0;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, e.start, e.stop) != hipSuccess) return -1.0;
+    // A dispatch's start event can be signalled while it still waits for the
+    // previous kernel on its stream: count from that kernel's end then.
+    float since_prev = 0.f;
+    if (e.prev && hipEventElapsedTime(&since_prev, e.prev, e.stop) == hipSuccess &&
+        since_prev > 0.f && since_prev < ms)
+        ms = since_prev;
+    return ms;
+}
 }  // namespace
+
+void prof_tag(int tag) { g_prof_tag = tag; }
+
+bool prof_on() { return g_prof_on; }
+
+void prof_layer(const char* record) {
+    if (!g_prof_on) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof_layers += record;
+    g_prof_layers += '\n';
+}
 
 bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_t* stop) {
     if (!g_prof_on) return false;
@@ -55,9 +85,10 @@ bool prof_events(const char* kernel, hipStream_t s, hipEvent_t* start, hipEvent_
         hipEvent_t a, b;
         if (hipEventCreate(&a) != hipSuccess) return false;
         if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return false; }
-        k.ev.push_back(ProfLaunch{a, b, nullptr});
+        k.ev.push_back(ProfLaunch{a, b, nullptr, -1});
     }
     ProfLaunch& L = k.ev[k.used++];
+    L.tag = g_prof_tag;
     auto it = g_prof_last.find(s);
     L.prev = it == g_prof_last.end() ? nullptr : it->second;
     g_prof_last[s] = L.stop;
@@ -132,67 +163,32 @@ int num_cus() {
 
 // ------------------------------------------------------------------ memory
 namespace {
-// Blocks are rounded up so that similar sizes share a free list.
-size_t round_size(size_t b) {
-    if (b <= 4096) return 4096;
-    if (b <= (1u << 20)) return (b + 65535) & ~size_t(65535);
-    return (b + (1u << 20) - 1) & ~size_t((1u << 20) - 1);
-}
-struct PoolKey {
-    int dev;
-    hipStream_t s;
-    size_t bytes;
-    bool operator<(const PoolKey& o) const {
-        if (dev != o.dev) return dev < o.dev;
-        if (s != o.s) return s < o.s;
-        return bytes < o.bytes;
+// HIP side of the pool (pool.hpp).
+struct HipPoolBackend {
+    void* alloc(size_t bytes) {
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        return p;
     }
+    void release(void* p) { (void)hipFree(p); }
+    void sync_device() { (void)hipDeviceSynchronize(); }
 };
-std::mutex g_pool_mu;
-std::multimap<PoolKey, void*> g_free;
-std::map<void*, size_t> g_size;
+HipPoolBackend g_pool_backend;
+PoolCore<HipPoolBackend, hipStream_t> g_pool(g_pool_backend);
 }  // namespace
 
 void* pool_alloc(size_t bytes, hipStream_t s) {
-    size_t rb = round_size(bytes);
-    int d = current_device();
-    {
-        std::lock_guard<std::mutex> lk(g_pool_mu);
-        auto it = g_free.find(PoolKey{d, s, rb});
-        if (it != g_free.end()) {
-            void* p = it->second;
-            g_free.erase(it);
-            return p;
-        }
-    }
-    void* p = nullptr;
-    if (hipMalloc(&p, rb) != hipSuccess) {
-        // Release cached blocks of this device and retry once.
-        std::vector<void*> drop;
-        {
-            std::lock_guard<std::mutex> lk(g_pool_mu);
-            for (auto it = g_free.begin(); it != g_free.end();) {
-                if (it->first.dev == d) { drop.push_back(it->second); it = g_free.erase(it); }
-                else ++it;
-            }
-            for (void* q : drop) g_size.erase(q);
-        }
-        hipDeviceSynchronize();
-        for (void* q : drop) hipFree(q);
-        if (!check(hipMalloc(&p, rb), "hipMalloc")) return nullptr;
-    }
-    std::lock_guard<std::mutex> lk(g_pool_mu);
-    g_size[p] = rb;
+    void* p = g_pool.alloc(current_device(), bytes, s);
+    if (!p) set_error("hipMalloc: out of device memory (%zu bytes)", bytes);
     return p;
 }
 
-void pool_free(void* p, hipStream_t s) {
-    if (!p) return;
-    std::lock_guard<std::mutex> lk(g_pool_mu);
-    auto it = g_size.find(p);
-    if (it == g_size.end()) return;
-    g_free.emplace(PoolKey{current_device(), s, it->second}, p);
-}
+void pool_free(void* p, hipStream_t s) { g_pool.free(current_device(), p, s); }
+
+size_t pool_cached_bytes() { return g_pool.cached_bytes(current_device()); }
 
 void* Arena::get(size_t bytes) {
     if (!base_) {
@@ -278,6 +274,7 @@ extern "C" void acfun_prof_enable(int on) {
     if (on) {                            // a new measurement starts empty; off keeps the records
         for (auto& kv : acfun::g_prof) kv.second.used = 0;
         acfun::g_prof_last.clear();
+        acfun::g_prof_layers.clear();
     }
     acfun::g_prof_on = on != 0;
 }
@@ -290,19 +287,54 @@ extern "C" double acfun_prof_kernel_ms(const char* kernel, int* launches) {
     if (it == acfun::g_prof.end() || it->second.used == 0) return 0.0;
     double total = 0.0;
     for (size_t i = 0; i < it->second.used; ++i) {
-        auto& e = it->second.ev[i];
-        if (!acfun::check(hipEventSynchronize(e.stop), "acfun_prof_kernel_ms")) return -1.0;
-        float ms = 0.f;
-        if (!acfun::check(hipEventElapsedTime(&ms, e.start, e.stop), "acfun_prof_kernel_ms"))
+        const double ms = acfun::launch_ms(it->second.ev[i]);
+        if (ms < 0) {
+            acfun::set_error("acfun_prof_kernel_ms: HIP event query failed");
             return -1.0;
-        // A dispatch's start event can be signalled while it still waits for the
-        // previous kernel on its stream: count from that kernel's end then.
-        float since_prev = 0.f;
-        if (e.prev && hipEventElapsedTime(&since_prev, e.prev, e.stop) == hipSuccess &&
-            since_prev > 0.f && since_prev < ms)
-            ms = since_prev;
+        }
         total += ms;
     }
     if (launches) *launches = (int)it->second.used;
     return total / (double)it->second.used;
+}
+
+extern "C" int acfun_prof_report(char* buf, int len) {
+    std::string r;
+    {
+        std::lock_guard<std::mutex> lk(acfun::g_prof_mu);
+        // per (tag, kernel): launch count and summed duration
+        std::map<std::pair<int, std::string>, std::pair<int, double>> agg;
+        for (auto& kv : acfun::g_prof)
+            for (size_t i = 0; i < kv.second.used; ++i) {
+                const double ms = acfun::launch_ms(kv.second.ev[i]);
+                if (ms < 0) {
+                    acfun::set_error("acfun_prof_report: HIP event query failed");
+                    return -1;
+                }
+                auto& a = agg[{kv.second.ev[i].tag, kv.first}];
+                a.first += 1;
+                a.second += ms;
+            }
+        char line[256];
+        for (auto& kv : agg) {
+            snprintf(line, sizeof(line), "K\t%d\t%s\t%d\t%.6f\n", kv.first.first,
+                     kv.first.second.c_str(), kv.second.first, kv.second.second);
+            r += line;
+        }
+        size_t p = 0;
+        while (p < acfun::g_prof_layers.size()) {
+            size_t e = acfun::g_prof_layers.find('\n', p);
+            if (e == std::string::npos) e = acfun::g_prof_layers.size();
+            r += "L\t";
+            r += acfun::g_prof_layers.substr(p, e - p);
+            r += '\n';
+            p = e + 1;
+        }
+    }
+    if (buf && len > 0) {
+        const size_t n = std::min(r.size(), (size_t)len - 1);
+        memcpy(buf, r.data(), n);
+        buf[n] = 0;
+    }
+    return (int)r.size() + 1;
 }

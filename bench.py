@@ -48,9 +48,15 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
     ap.add_argument("--profile", metavar="CFG", default=None,
-                    help="for rocprofv3 --pmc runs: 5 steps of CFG (cfg1, cfg2a, cfg2b, cfg3a, "
+                    help="for rocprofv3 runs: 5 steps of CFG (cfg1, cfg2a, cfg2b, cfg3a, "
                          "cfg3b, cfg3a_q, cfg3b_q, cfg4a, cfg4b), then 3 plain copies of 256 MiB "
-                         "(the counter scale reference); prints no JSON line")
+                         "(the counter scale reference); prints no JSON line.  cfg5_fp32 / "
+                         "cfg5_int8: two batch-64 inferences of the config-5 model (the first "
+                         "makes its Winograd filter transforms), the second timed per layer "
+                         "(--layers-md)")
+    ap.add_argument("--layers-md", metavar="PATH", default=None,
+                    help="with --profile cfg5_*: write the per-layer table of the second batch "
+                         "(markdown) to PATH")
     ap.add_argument("--traffic", action="store_true", help="the same as --profile cfg2a")
     ap.add_argument("--tune", action="store_true",
                     help="run the tile search (acfun_autotune) over every config's shapes first, as "
@@ -130,6 +136,138 @@ def roofline(bound, work, ms, kernel, work_note, traffic_name=None):
             "frac": round(ach / peak, 4) if ach else None,
             "traffic": read_traffic(traffic_name) if traffic_name else None,
             "kernel": kernel, "kernel_ms": round(ms, 5) if ms else None, "work": work_note}
+
+
+# ------------------------------------------------------------------ config 5 per layer
+LAYER_TYPES = {1: "conv", 2: "fc", 3: "relu", 4: "maxpool", 5: "softmax", 6: "bn", 7: "convg",
+               8: "add", 9: "gap", 10: "input"}
+
+
+def layer_work(L, names):
+    """Executed work of one model layer, from its shape and the kernels that
+    ran it: (fp32 MFMA FLOPs, int8 MFMA ops, compulsory HBM bytes).
+    F(2,3) / F(4,3) layers count the transform-domain products the algorithm
+    needs (2 * tiles * points * Cin * Cout, no padding), other convs and the FC
+    the direct 2 * M * N * K; bytes are the input read, the output written and
+    the weights once (fp32 activations, as the model keeps them)."""
+    import math
+    N, H, W, C, OH, OW, OC = (L[k] for k in ("N", "H", "W", "C", "OH", "OW", "OC"))
+    t = L["type"]
+    fp32 = int8 = 0.0
+    act_in, act_out = 4.0 * N * H * W * C, 4.0 * N * OH * OW * OC
+    wbytes = 0.0
+    if t in (1, 7):
+        KH, KW, g = L["KH"], L["KW"], max(1, L["groups"])
+        direct = 2.0 * N * OH * OW * OC * KH * KW * (C // g)
+        wbytes = KH * KW * (C // g) * OC * (1.0 if L["int8"] else 4.0)
+        if L["int8"]:
+            int8 = direct
+        elif any(n.startswith("k_wino23") for n in names):
+            fp32 = 2.0 * N * math.ceil(OH / 2) * math.ceil(OW / 2) * 16 * C * OC
+        elif any(n.startswith(("k_wino43", "k_wino_fused")) for n in names):
+            fp32 = 2.0 * N * math.ceil(OH / 4) * math.ceil(OW / 4) * 36 * C * OC
+        else:
+            fp32 = direct
+        if L["residual"]:
+            act_out *= 2
+    elif t == 2:
+        fp32 = 2.0 * N * H * W * C * OC
+        wbytes = 4.0 * H * W * C * OC
+    elif t == 8:
+        act_in *= 2
+    return fp32, int8, act_in + act_out + wbytes
+
+
+def model_layer_profile(lib, run):
+    """Runs `run` (one inference) with kernel timing on and returns the layers
+    that launched kernels: shape, kernels with their summed ms, executed work
+    and the layer's roofline floor (max of MFMA time at peak and HBM time)."""
+    from acfun_amd import capi
+    lib.acfun_prof_enable(1)
+    run()
+    lib.acfun_prof_enable(0)
+    kernels, layers = capi.prof_report()
+    rows = []
+    for L in layers:
+        ks = {name: v for (tag, name), v in kernels.items() if tag == L["i"]}
+        if not ks:
+            continue
+        fp32, int8, byt = layer_work(L, ks)
+        ms = sum(v[1] for v in ks.values())
+        floor = max(fp32 / PEAK_FP32 + int8 / PEAK_INT8, byt / PEAK_HBM) * 1e3
+        rows.append(dict(L, kernels=ks, ms=ms, fp32=fp32, int8=int8, bytes=byt, floor_ms=floor))
+    untagged = {name: v for (tag, name), v in kernels.items() if tag < 0}
+    return rows, untagged
+
+
+def layer_table_md(rows, untagged, tag):
+    """Markdown: the layers grouped by shape and route, largest time first."""
+    groups = {}
+    for r in rows:
+        shape = (f"{LAYER_TYPES.get(r['type'], r['type'])} {r['KH']}x{r['KW']}/{r['stride']} "
+                 f"{r['H']}x{r['W']}x{r['C']} -> {r['OH']}x{r['OW']}x{r['OC']}"
+                 + (" +add" if r["residual"] else "") if r["type"] in (1, 7) else
+                 f"{LAYER_TYPES.get(r['type'], r['type'])} {r['H']}x{r['W']}x{r['C']} -> "
+                 f"{r['OH']}x{r['OW']}x{r['OC']}")
+        key = (shape, " + ".join(sorted(r["kernels"])))
+        g = groups.setdefault(key, dict(n=0, ms=0.0, fp32=0.0, int8=0.0, bytes=0.0, floor=0.0))
+        g["n"] += 1
+        g["ms"] += r["ms"]
+        g["fp32"] += r["fp32"]
+        g["int8"] += r["int8"]
+        g["bytes"] += r["bytes"]
+        g["floor"] += r["floor_ms"]
+    total = sum(g["ms"] for g in groups.values())
+    out = [f"| layer shape (per batch of {rows[0]['N'] if rows else 0}) | kernels | layers | ms | share | "
+           "executed GFLOP fp32 / GOP int8 | TFLOP/s (TOP/s) | frac of peak | floor ms | time / floor |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for (shape, ks), g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"]):
+        work = g["int8"] if g["int8"] else g["fp32"]
+        peak = PEAK_INT8 if g["int8"] else PEAK_FP32
+        rate = work / (g["ms"] * 1e-3) / 1e12 if g["ms"] and work else 0.0
+        out.append(f"| {shape} | {ks} | {g['n']} | {g['ms']:.4f} | {g['ms'] / total:.3f} | "
+                   + (f"{g['int8'] / 1e9:.2f} (int8)" if g["int8"] else f"{g['fp32'] / 1e9:.2f}")
+                   + f" | {rate:.1f} | {rate * 1e12 / peak:.3f} | {g['floor']:.4f} | "
+                   f"{g['ms'] / g['floor'] if g['floor'] else 0:.2f} |")
+    if untagged:
+        out.append("")
+        out.append("Launches outside the layers (the model's input/output copies are not kernels): "
+                   + ", ".join(f"{k} {v[0]}x {v[1]:.4f} ms" for k, v in sorted(untagged.items())))
+    kern = {}
+    for r in rows:
+        for name, (n, ms) in r["kernels"].items():
+            a = kern.setdefault(name, [0, 0.0])
+            a[0] += n
+            a[1] += ms
+    out.append("")
+    out.append(f"Per kernel name ({tag}, this batch): | kernel | launches | total ms |")
+    out.append("|---|---|---|")
+    for name, (n, ms) in sorted(kern.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| {name} | {n} | {ms:.4f} |")
+    return "\n".join(out) + "\n"
+
+
+def cfg5_roofline(rows, step_ms, int8):
+    """Config 5's roofline block: the batch's executed MFMA work over the step
+    time (fp32 model: fp32 FLOPs; int8 model: the int8 convs' ops), plus the
+    sum of per-layer floors over the step time."""
+    fp32 = sum(r["fp32"] for r in rows)
+    i8 = sum(r["int8"] for r in rows)
+    floor = sum(r["floor_ms"] for r in rows)
+    kern_ms = sum(r["ms"] for r in rows)
+    if int8:
+        blk = roofline("mfma-int8", i8, step_ms, "whole batch (every layer's kernels)",
+                       f"executed int8 MFMA ops of the int8 convs, {i8 / 1e9:.1f} GOP per batch "
+                       f"(the fp32 FC: {fp32 / 1e9:.2f} GFLOP, not counted), over the step time")
+    else:
+        blk = roofline("mfma-fp32", fp32, step_ms, "whole batch (every layer's kernels)",
+                       f"executed fp32 MFMA FLOPs, {fp32 / 1e9:.1f} GFLOP per batch: F(2,3) "
+                       "transform-domain products for the Winograd layers, direct 2*M*N*K for "
+                       "the others, over the step time")
+    blk["frac_of_layer_floors"] = round(floor / step_ms, 4) if step_ms else None
+    blk["layer_floor_ms"] = round(floor, 4)
+    blk["kernels_ms"] = round(kern_ms, 4)
+    return blk
 
 
 # ------------------------------------------------------------------ the configs
@@ -257,6 +395,28 @@ def make_configs(lib, torch, dev, sp, rng, check):
     inC, inH, inW, recs = acfun0.resnet50(np.random.default_rng(5))
     cfg["cfg5"] = dict(recs=(inC, inH, inW, recs))
     return cfg
+
+
+def load_cfg5(lib, torch, dev, rng, cfg, int8):
+    """Writes config 5's version-2 ResNet-50 to a temporary file and loads it
+    (int8: flags 1); returns (model, path, input [64,224,224,3], output)."""
+    import numpy as np
+
+    from acfun_amd import acfun0
+    inC, inH, inW, recs = cfg["cfg5"]["recs"]
+    fd, path = tempfile.mkstemp(suffix=".acfun")
+    os.close(fd)
+    acfun0.write(path, inC, inH, inW, recs, version=2)
+    xin = torch.from_numpy(rng.uniform(0, 1, (64, inH, inW, inC)).astype(np.float32)).to(dev)
+    out = torch.empty((64, 1000), device=dev)
+    m = lib.acfun_model_load_ex(path.encode(), 1 if int8 else 0)
+    return m, path, xin, out
+
+
+def check_infer(lib, m, xin, out, sp):
+    from acfun_amd import capi
+    if lib.acfun_dev_model_infer_batch(m, 64, xin.data_ptr(), out.data_ptr(), sp) != 1000:
+        raise RuntimeError(capi.last_error())
 
 
 def rotation_sets(x, y, extra=0, total=320 << 20):
@@ -474,6 +634,22 @@ def main():
 
     if args.traffic:
         args.profile = "cfg2a"
+    if args.profile in ("cfg5_fp32", "cfg5_int8"):
+        int8 = args.profile == "cfg5_int8"
+        m, path, xin, out = load_cfg5(lib, torch, dev, rng, cfg, int8)
+        run = lambda: check_infer(lib, m, xin, out, sp)
+        run()                                          # makes the Winograd filter transforms
+        torch.cuda.synchronize()
+        rows, untagged = model_layer_profile(lib, run)
+        torch.cuda.synchronize()
+        lib.acfun_model_destroy(m)
+        os.unlink(path)
+        md = layer_table_md(rows, untagged, args.profile)
+        if args.layers_md:
+            with open(args.layers_md, "w") as f:
+                f.write(md)
+        print(md, flush=True)
+        return
     if args.profile:
         if args.profile not in cfg or "step" not in cfg[args.profile]:
             raise SystemExit(f"bench.py: no configuration {args.profile!r}")
@@ -652,31 +828,23 @@ def main():
             "kernel_ms": k}
 
         # 5: ResNet-50-style, batch 64, fp32 and int8
-        inC, inH, inW, recs = cfg["cfg5"]["recs"]
-        fd, path = tempfile.mkstemp(suffix=".acfun")
-        os.close(fd)
-        acfun0.write(path, inC, inH, inW, recs, version=2)
-        xin = torch.from_numpy(rng.uniform(0, 1, (64, 224, 224, 3)).astype(np.float32)).to(dev)
-        out = torch.empty((64, 1000), device=dev)
-        gfl = acfun0.resnet50_flops()
-        for tag, flags in (("fp32", 0), ("int8", 1)):
-            m = lib.acfun_model_load_ex(path.encode(), flags)
+        for tag, int8 in (("fp32", False), ("int8", True)):
+            m, path, xin, out = load_cfg5(lib, torch, dev, rng, cfg, int8)
             if not m:
                 configs[f"cfg5_resnet50_b64_{tag}"] = {"error": capi.last_error()}
                 continue
-
-            def s6():
-                if lib.acfun_dev_model_infer_batch(m, 64, xin.data_ptr(), out.data_ptr(), sp) != 1000:
-                    raise RuntimeError(capi.last_error())
+            s6 = lambda m=m, xin=xin, out=out: check_infer(lib, m, xin, out, sp)
             t = T.run(s6, max(3, steps // 4), 2)
-            peak = PEAK_FP32 if tag == "fp32" else PEAK_INT8
+            rows, _ = model_layer_profile(lib, s6)
+            gfl = acfun0.resnet50_flops()
             configs[f"cfg5_resnet50_b64_{tag}"] = {
                 "ms": round(t, 3), "images_per_s": round(64 / (t * 1e-3), 1),
-                "TFLOPS": round(64 * gfl / (t * 1e-3) / 1e12, 3),
-                "frac_peak": round(64 * gfl / (t * 1e-3) / peak, 4),
-                "work": f"{gfl / 1e9:.2f} GFLOP per image (convs and FC, direct count)"}
+                "TFLOPS_direct_equivalent": round(64 * gfl / (t * 1e-3) / 1e12, 3),
+                "direct_work": f"{gfl / 1e9:.2f} GFLOP per image (convs and FC, direct count)",
+                "roofline": cfg5_roofline(rows, t, int8),
+                "per_layer": "profiles/kernels_cfg5_%s.md (bench.py --profile cfg5_%s)" % (tag, tag)}
             lib.acfun_model_destroy(m)
-        os.unlink(path)
+            os.unlink(path)
     line["configs"] = configs
     line["config"]["tile_search"] = lib.acfun_tune_status().decode()
 

@@ -269,14 +269,21 @@ int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float*
                                 void* stream);
 
 /* Kernel timing for measurement.  acfun_prof_enable(1) clears the records and
- * starts launching the library's main kernels (k_wino23, k_wino_fused,
- * k_gemm_f32, k_igemm_i8, k_dwconv, k_gconv, k_maxpool) with HIP start/stop
- * events that the dispatch itself signals; acfun_prof_enable(0) stops.
+ * starts launching every kernel of the library with HIP start/stop events that
+ * the dispatch itself signals; acfun_prof_enable(0) stops.
  * acfun_prof_kernel_ms() waits for the recorded events and returns the mean
  * execution time in ms of the named kernel (0 if none, -1 on a HIP error) and
  * the launch count in *launches (may be NULL). */
 void acfun_prof_enable(int on);
 double acfun_prof_kernel_ms(const char* kernel, int* launches);
+/* The records as text, one line each, tab-separated:
+ *   K  tag  kernel  launches  total_ms    per (tag, kernel name)
+ *   L  i type N H W C OH OW OC KH KW stride pad groups int8 fused_into act residual
+ *                                         per layer a model ran while timing
+ * tag is the model layer (fused index i of an L line) the launch belongs to,
+ * -1 outside model inference.  Writes at most len bytes (NUL-terminated) and
+ * returns the length the whole report needs (with the NUL), -1 on a HIP error. */
+int acfun_prof_report(char* buf, int len);
 
 #ifdef __cplusplus
 }

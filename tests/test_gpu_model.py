@@ -209,3 +209,38 @@ def test_model_winograd_cache_repeats(gpu, rng, tmp_path):
     finally:
         gpu.acfun_model_destroy(m)
 
+
+
+def test_model_layer_profile_tags(gpu, rng, tmp_path):
+    """acfun_prof_report: every kernel a model launches carries its layer's
+    index, every executed layer has a record with its shapes, and a launch
+    outside the model is untagged."""
+    inC, H, W, recs = acfun0.resnet50(rng, in_hw=32, width=8, blocks=(1, 1), classes=10)
+    path = _write(tmp_path, "r.acfun", inC, H, W, recs, 2)
+    m = _load(gpu, path)
+    x = rng.uniform(0, 1, (2, H, W, inC)).astype(np.float32)
+    y = np.zeros((2, 10), np.float32)
+    try:
+        assert gpu.acfun_model_infer_batch(m, 2, P(x), P(y)) == 10, capi.last_error()
+        gpu.acfun_prof_enable(1)
+        try:
+            assert gpu.acfun_model_infer_batch(m, 2, P(x), P(y)) == 10, capi.last_error()
+            A = rng.uniform(-1, 1, (64, 64)).astype(np.float32)
+            Cm = np.zeros((64, 64), np.float32)
+            gpu.acfun_gemm(64, 64, 64, P(A), P(A), P(Cm))
+        finally:
+            gpu.acfun_prof_enable(0)
+        kernels, layers = capi.prof_report()
+    finally:
+        gpu.acfun_model_destroy(m)
+    idx = {L["i"]: L for L in layers}
+    assert layers and all(L["N"] == 2 for L in layers)
+    tags = {t for (t, _) in kernels}
+    assert -1 in tags                                    # the GEMM after the model
+    assert tags - {-1} <= set(idx)                       # every tagged launch names a layer
+    convs = [L for L in layers if L["type"] == 1 and L["fused_into"] == -2]
+    assert convs and all(L["i"] in tags for L in convs)  # every conv launched its kernels
+    first = idx[0]
+    assert (first["H"], first["W"], first["C"], first["OC"], first["KH"], first["stride"]) == \
+        (32, 32, 3, 8, 7, 2)
+    assert all(n > 0 and ms > 0 for (n, ms) in kernels.values())
