@@ -308,11 +308,37 @@ __device__ void absmax_block(const float* __restrict__ x, size_t n, float* __res
 // channels of one pixel per lane and one 16-byte store.  Every block first
 // reduces the absmax partials to the tensor's max|x| and forms inv_s =
 // 127/max (src/conv_int8.cpp:78-81); block 0 also writes the device scalars
-// scal = {inv_s, sa = max/127, zero flag, max}.
+// scal = {inv_s, sa = max/127, zero flag, max}.  MODE 0: RNE; 2: the
+// Winograd route's rule.  The grid is bounded (the partials are reduced by at
+// most that many blocks) and strides over the groups, each lane loading its
+// next group while the current one is converted and stored.
+template <int MODE>
 __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, long long pix,
                                                  int Cin, int Cinp, int8_t* __restrict__ q,
                                                  const float* __restrict__ part, int nparts,
-                                                 float* __restrict__ scal, int mode, int cvec) {
+                                                 float* __restrict__ scal, int cvec) {
+    const int groups = Cinp >> 4;
+    const long long total = pix * groups, stride = (long long)gridDim.x * 256;
+    const bool vec = (Cin & 3) == 0 && (((uintptr_t)x) & 15u) == 0;
+    auto load = [&](long long g, float* v) {
+        const long long pp = g / groups;
+        const int c0 = (int)(g - pp * groups) * 16;
+        const float* src = x + pp * Cin + c0;
+        if (vec && c0 + 16 <= Cin) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 f = ((const float4*)src)[k];
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = c0 + k < Cin ? src[k] : 0.0f;
+        }
+    };
+    // the first group's values load while the partials are reduced
+    long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+    float v[16];
+    if (g < total) load(g, v);
     float m = 0.0f;
     for (int i = threadIdx.x; i < nparts; i += 256) { float a = part[i]; m = a > m ? a : m; }
     for (int off = 32; off > 0; off >>= 1) {
@@ -332,25 +358,9 @@ __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, lo
         scal[2] = zero ? 1.0f : 0.0f;
         scal[3] = maxa;
     }
-    const int groups = Cinp >> 4;
-    // grid-stride: a bounded grid, so the partials above are reduced by a
-    // bounded number of blocks
-    for (long long g = (long long)blockIdx.x * 256 + threadIdx.x; g < pix * groups;
-         g += (long long)gridDim.x * 256) {
+    for (; g < total; g += stride) {
         const long long pp = g / groups;
         const int c0 = (int)(g - pp * groups) * 16;
-        const float* src = x + pp * Cin + c0;
-        float v[16];
-        if (c0 + 16 <= Cin && (((uintptr_t)src) & 15u) == 0) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float4 f = ((const float4*)src)[k];
-                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = c0 + k < Cin ? src[k] : 0.0f;
-        }
         unsigned w[4] = {0u, 0u, 0u, 0u};
         if (!zero) {
 #pragma unroll
@@ -360,7 +370,7 @@ __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, lo
                 if (c < Cin) {
                     const float t = __fmul_rn(v[k], inv_s);
                     int r;
-                    if (mode == 0) r = x86_cvt(rintf(t));
+                    if (MODE == 0) r = x86_cvt(rintf(t));
                     else if (c < cvec) r = x86_cvt(truncf(__fadd_rn(t, copysignf(0.5f, t))));
                     else r = x86_lround(t);
                     out = x86_u8(r, 128) - 128;
@@ -368,6 +378,7 @@ __global__ __launch_bounds__(256) void k_quant16(const float* __restrict__ x, lo
                 w[k >> 2] |= ((unsigned)out & 0xffu) << (8 * (k & 3));
             }
         }
+        if (g + stride < total) load(g + stride, v);
         *(i4*)(q + pp * Cinp + c0) = i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     }
 }
@@ -867,7 +878,7 @@ namespace {
 bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s, Arena& ar,
                      bool region, const I8Weights* pre, const float* res, float* amax_out,
-                     const float* amax_in) {
+                     const float* amax_in, I8Quant* shared = nullptr) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
                       g.W >= 3 && g.Cin >= 4 && Cout >= 4;
@@ -894,26 +905,50 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         // absmax partials -> quantize (reduces them, writes the scalars) -> k_i8mm,
         // whose epilogue forms the per-channel factors from the scalars
         constexpr int kParts = 512;
-        float* scal = (float*)ar.get((size_t)(8 + kParts) * sizeof(float));
-        int8_t* q = (int8_t*)ar.get((size_t)pix * Cinp);
+        const int mode = wino ? 2 : 0;
+        // A shared tensor already quantized with this rule: no absmax, no quantizer.
+        const bool reuse = shared && shared->ready && shared->mode == mode;
+        float* scal = reuse || shared ? nullptr : (float*)ar.get((size_t)(8 + kParts) * sizeof(float));
+        int8_t* q = reuse || shared ? nullptr : (int8_t*)ar.get((size_t)pix * Cinp);
+        float* part = nullptr;
+        if (shared) {
+            q = shared->q;
+            scal = shared->scal;
+            if (!reuse && !amax_in) {
+                part = (float*)ar.get((size_t)kParts * sizeof(float));
+                if (!part) return false;
+            }
+        } else {
+            part = scal ? scal + 8 : nullptr;
+        }
         if (!scal || !q) return false;
-        float* part = scal + 8;
         long long n4 = (long long)(inN / 4);
         // With amax_in (the producing layer folded its output's max|x| in) the
         // absmax pass is skipped and the quantizer reads that one "partial".
-        int nb = amax_in ? 0 : (int)((n4 + 1023) / 1024);
-        if (!amax_in) nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
+        int nb = amax_in || reuse ? 0 : (int)((n4 + 1023) / 1024);
+        if (!amax_in && !reuse) nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
         if (nb + (prepared ? 0 : Cout) > 0) {
             ACFUN_LAUNCH("k_absmax_prep", k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s, in,
                                inN, part, nb, wq, g.KH * g.KW, g.Cin, Cinp, Cout, nbt, ldb, nsw);
             if (!check_launch("k_absmax_prep")) return false;
         }
-        const long long groups = pix * (Cinp / 16);
-        const long long qb = std::min((groups + 255) / 256, 8ll * num_cus());
-        ACFUN_LAUNCH("k_quant16", k_quant16, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin, Cinp,
-                           q, amax_in ? amax_in : part, amax_in ? kAmaxParts : nb,
-                           scal, wino ? 2 : 0, g.Cin & ~15);
-        if (!check_launch("k_quant16")) return false;
+        if (!reuse) {
+            const long long groups = pix * (Cinp / 16);
+            const long long qb = std::min((groups + 255) / 256, 8ll * num_cus());
+            if (mode == 0)
+                ACFUN_LAUNCH("k_quant16", k_quant16<0>, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin,
+                             Cinp, q, amax_in ? amax_in : part, amax_in ? kAmaxParts : nb, scal,
+                             g.Cin & ~15);
+            else
+                ACFUN_LAUNCH("k_quant16", k_quant16<2>, dim3((unsigned)qb), dim3(256), 0, s, in, pix, g.Cin,
+                             Cinp, q, amax_in ? amax_in : part, amax_in ? kAmaxParts : nb, scal,
+                             g.Cin & ~15);
+            if (!check_launch("k_quant16")) return false;
+            if (shared) {
+                shared->mode = mode;
+                shared->ready = true;
+            }
+        }
         I8M p{};
         i8mm_conv(p, q, g, Cinp, bt, ldb, Cout);
         p.act = act; p.scal = scal; p.ws = ws; p.bias = bias; p.Cf = out;
@@ -1011,10 +1046,17 @@ void* noalloc_region() {
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre, const float* res, float* amax_out,
-                     const float* amax_in) {
+                     const float* amax_in, I8Quant* shared) {
     Arena ar(s);
+    const long long pix = (long long)g.N * g.H * g.W;
+    if (shared && !i8mm_fits(pix * rup(g.Cin, 16), Cout, rup(g.KH * g.KW * rup(g.Cin, 16), 128)))
+        shared = nullptr;   // (the large-operand path quantizes per call)
     return conv2d_int8_run(in, g, wq, ws, bias, Cout, out, act, s, ar, false, pre, res, amax_out,
-                           amax_in);
+                           amax_in, shared);
+}
+
+size_t i8_quant_bytes(long long pix, int Cin) {
+    return Arena::aligned((size_t)pix * rup(Cin, 16)) + 8 * sizeof(float);
 }
 
 size_t conv2d_int8_noalloc_need(const ConvShape& g, int Cout) {

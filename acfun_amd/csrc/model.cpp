@@ -424,6 +424,37 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         slot = amx.as<float>();
         if (!fill_f32(slot, (size_t)L * kI8AmaxParts, 0.0f, s)) return 0;
     }
+    // int8 convs that read the same tensor with the same rounding rule (a
+    // stage's projection shortcut and its first block's 1x1 conv) quantize it
+    // once: the first writes a shared s8 tensor, the others reuse it.
+    // root(t): the tensor an alias stands for (-1 = the model input).
+    auto root = [&](int t) {
+        while (t >= 0 && alias[t] != -2) t = alias[t];
+        return t;
+    };
+    std::vector<int> qkey(L, -3), qlast(L, -1);      // per int8 conv: (root input, rule) key
+    if (m->int8) {
+        Dims c{m->inH, m->inW, m->inC};
+        int xt = -1;
+        for (int i = 0; i < L; ++i) {
+            const Layer& F = m->layers[i];
+            Dims in = c;
+            if (F.type == 10) { xt = F.from; in = F.from < 0 ? Dims{m->inH, m->inW, m->inC} : out[F.from]; }
+            if (F.type == 1 && F.wq && alias[i] == -2) {
+                const bool wino = F.p[0] == 3 && F.p[1] == 3 && F.p[3] == 1 && F.p[4] == 1 &&
+                                  in.H >= 3 && in.W >= 3 && in.C >= 4 && out[i].C >= 4;
+                qkey[i] = 2 * (root(xt) + 1) + (wino ? 1 : 0);   // >= 0
+            }
+            c = out[i];
+            xt = i;
+        }
+        for (int i = 0; i < L; ++i)
+            if (qkey[i] >= 0)
+                for (int j = i + 1; j < L; ++j)
+                    if (qkey[j] == qkey[i]) qlast[i] = j;    // a later reader of the same quantization
+    }
+    struct SharedQ { int key = -3, last = -1; Scratch mem; I8Quant q; };
+    std::vector<SharedQ> sq;
     auto tensor_of = [&](int idx) -> const float* { return idx < 0 ? din : buf[idx]; };
     cur = Dims{m->inH, m->inW, m->inC};
     const float* x = din;
@@ -485,9 +516,28 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                 if (m->int8 && F.type == 1 && F.wq) {
                     const float* ain =
                         xi >= 0 && amax_of[xi] >= 0 ? slot + (size_t)amax_of[xi] * kI8AmaxParts : nullptr;
+                    I8Quant* shq = nullptr;
+                    for (auto& e : sq)
+                        if (e.key == qkey[i]) shq = &e.q;
+                    if (!shq && qlast[i] > i) {              // the first of several readers
+                        sq.emplace_back();
+                        SharedQ& e = sq.back();
+                        e.key = qkey[i];
+                        e.last = qlast[i];
+                        for (int j = i + 1; j < L; ++j)
+                            if (qkey[j] == qkey[i]) e.last = j;
+                        const long long pix = (long long)N * in.H * in.W;
+                        e.mem = Scratch(i8_quant_bytes(pix, in.C), s);
+                        if (!e.mem.p) return 0;
+                        e.q.q = e.mem.as<int8_t>();
+                        e.q.scal = (float*)(e.mem.as<char>() + (i8_quant_bytes(pix, in.C) - 8 * sizeof(float)));
+                        shq = &e.q;
+                    }
                     ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res,
-                                         slot + (size_t)i * kI8AmaxParts, ain);
+                                         slot + (size_t)i * kI8AmaxParts, ain, shq);
                     amax_of[i] = i;
+                    for (auto it = sq.begin(); it != sq.end();)
+                        it = it->last <= i ? sq.erase(it) : std::next(it);
                 } else if (res && F.p[3] == 1 && F.p[4] == 0 && M < (1ll << 31) &&
                            gemm32_ok((int)M, o.C, in.C, x, in.C, F.w, o.C)) {
                     ok = gemm32_f32((int)M, o.C, in.C, x, in.C, F.w, o.C, y, o.C, F.b, act, s, res,

@@ -301,10 +301,24 @@ void i8_release(I8Weights& w);
 // amax_in (nullable): such partials of the input, from its producer, used in
 // place of the absmax pass.
 constexpr int kI8AmaxParts = 768;
+// A quantized activation tensor shared by several int8 convs that read the same
+// input with the same rounding rule (a model's projection shortcut and the
+// first conv of its block): q [pix][Cinp] s8 and its 8-float scalar block,
+// in memory the caller owns (i8_quant_bytes).  The first call with ready ==
+// false quantizes into it and sets ready; later calls skip the absmax and
+// quantize passes.  mode: 0 RNE (GEMM routes), 2 the Winograd route's rule.
+struct I8Quant {
+    int8_t* q = nullptr;
+    float* scal = nullptr;
+    int mode = -1;
+    bool ready = false;
+};
+size_t i8_quant_bytes(long long pix, int Cin);      // q plus the scalar block
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre = nullptr, const float* res = nullptr,
-                     float* amax_out = nullptr, const float* amax_in = nullptr);
+                     float* amax_out = nullptr, const float* amax_in = nullptr,
+                     I8Quant* shared = nullptr);
 // The int8-in / int8-out convolution (a requantized s8 output): s8 activations
 // q [pix][ldq_in = roundup(Cin,16)] with per-tensor scale *s_in (device; 0 =
 // all-zero input) -> s8 out [pixo][ldo] (ldo a multiple of 16, columns Cout..

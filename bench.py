@@ -210,7 +210,9 @@ def layer_table_md(rows, untagged, tag):
                  f"{LAYER_TYPES.get(r['type'], r['type'])} {r['H']}x{r['W']}x{r['C']} -> "
                  f"{r['OH']}x{r['OW']}x{r['OC']}")
         key = (shape, " + ".join(sorted(r["kernels"])))
-        g = groups.setdefault(key, dict(n=0, ms=0.0, fp32=0.0, int8=0.0, bytes=0.0, floor=0.0))
+        g = groups.setdefault(key, dict(n=0, ms=0.0, fp32=0.0, int8=0.0, bytes=0.0, floor=0.0, kms={}))
+        for name, (_, kms) in r["kernels"].items():
+            g["kms"][name] = g["kms"].get(name, 0.0) + kms
         g["n"] += 1
         g["ms"] += r["ms"]
         g["fp32"] += r["fp32"]
@@ -218,10 +220,11 @@ def layer_table_md(rows, untagged, tag):
         g["bytes"] += r["bytes"]
         g["floor"] += r["floor_ms"]
     total = sum(g["ms"] for g in groups.values())
-    out = [f"| layer shape (per batch of {rows[0]['N'] if rows else 0}) | kernels | layers | ms | share | "
+    out = [f"| layer shape (per batch of {rows[0]['N'] if rows else 0}) | kernels (ms) | layers | ms | share | "
            "executed GFLOP fp32 / GOP int8 | TFLOP/s (TOP/s) | frac of peak | floor ms | time / floor |",
            "|---|---|---|---|---|---|---|---|---|---|"]
-    for (shape, ks), g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"]):
+    for (shape, _), g in sorted(groups.items(), key=lambda kv: -kv[1]["ms"]):
+        ks = ", ".join(f"{k} {v:.4f}" for k, v in sorted(g["kms"].items(), key=lambda kv: -kv[1]))
         work = g["int8"] if g["int8"] else g["fp32"]
         peak = PEAK_INT8 if g["int8"] else PEAK_FP32
         rate = work / (g["ms"] * 1e-3) / 1e12 if g["ms"] and work else 0.0
