@@ -876,6 +876,113 @@ __global__ __launch_bounds__(256) void k_gconv3_pool_img(
     }
 }
 
+// The same fused pair by rows: one 512-thread workgroup per (image, pooled
+// row) stages, for every group at once, the input rows its three conv rows
+// read (2 * stride + 3 rows, each pixel's channels read once) and the whole
+// weight tensor in LDS.  Conv task t is output-channel quad t / (3 OW) of
+// pixel t % (3 OW) of the three conv rows: the lanes of a wave share one or
+// two quads, so their weight reads are LDS broadcasts.  The conv rows go to
+// LDS and are pooled.  The arithmetic per value is k_gconv3_pool's: bias,
+// then taps (kh, kw) in order with the in-range ones only, input channels in
+// order, fmaf; the same activation and max rules.
+// LDS (floats): IR * W * Cin + Cout * 9 * CP + 3 * OW * Cout + Cout.
+template <int CINQ>
+__global__ __launch_bounds__(512) void k_gconv3_pool_row(
+    const float* __restrict__ in, int H, int W, int Cin, const float* __restrict__ w,
+    const float* __restrict__ bias, int Cout, int stride, int pad, int groups, int OH, int OW,
+    int act, int vec_end, int PP, int PH, int PW, int pvec_end, float* __restrict__ out,
+    int post_relu) {
+    constexpr int CP = 4 * CINQ;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    // workgroup -> (image, pooled row), XCD-ordered: the pooled rows of an image,
+    // which share input rows, run on one L2
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    const int L = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+    const int n = L / PH, ph = L - n * PH;
+    const int IR = 2 * stride + 3;                         // input rows of three conv rows
+    const int oh0 = 2 * ph - PP;                           // first conv row (may be -1)
+    const int ih0 = oh0 * stride - pad;                    // first staged input row
+    const int Cout_p = Cout / groups, nqa = Cout >> 2;
+    const int rowf4 = W * Cin / 4, npix = 3 * OW;
+    float* const xs = lds;                                 // [IR][W][Cin]
+    float* const wsm = xs + IR * W * Cin;                  // [groups][9 * CP][Cout_p], as w
+    float* const ys = wsm + Cout * 9 * CP;                 // [3][OW][Cout]
+    float* const bsm = ys + 3 * OW * Cout;                 // [Cout] bias (0 without one)
+    const int tid = threadIdx.x;
+    const float* img = in + (long long)n * H * W * Cin;
+    for (int i = tid; i < Cout; i += 512) bsm[i] = bias ? bias[i] : 0.0f;
+    for (int i = tid; i < IR * rowf4; i += 512) {
+        const int r = i / rowf4, ih = ih0 + r;
+        if ((unsigned)ih < (unsigned)H)                  // rows past the image are never read
+            ((f4*)xs)[i] = ((const f4*)(img + (long long)ih * W * Cin))[i - r * rowf4];
+    }
+    for (int i = tid; i < Cout * 9 * CP / 4; i += 512) ((f4*)wsm)[i] = ((const f4*)w)[i];
+    __syncthreads();
+    for (int t = tid; t < npix * nqa; t += 512) {
+        const int q = t / npix, pix = t - q * npix;
+        const int r = pix / OW, ow = pix - r * OW;
+        const int oh = oh0 + r;
+        if ((unsigned)oh >= (unsigned)OH) continue;         // (the pool skips this row)
+        const int co = 4 * q, g = co / Cout_p, oc = co - g * Cout_p;
+        const float* wg = wsm + g * Cout_p * 9 * CP + oc;
+        f4 sv = *(const f4*)(bsm + co);
+#pragma unroll
+        for (int kt = 0; kt < 9; ++kt) {
+            const int ih = oh * stride - pad + kt / 3, iw = ow * stride - pad + kt % 3;
+            if ((unsigned)ih >= (unsigned)H || (unsigned)iw >= (unsigned)W) continue;
+            const f4* xp = (const f4*)(xs + ((ih - ih0) * W + iw) * Cin + g * CP);
+            f4 xv[CINQ];
+#pragma unroll
+            for (int c = 0; c < CINQ; ++c) xv[c] = xp[c];
+#pragma unroll
+            for (int i = 0; i < CP; ++i) {
+                const float xi = xv[i >> 2][i & 3];
+                const f4 wq = *(const f4*)(wg + (kt * CP + i) * Cout_p);
+                sv.x = fmaf(xi, wq.x, sv.x);
+                sv.y = fmaf(xi, wq.y, sv.y);
+                sv.z = fmaf(xi, wq.z, sv.z);
+                sv.w = fmaf(xi, wq.w, sv.w);
+            }
+        }
+        if (act == 1) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (oc + u < vec_end) sv[u] = vmax(sv[u], 0.0f);
+                else if (sv[u] < 0.0f) sv[u] = 0.0f;
+            }
+        }
+        *(f4*)(ys + (r * OW + ow) * Cout + co) = sv;
+    }
+    __syncthreads();
+    for (int t = tid; t < PW * nqa; t += 512) {
+        const int q = t % nqa, pw = t / nqa;
+        const int co = 4 * q;
+        f4 m = {-1e30f, -1e30f, -1e30f, -1e30f};
+        for (int kh = 0; kh < 3; ++kh) {
+            const int oh = oh0 + kh;
+            if ((unsigned)oh >= (unsigned)OH) continue;
+            for (int kw = 0; kw < 3; ++kw) {
+                const int ow = 2 * pw - PP + kw;
+                if ((unsigned)ow >= (unsigned)OW) continue;
+                const f4 v = *(const f4*)(ys + (kh * OW + ow) * Cout + co);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (co + u < pvec_end) m[u] = vmax(m[u], v[u]);
+                    else if (v[u] > m[u]) m[u] = v[u];
+                }
+            }
+        }
+        if (post_relu) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (co + u < pvec_end) m[u] = vmax(m[u], 0.0f);
+                else if (m[u] < 0.0f) m[u] = 0.0f;
+            }
+        }
+        *(f4*)(out + (((long long)n * PH + ph) * PW + pw) * Cout + co) = m;
+    }
+}
+
 // MaxPool: channels below vec_end use max_ps semantics, the rest the scalar
 // compare of src/layers.cpp:221-246 (they differ only for NaN / signed zero).
 __global__ void k_maxpool(const float* __restrict__ in, int N, int H, int W, int C, int pool,
@@ -1112,6 +1219,30 @@ bool gconv_pool_f32(const float* in, int N, int H, int W, int Cin, const float* 
     // the conv's and the pool's per-channel rules, as gconv_f32 and maxpool_f32 pick them
     const int vec_end = Cout_p >= 16 ? Cout_p : (Cout_p >= 8 ? (Cout_p & ~7) : 0);
     const int pvec_end = Cout >= 16 ? (Cout & ~15) : (Cout >= 8 ? (Cout & ~7) : 0);
+    // one workgroup per (image, pooled row) with its input rows, the weights and
+    // its three conv rows in LDS
+    const size_t row_lds = ((size_t)(2 * stride + 3) * W * Cin + (size_t)Cout * 9 * Cin_p +
+                            (size_t)3 * OW * Cout + Cout) * sizeof(float);
+    if (row_lds <= 64 * 1024 && (long long)N * PH < (1ll << 31) && W * Cin % 4 == 0) {
+        static bool attr = false;
+        if (!attr) {
+            attr = true;
+            (void)hipFuncSetAttribute((const void*)k_gconv3_pool_row<1>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+            (void)hipFuncSetAttribute((const void*)k_gconv3_pool_row<2>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+        }
+        const dim3 grid((unsigned)(N * PH));
+        if (Cin_p == 4)
+            ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool_row<1>, grid, dim3(512), row_lds, s, in, H, W, Cin,
+                         w, bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW,
+                         pvec_end, out, post_relu);
+        else
+            ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool_row<2>, grid, dim3(512), row_lds, s, in, H, W, Cin,
+                         w, bias, Cout, stride, pad, groups, OH, OW, act, vec_end, ppad, PH, PW,
+                         pvec_end, out, post_relu);
+        return check_launch("k_gconv3_pool_row");
+    }
     // small images: one workgroup per (image, group) with the image in LDS
     const size_t img_lds = ((size_t)H * W * Cin_p + (size_t)OH * OW * Cout_p) * sizeof(float);
     if (img_lds <= 48 * 1024 && Cout_p / 4 <= 256 && (long long)N * groups < (1ll << 31)) {

@@ -156,7 +156,9 @@ GCASES = [
     (2, 9, 9, 16, 128, 4, 1, 1, 0, 1, 1),       # 32 output channels per group, no activation
     (1, 10, 10, 12, 12, 3, 1, 1, 1, 1, 0),      # 4 output channels per group: the two-kernel path
     (1, 60, 58, 16, 64, 2, 1, 1, 1, 1, 1),      # image too large for LDS: one lane per pooled quad
-    (2, 41, 40, 24, 48, 6, 2, 1, 1, 0, 0),      # the same, stride 2, pool pad 0
+    (2, 41, 40, 24, 48, 6, 2, 1, 1, 0, 0),      # stride 2, pool pad 0 (row kernel)
+    (1, 8, 8, 128, 512, 32, 1, 1, 1, 1, 0),     # rows of all groups too large for LDS: per image x group
+    (2, 5, 5, 24, 48, 6, 1, 0, 1, 1, 1),        # conv pad 0: 3 x 3 conv output, 2 x 2 pooled
 ]
 
 
