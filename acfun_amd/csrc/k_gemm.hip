@@ -424,7 +424,7 @@ TileCfg tuned_f32_tile(int M, int N, int K, int batch) {
                 hipMemsetD32Async((hipDeviceptr_t)b->p, kTuneFill, bb / 4, s) != hipSuccess)
                 return TuneRunner();
             return [=](int cand, hipStream_t st) {
-                const TileCfg t = f32_cand(cand);
+                const TileCfg t = cand < 0 ? default_f32_tile(M, N, K) : f32_cand(cand);
                 if (t.split > 1 && K < 256 * t.split) return false;
                 return gemm_f32_cfg(M, N, K, a->as<float>(), b->as<float>(), cc->as<float>(), t, st);
             };

@@ -450,6 +450,7 @@ TuneMaker g32_maker(int M, int N, int K, const G32Conv& cv) {
             hipMemsetD32Async((hipDeviceptr_t)b->p, kTuneFill, bbytes / 4, s) != hipSuccess)
             return TuneRunner();
         return [=](int cand, hipStream_t st) {
+            if (cand < 0) cand = g32_index(pick_g32(M, N, K));     // the built-in choice
             if (!g32_admits(cand, K)) return false;
             return launch_cand<CONV>(cand, M, N, K, a->as<float>(), CONV ? cv.Cin : K, b->as<float>(), N,
                                      c->as<float>(), N, nullptr, 0, st, nullptr, 0, cv);

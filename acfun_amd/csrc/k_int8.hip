@@ -723,7 +723,8 @@ TuneMaker i8mm_maker(const I8M& q, int am) {
             p.ws = vf; p.bias = vf + p.N; p.Sw = (const int*)(vf + 2 * p.N); p.scal = vf + 3 * p.N;
             p.s_in = nullptr; p.alpha = p.beta = nullptr; p.res = nullptr; p.amax = nullptr;
             p.epi = EPI_GEMM; p.act = 0; p.vec = 1;
-            const I8Tile t = i8mm_cand(cand, pick_i8mm_tile(p.M, p.N, p.K).per_cu);
+            const I8Tile d = pick_i8mm_tile(p.M, p.N, p.K);
+            const I8Tile t = cand < 0 ? d : i8mm_cand(cand, d.per_cu);
             return launch_i8mm_f32(p, t, am, st);
         };
     };

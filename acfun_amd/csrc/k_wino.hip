@@ -1509,6 +1509,36 @@ bool w23_launch(int c, const float* in, const float* U, const float* bias, float
     return launch_wino23u<8>(in, U, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
 }
 
+// The built-in choice of unit kernel for plan 1 (the tile search's candidate -1).
+bool w23_default(const float* in, const float* Up, const float* bias, float* out, int N, int H, int W,
+                 int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s) {
+    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
+    bool launched = false;
+    if (small) {
+        if (!launch_wino23p<4, 2>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+                                  s, &launched))
+            return false;
+        if (launched) return true;
+    }
+    if (tW >= 12) {
+        if (!launch_wino23p<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
+                                s, &launched))
+            return false;
+        if (launched) return true;
+        return launch_wino23u<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
+                                  act, s);
+    }
+    // 8-wide units: the persistent kernel measured faster at 8 chunks per
+    // unit and slower at 32 (ResNet-50's 14 x 14 x 256 stage)
+    if (Cinp <= 64) {
+        if (!launch_wino23p<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s,
+                               &launched))
+            return false;
+        if (launched) return true;
+    }
+    return launch_wino23u<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
+}
+
 // The replay the tile search times: input and filter transform of the shape
 // filled with a constant, no bias, no activation.
 TuneMaker w23_maker(int N, int H, int W, int Cin, int Cout) {
@@ -1525,6 +1555,9 @@ TuneMaker w23_maker(int N, int H, int W, int Cin, int Cout) {
             hipMemsetD32Async((hipDeviceptr_t)u->p, kTuneFill, ub / 4, s) != hipSuccess)
             return TuneRunner();
         return [=](int cand, hipStream_t st) {
+            if (cand < 0)
+                return w23_default(x->as<float>(), u->as<float>(), nullptr, o->as<float>(), N, H, W, Cin,
+                                   Cinp, Cout, tH, tW, 0, st);
             bool launched = false;
             if (!w23_launch(cand, x->as<float>(), u->as<float>(), nullptr, o->as<float>(), N, H, W, Cin,
                             Cinp, Cout, tH, tW, 0, st, &launched))
@@ -1548,7 +1581,6 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
     Scratch Uown(Upre ? 0 : (size_t)16 * Cout * Cinp * sizeof(float), s);
     if (!Upre && !Uown.p) return false;
     const float* Up = Upre ? Upre : Uown.as<float>();
-    const bool small = tH >= 3 && tH <= 4 && tW >= 3 && tW <= 4 && Cinp >= 32;
     if (plan == 1) {
         if (!Upre && !wino23_filter_impl(w, Cin, Cout, 1, Uown.as<float>(), s)) return false;
         // the tile search's choice of unit kernel for this shape, if any
@@ -1562,30 +1594,7 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
                 return false;
             if (launched) return true;
         }
-        bool launched = false;
-        if (small) {
-            if (!launch_wino23p<4, 2>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
-                                      s, &launched))
-                return false;
-            if (launched) return true;
-        }
-        if (tW >= 12) {
-            if (!launch_wino23p<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act,
-                                    s, &launched))
-                return false;
-            if (launched) return true;
-            return launch_wino23u<16>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW,
-                                      act, s);
-        }
-        // 8-wide units: the persistent kernel measured faster at 8 chunks per
-        // unit and slower at 32 (ResNet-50's 14 x 14 x 256 stage)
-        if (Cinp <= 64) {
-            if (!launch_wino23p<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s,
-                                   &launched))
-                return false;
-            if (launched) return true;
-        }
-        return launch_wino23u<8>(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
+        return w23_default(in, Up, bias, out, N, H, W, Cin, Cinp, Cout, tH, tW, act, s);
     }
     if (!Upre && !wino23_filter_impl(w, Cin, Cout, 0, Uown.as<float>(), s)) return false;
     // Block: TC tile columns x R tile rows of one image, R*TC <= 128 slots and

@@ -13,10 +13,13 @@
 // A kernel family asks tune_lookup() for its shape's choice and, the first
 // time a shape is seen in a process, registers it with tune_record() together
 // with a maker that can replay the launch on scratch operands of that shape.
-// acfun_autotune() times every candidate of every registered shape (plus the
-// GEMM shapes named in ACFUN_TUNE_SHAPES="MxNxK,..."), keeps the fastest and
-// writes the table to the cache file ($ACFUN_TUNE_CACHE, else
-// $HOME/.cache/acfun_amd/tune.txt), one line per (arch, kind, shape):
+// acfun_autotune() times, for every registered shape (plus the GEMM shapes
+// named in ACFUN_TUNE_SHAPES="MxNxK,..."), the built-in choice (candidate -1 of
+// the runner) and every candidate in three interleaved rounds, adopts a
+// candidate only when it beats the built-in choice by more than 3%
+// (tune_rule.hpp; choice -1 keeps the built-in one) and writes the table to
+// the cache file ($ACFUN_TUNE_CACHE, else $HOME/.cache/acfun_amd/tune.txt), one
+// line per (arch, kind, shape):
 //   <arch> <kind> <ncand> <k0>,<k1>,... <choice>
 // so one file serves several GPU types.  Later processes read it at first
 // use; ACFUN_AUTOTUNE=1 runs the search at the first GEMM of a process.
@@ -34,6 +37,7 @@
 #include <vector>
 
 #include "rt.hpp"
+#include "tune_rule.hpp"
 
 namespace acfun {
 namespace {
@@ -49,6 +53,7 @@ bool g_loaded = false;
 bool g_busy = false;
 std::string g_status = "default heuristics (no tile search run)";
 long long g_hits = 0;                           // launches that used a searched choice
+int g_adopted = 0;                              // shapes whose search replaced the built-in choice
 std::string g_status_out;
 
 std::string cache_path() {
@@ -67,7 +72,7 @@ void load_cache_locked() {
     while (fscanf(f, "%63s %15s %d %511s %d", arch, kind, &ncand, keys, &choice) == 5) {
         std::vector<int> key;
         for (char* t = strtok(keys, ","); t; t = strtok(nullptr, ",")) key.push_back(atoi(t));
-        if (choice < 0 || choice >= ncand || key.empty()) continue;
+        if (choice < -1 || choice >= ncand || key.empty()) continue;
         g_table[TKey{arch, kind, key}] = {choice, ncand};
         ++n;
     }
@@ -102,21 +107,16 @@ bool save_cache_locked() {
     return fclose(f) == 0;
 }
 
-// Mean time of one run of candidate c: one untimed run, then the best of three
-// timed batches of five; a candidate the shape does not admit returns +inf.
-float time_candidate(const TuneRunner& run, int c, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    if (!run(c, s)) return 1e30f;
-    float best = 1e30f;
-    for (int r = 0; r < 3; ++r) {
-        if (hipEventRecord(e0, s) != hipSuccess) return 1e30f;
-        for (int i = 0; i < 5; ++i)
-            if (!run(c, s)) return 1e30f;
-        if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e30f;
-        float ms = 0.f;
-        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e30f;
-        best = std::min(best, ms / 5.f);
-    }
-    return best;
+// Mean time of one run of candidate c (-1: the built-in choice) over one
+// timed batch of five; a candidate the shape does not admit returns +inf.
+float time_batch(const TuneRunner& run, int c, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    if (hipEventRecord(e0, s) != hipSuccess) return 1e30f;
+    for (int i = 0; i < 5; ++i)
+        if (!run(c, s)) return 1e30f;
+    if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e30f;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e30f;
+    return ms / 5.f;
 }
 
 }  // namespace
@@ -207,16 +207,20 @@ void autotune_run() {
             }
             TuneRunner run = p.maker ? p.maker() : TuneRunner();
             if (!run) continue;
-            int best = -1;
-            float best_ms = 1e30f;
-            for (int c = 0; c < p.ncand; ++c) {
-                const float ms = time_candidate(run, c, s, e0, e1);
-                if (ms < best_ms) { best_ms = ms; best = c; }
-            }
+            // index 0: the built-in choice (runner candidate -1), then the candidates;
+            // one untimed run each, then three rounds that time every one in turn
+            std::vector<float> ms(p.ncand + 1, 1e30f);
+            std::vector<bool> ok(p.ncand + 1, false);
+            for (int c = -1; c < p.ncand; ++c) ok[c + 1] = run(c, s);
+            for (int r = 0; r < 3; ++r)
+                for (int c = -1; c < p.ncand; ++c)
+                    if (ok[c + 1]) ms[c + 1] = std::min(ms[c + 1], time_batch(run, c, s, e0, e1));
             (void)hipStreamSynchronize(s);
-            if (best < 0) continue;
+            const int choice = tune_pick(ms[0], ms.data() + 1, p.ncand);
+            if (choice < 0 && !(ms[0] < 1e29f)) continue;   // nothing could be timed
             std::lock_guard<std::mutex> lk(g_mu);
-            g_table[k] = {best, p.ncand};
+            g_table[k] = {choice, p.ncand};
+            if (choice >= 0) ++g_adopted;
             ++tuned;
         }
     }
@@ -228,7 +232,9 @@ void autotune_run() {
     const bool saved = save_cache_locked();
     g_busy = false;
     g_status = "tile search (" + std::string(device_arch()) + "): " + std::to_string(tuned) +
-               " shapes tuned, " + (saved ? "cached at " : "NOT cached (cannot write) ") + cache_path();
+               " shapes searched, " + std::to_string(g_adopted) +
+               " beat their built-in choice by more than 3%, " +
+               (saved ? "cached at " : "NOT cached (cannot write) ") + cache_path();
 }
 
 const char* tune_status() {

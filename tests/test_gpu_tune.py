@@ -1,12 +1,14 @@
 """The tile search on the GPU (acfun_autotune; tune.cpp), in child processes
 (tests/tune_replay.py) with their own cache file:
   - search: one shape of each family (k_gemm32 GEMM and implicit-GEMM conv,
-    k_i8mm, the F(2,3) unit kernels, k_gemm_f32) runs, is searched, cached
-    under the device's arch and each family's name, and still matches the
-    oracle with the searched choices;
+    k_i8mm, the F(2,3) unit kernels, k_gemm_f32) runs, is searched against its
+    built-in choice (adopting a candidate only past a 3% margin), cached under
+    the device's arch and each family's name, and still matches the oracle
+    with the searched choices;
   - forced: a cache file assigns every candidate of every family to a shape;
     each result matches the oracle (fp32 within 1e-4 / Winograd 1e-3, int8 bit
-    for bit), and every case ran with its assigned choice."""
+    for bit), and every case ran with its assigned choice; choice -1 (the
+    built-in one kept by the search) loads and runs as well."""
 import os
 import subprocess
 import sys
@@ -54,6 +56,8 @@ def _forced_cache():
         lines.append(f"gfx950 w23 5 {N},{H},{W},{Cin},{Cout} {c}")
     for c, (M, N, K) in enumerate(R.F32):
         lines.append(f"gfx950 f32 16 {M},{N},{K} {c}")
+    M, N, K = R.F32_KEPT
+    lines.append(f"gfx950 f32 16 {M},{N},{K} -1")
     return "\n".join(lines) + "\n"
 
 

@@ -7,7 +7,8 @@
   python tests/tune_replay.py forced  -- runs shapes to which the cache file
       (written by the parent) assigns every candidate of every family, and
       checks each result against the oracle: every choice the search can make
-      computes the same result.
+      computes the same result, including -1 (the search kept the built-in
+      choice).
 
 Prints one line per step and "tune ok" at the end; exits non-zero on failure."""
 import os
@@ -32,6 +33,7 @@ I8 = [(2, 10 + c, 12, 64, 3, 3, 48, 2, 1) for c in range(5)]              # stri
 W23 = [(0, 2, 40, 36 + 2 * c, 32, 40) for c in range(4)] + [(4, 3, 7, 7, 64, 32)] + \
       [(c, 3, 18, 20, 24, 32) for c in (2, 3)]                             # cand, N, H, W, Cin, Cout
 F32 = [(70 + c, 36, 301) for c in range(16)]                               # K % 4 != 0 -> k_gemm_f32
+F32_KEPT = (86, 36, 301)         # cached as -1: the search kept the built-in choice
 
 
 def gemm_case(L, rng, M, N, K):
@@ -88,7 +90,7 @@ def run_all(L, rng, forced):
         check(*int8_case(L, rng, *c), 0.5)
     for c, N, H, W, Cin, Cout in (W23 if forced else W23[:1]):
         check(*conv_case(L, rng, N, H, W, Cin, 3, 3, Cout, 1, 1, "wino23[cand %d]" % c), WINO_TOL)
-    for M, N, K in (F32 if forced else F32[:1]):
+    for M, N, K in (F32 + [F32_KEPT] if forced else F32[:1]):
         check(*gemm_ragged_case(L, rng, M, N, K), GEMM_TOL)
 
 
@@ -105,7 +107,7 @@ def main():
         L.acfun_autotune()
         status = L.acfun_tune_status().decode()
         print("status:", status, flush=True)
-        if "shapes tuned" not in status or "cached at" not in status:
+        if "shapes searched" not in status or "cached at" not in status:
             sys.exit(1)
         lines = open(cache).read().split("\n")
         kinds = {ln.split()[1] for ln in lines if ln.strip()}
@@ -119,7 +121,7 @@ def main():
     # every case above ran with its cached (searched or assigned) choice
     status = L.acfun_tune_status().decode()
     hits = int(status.rsplit("; ", 1)[1].split()[0])
-    need = 5 if mode == "search" else len(G32_GEMM) + len(G32_CONV) + len(I8) + len(W23) + len(F32)
+    need = 5 if mode == "search" else len(G32_GEMM) + len(G32_CONV) + len(I8) + len(W23) + len(F32) + 1
     print("status:", status, "(need %d)" % need, flush=True)
     if hits < need:
         sys.exit(1)
