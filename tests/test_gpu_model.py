@@ -244,3 +244,56 @@ def test_model_layer_profile_tags(gpu, rng, tmp_path):
     assert (first["H"], first["W"], first["C"], first["OC"], first["KH"], first["stride"]) == \
         (32, 32, 3, 8, 7, 2)
     assert all(n > 0 and ms > 0 for (n, ms) in kernels.values())
+
+
+def test_resnet50_int8_head_batch3(gpu, rng, tmp_path):
+    """Config 5's full graph in int8 mode at batch 3: the head (global pool,
+    FC, softmax) after a body whose int8 convs use one activation scale over
+    the batch, against the oracle's chain (Winograd tolerance: the FC runs on
+    the fp32 GEMM engine)."""
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5))
+    path = _write(tmp_path, "r50.acfun", inC, H, W, recs, 2)
+    n = 3
+    x = rng.uniform(0, 1, (n, H, W, inC)).astype(np.float32)
+    m = _load(gpu, path, 1)
+    try:
+        got = np.full((n, 1000), np.nan, np.float32)
+        assert gpu.acfun_model_infer_batch(m, n, P(x), P(got)) == 1000, capi.last_error()
+    finally:
+        gpu.acfun_model_destroy(m)
+    print("oracle ResNet-50 int8 with head, batch", n, flush=True)
+    want = omodel.run(open(path, "rb").read(), x, int8=True)
+    assert rel_err(got, want) < TOL, rel_err(got, want)
+    assert np.allclose(got.sum(axis=1), 1.0, atol=1e-4)
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_resnet50_b64_batch_permutation(gpu, rng, int8, tmp_path):
+    """Config 5's body at the bench's batch of 64 (no oracle at this size): the
+    batch-wide int8 activation scales are maxima over the batch, and every
+    kernel's arithmetic per output element is independent of the image's place
+    in the batch, so permuting the 64 input images permutes the outputs bit for
+    bit (int8), and within 1e-6 (fp32)."""
+    import torch
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5), head=False)
+    path = _write(tmp_path, "r50h.acfun", inC, H, W, recs, 2)
+    n = 64
+    x = torch.rand((n, H, W, inC), device="cuda", generator=torch.Generator(device="cuda").manual_seed(11))
+    perm = torch.from_numpy(np.random.default_rng(2).permutation(n)).cuda()
+    xp = x[perm].contiguous()
+    y = torch.full((n, 7 * 7 * 2048), float("nan"), device="cuda")
+    yp = torch.full_like(y, float("nan"))
+    m = _load(gpu, path, 1 if int8 else 0)
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        assert gpu.acfun_dev_model_infer_batch(m, n, x.data_ptr(), y.data_ptr(), s) == y.shape[1], capi.last_error()
+        assert gpu.acfun_dev_model_infer_batch(m, n, xp.data_ptr(), yp.data_ptr(), s) == y.shape[1], capi.last_error()
+        torch.cuda.synchronize()
+    finally:
+        gpu.acfun_model_destroy(m)
+    a, b = y[perm].cpu().numpy(), yp.cpu().numpy()
+    assert not np.isnan(a).any() and np.count_nonzero(a) > a.size // 4
+    if int8:
+        assert_bitexact(b, a, "int8 ResNet-50 body, batch 64 permuted")
+    else:
+        assert rel_err(b, a) < 1e-6, rel_err(b, a)
