@@ -398,7 +398,7 @@ bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, in
                                   KS * NST * g32_stage(BM, BN) * 4);
     }
     dim3 grid((unsigned)(((N + BN - 1) / BN) * ((M + BM - 1) / BM)));
-    ACFUN_LAUNCH("k_gemm_f32", (k_gemm32<BM, BN, NST, CONV, KS>), grid, dim3(256 * KS), lds, s, A, B, C,
+    ACFUN_LAUNCH("k_gemm32", (k_gemm32<BM, BN, NST, CONV, KS>), grid, dim3(256 * KS), lds, s, A, B, C,
                  bias, res, M, N, K, lda, ldb, ldc, ldr, act, cv);
     return check_launch("k_gemm32");
 }

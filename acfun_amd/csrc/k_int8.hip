@@ -875,11 +875,33 @@ bool conv_int8_direct_dev(const uint8_t* inQ, const ConvShape& g, const int8_t* 
 }
 
 namespace {
+// p (the conv, fp32 factors set up) with its output requantized to s8 as o
+// describes: two k_i8mm passes, or for K >= 512 one fp32 pass into a scratch
+// buffer and k_requant_s8 (launch_i8mm_rq).
+bool launch_q8out(I8M& p, const I8Out& o, Arena& ar, hipStream_t s) {
+    if (o.ldo % 16 != 0 || o.ldo < p.N || (((uintptr_t)o.q) & 15u) ||
+        (long long)p.M * o.ldo >= 0x7fffffffll) {
+        set_error("conv2d_int8: bad s8 output layout");
+        return false;
+    }
+    float* parts = (float*)ar.get((size_t)kAmaxParts * sizeof(float));
+    if (!parts) return false;
+    p.Cf = nullptr; p.res = nullptr; p.amax = nullptr;
+    p.Cq = o.q; p.ldq = o.ldo; p.rule = o.rule; p.s_out = o.s_out;
+    float* ybuf = nullptr;
+    if (p.K >= 512 || !o.recompute) {
+        ybuf = (float*)ar.get((size_t)p.M * p.N * sizeof(float));
+        if (!ybuf) return false;
+    }
+    return launch_i8mm_rq(p, parts, ybuf, s);
+}
+
 // acfun_conv2d_int8 on device with every temporary taken from `ar`.
 bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s, Arena& ar,
                      bool region, const I8Weights* pre, const float* res, float* amax_out,
-                     const float* amax_in, I8Quant* shared = nullptr) {
+                     const float* amax_in, I8Quant* shared = nullptr,
+                     const I8Out* q8out = nullptr) {
     if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
     const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
                       g.W >= 3 && g.Cin >= 4 && Cout >= 4;
@@ -957,7 +979,12 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         p.amax = amax_out;
         if (wino) p.epi = EPI_WINO;
         else { p.epi = EPI_GEMM; p.Sw = sw; }
+        if (q8out) return launch_q8out(p, *q8out, ar, s);
         return launch_i8mm(p, s);
+    }
+    if (q8out) {
+        set_error("conv2d_int8: an s8 output needs operands within 32-bit offsets");
+        return false;
     }
     // (operands past 32-bit offsets: amax_in is not needed, the absmax pass
     // below runs; amax_out is filled by a pass over the output at the end)
@@ -1047,13 +1074,41 @@ void* noalloc_region() {
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre, const float* res, float* amax_out,
-                     const float* amax_in, I8Quant* shared) {
+                     const float* amax_in, I8Quant* shared, const I8Out* q8out) {
     Arena ar(s);
     const long long pix = (long long)g.N * g.H * g.W;
     if (shared && !i8mm_fits(pix * rup(g.Cin, 16), Cout, rup(g.KH * g.KW * rup(g.Cin, 16), 128)))
         shared = nullptr;   // (the large-operand path quantizes per call)
     return conv2d_int8_run(in, g, wq, ws, bias, Cout, out, act, s, ar, false, pre, res, amax_out,
-                           amax_in, shared);
+                           amax_in, shared, q8out);
+}
+
+bool conv2d_int8_s8in_dev(const int8_t* q, const float* s_in, const ConvShape& g,
+                          const I8Weights& pre, const float* ws, const float* bias, int Cout,
+                          float* out, int act, hipStream_t s, const float* res, float* amax_out,
+                          const I8Out* q8out) {
+    if (g.OH <= 0 || g.OW <= 0 || Cout <= 0 || g.N <= 0) return true;
+    const int Cinp = rup(g.Cin, 16);
+    const long long pix = (long long)g.N * g.H * g.W;
+    if (!pre.bt || pre.taps != g.KH * g.KW || pre.Cin != g.Cin || pre.N != Cout ||
+        !i8mm_fits(pix * Cinp, Cout, pre.ldb) || (((uintptr_t)q) & 15u)) {
+        set_error("conv2d_int8_s8in: needs prepared weights, a 16-byte aligned s8 input and "
+                  "operands within 32-bit offsets");
+        return false;
+    }
+    const bool wino = g.KH == 3 && g.KW == 3 && g.stride == 1 && g.pad == 1 && g.H >= 3 &&
+                      g.W >= 3 && g.Cin >= 4 && Cout >= 4;
+    I8M p{};
+    i8mm_conv(p, q, g, Cinp, pre.bt, pre.ldb, Cout);
+    p.act = act; p.s_in = s_in; p.ws = ws; p.bias = bias;
+    if (wino) p.epi = EPI_WINO;
+    else { p.epi = EPI_GEMM; p.Sw = pre.sw; }
+    if (q8out) {
+        Arena ar(s);
+        return launch_q8out(p, *q8out, ar, s);
+    }
+    p.Cf = out; p.res = res; p.ldr = Cout; p.amax = amax_out;
+    return launch_i8mm(p, s);
 }
 
 size_t i8_quant_bytes(long long pix, int Cin) {

@@ -126,6 +126,15 @@ void quantize_cols(const std::vector<float>& w, int K, int N, std::vector<float>
     }
 }
 
+// ACFUN_I8_CHAIN=0 turns the int8 models' s8 chain off (read once).
+bool int8_chain_enabled() {
+    static const int on = [] {
+        const char* e = std::getenv("ACFUN_I8_CHAIN");
+        return e && *e == '0' ? 0 : 1;
+    }();
+    return on != 0;
+}
+
 }  // namespace
 
 struct AcfunModel {
@@ -455,6 +464,45 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
     }
     struct SharedQ { int key = -3, last = -1; Scratch mem; I8Quant q; };
     std::vector<SharedQ> sq;
+    // The int8 chain: an int8 conv whose output has one reader, an int8 conv
+    // taking it as its input, writes it as s8 with its scale (I8Out: the
+    // values and scale the reader's quantizer would form from the fp32 tensor,
+    // bit for bit) and the reader multiplies that s8 tensor directly; neither
+    // the fp32 tensor nor the reader's absmax/quantize passes exist.  Tensors
+    // an Add, a projection shortcut or the model output also read stay fp32.
+    // ACFUN_I8_CHAIN=0 keeps every tensor fp32 (the same results).
+    std::vector<int> chain_to(L, -1), chain_rule(L, 0);
+    if (m->int8 && int8_chain_enabled()) {
+        std::vector<int> nread(L + 1, 0), reader(L + 1, -1), rin(L, -2);   // index: root + 1
+        auto note = [&](int r, int k) { ++nread[r + 1]; reader[r + 1] = k; };
+        int xt = -1;
+        for (int k = 0; k < L; ++k) {
+            const Layer& F = m->layers[k];
+            if (alias[k] == -2) {                    // executes (Input layers always alias)
+                rin[k] = root(xt);
+                note(rin[k], k);
+                if (F.type == 8) note(root(F.from), k);
+                if (res_of[k] != -3) note(root(res_of[k]), k);
+            }
+            xt = k;
+        }
+        if (L > 0) note(root(L - 1), L);             // the model output
+        for (int i = 0; i < L; ++i) {
+            const Layer& F = m->layers[i];
+            if (!(F.type == 1 && F.wq && alias[i] == -2) || nread[i + 1] != 1) continue;
+            const int j = reader[i + 1];
+            if (j >= L || rin[j] != i) continue;
+            const Layer& G = m->layers[j];
+            if (!(G.type == 1 && G.wq)) continue;
+            const Dims& d = out[i];                  // the reader's input
+            const bool wino = G.p[0] == 3 && G.p[1] == 3 && G.p[3] == 1 && G.p[4] == 1 &&
+                              d.H >= 3 && d.W >= 3 && d.C >= 4 && out[j].C >= 4;
+            chain_to[i] = j;
+            chain_rule[i] = wino ? 1 : 0;
+        }
+    }
+    struct S8T { Scratch q, scale; };
+    std::vector<S8T> s8t(L);                        // chained s8 tensors by producer
     auto tensor_of = [&](int idx) -> const float* { return idx < 0 ? din : buf[idx]; };
     cur = Dims{m->inH, m->inW, m->inC};
     const float* x = din;
@@ -491,7 +539,9 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
         }
         bool inplace = (F.type == 3 || F.type == 5 || F.type == 6 || F.type == 10);
         float* y;
-        if (inplace && F.type != 10 && xi >= 0 && last_use[xi] == i && hold[xi].p) {
+        if (chain_to[i] >= 0) {
+            y = nullptr;                             // the output exists only as s8 (s8t[i])
+        } else if (inplace && F.type != 10 && xi >= 0 && last_use[xi] == i && hold[xi].p) {
             // take over the input buffer
             y = buf[xi];
             hold[i] = std::move(hold[xi]);
@@ -533,9 +583,29 @@ int run_model(AcfunModel* m, int N, const float* din, float* dout, hipStream_t s
                         e.q.scal = (float*)(e.mem.as<char>() + (i8_quant_bytes(pix, in.C) - 8 * sizeof(float)));
                         shq = &e.q;
                     }
-                    ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res,
-                                         slot + (size_t)i * kI8AmaxParts, ain, shq);
-                    amax_of[i] = i;
+                    I8Out qout;
+                    if (chain_to[i] >= 0) {
+                        qout.ldo = (o.C + 15) / 16 * 16;
+                        qout.rule = chain_rule[i];
+                        qout.recompute = false;
+                        s8t[i].q = Scratch((size_t)N * o.H * o.W * qout.ldo, s);
+                        s8t[i].scale = Scratch(sizeof(float), s);
+                        if (!s8t[i].q.p || !s8t[i].scale.p) return 0;
+                        qout.q = s8t[i].q.as<int8_t>();
+                        qout.s_out = s8t[i].scale.as<float>();
+                    }
+                    const I8Out* qo = chain_to[i] >= 0 ? &qout : nullptr;
+                    const int rx = root(xi);
+                    if (rx >= 0 && s8t[rx].q.p) {            // an s8 input from the chain
+                        ok = conv2d_int8_s8in_dev(s8t[rx].q.as<int8_t>(), s8t[rx].scale.as<float>(), g,
+                                                  F.i8, F.ws, F.b, o.C, y, act, s, res,
+                                                  slot + (size_t)i * kI8AmaxParts, qo);
+                        s8t[rx] = S8T();                     // its only reader
+                    } else {
+                        ok = conv2d_int8_dev(x, g, F.wq, F.ws, F.b, o.C, y, act, s, &F.i8, res,
+                                             slot + (size_t)i * kI8AmaxParts, ain, shq, qo);
+                    }
+                    amax_of[i] = qo ? -1 : i;
                     for (auto it = sq.begin(); it != sq.end();)
                         it = it->last <= i ? sq.erase(it) : std::next(it);
                 } else if (res && F.p[3] == 1 && F.p[4] == 0 && M < (1ll << 31) &&

@@ -314,11 +314,33 @@ struct I8Quant {
     bool ready = false;
 };
 size_t i8_quant_bytes(long long pix, int Cin);      // q plus the scalar block
+// A requantized s8 output (a model's int8 chain): q [pixo][ldo], ldo = Cout
+// rounded up to 16 (columns Cout.. written 0), *s_out = max|y|/127 (0 for an
+// all-zero y), rounded with rule (0 RNE; 1 the Winograd route's input rule),
+// the values acfun_conv2d_int8's consumer would quantize y to.
+struct I8Out {
+    int8_t* q = nullptr;
+    int ldo = 0;
+    float* s_out = nullptr;
+    int rule = 0;
+    // true: for K < 512 recompute the tile in a second pass instead of storing
+    // and requantizing the fp32 output (the API entry's choice); false: always
+    // one fp32 pass and the requantizer (what a model's chain measured faster)
+    bool recompute = true;
+};
+// q8out (nullable): write the s8 output instead of out (res and amax_out unused).
 bool conv2d_int8_dev(const float* in, const ConvShape& g, const int8_t* wq, const float* ws,
                      const float* bias, int Cout, float* out, int act, hipStream_t s,
                      const I8Weights* pre = nullptr, const float* res = nullptr,
                      float* amax_out = nullptr, const float* amax_in = nullptr,
-                     I8Quant* shared = nullptr);
+                     I8Quant* shared = nullptr, const I8Out* q8out = nullptr);
+// The same on an s8 input of a chain: q [pix][Cin rounded up to 16] with scale
+// *s_in (device; 0 = all-zero input) and prepared weights; fp32 output (out,
+// res, amax_out as above) or, with q8out, s8.
+bool conv2d_int8_s8in_dev(const int8_t* q, const float* s_in, const ConvShape& g,
+                          const I8Weights& pre, const float* ws, const float* bias, int Cout,
+                          float* out, int act, hipStream_t s, const float* res, float* amax_out,
+                          const I8Out* q8out);
 // The int8-in / int8-out convolution (a requantized s8 output): s8 activations
 // q [pix][ldq_in = roundup(Cin,16)] with per-tensor scale *s_in (device; 0 =
 // all-zero input) -> s8 out [pixo][ldo] (ldo a multiple of 16, columns Cout..

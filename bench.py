@@ -56,7 +56,7 @@ def parse():
                          "(--layers-md)")
     ap.add_argument("--layers-md", metavar="PATH", default=None,
                     help="with --profile cfg5_*: write the per-layer table of the second batch "
-                         "(markdown) to PATH")
+                         "(markdown) to PATH and its layers with their launch counts to PATH.json")
     ap.add_argument("--traffic", action="store_true", help="the same as --profile cfg2a")
     ap.add_argument("--tune", action="store_true",
                     help="run the tile search (acfun_autotune) over every config's shapes first, as "
@@ -651,6 +651,13 @@ def main():
         if args.layers_md:
             with open(args.layers_md, "w") as f:
                 f.write(md)
+            # the layers in execution order with their launch counts, so that a
+            # kernel trace of the same run can be split by layer
+            with open(args.layers_md + ".json", "w") as f:
+                json.dump({"layers": [dict({k: v for k, v in r.items() if k != "kernels"},
+                                           kernels={n: list(v) for n, v in r["kernels"].items()})
+                                      for r in rows],
+                           "untagged": {n: list(v) for n, v in untagged.items()}}, f)
         print(md, flush=True)
         return
     if args.profile:
@@ -719,11 +726,11 @@ def main():
 
         # 1: GEMM 1024^3
         t = T.run(cfg["cfg1"]["step"], steps, args.warmup)
-        k = T.kernel_ms(lib, cfg["cfg1"]["step"], steps, ["k_gemm_f32"])
+        k = T.kernel_ms(lib, cfg["cfg1"]["step"], steps, ["k_gemm32"])
         flop = 2.0 * 1024 ** 3
         configs["cfg1_gemm_1024"] = {
             "ms": round(t, 5), "TFLOPS": round(flop / (t * 1e-3) / 1e12, 3),
-            "roofline": roofline("mfma-fp32", flop, k["k_gemm_f32"], "k_gemm32",
+            "roofline": roofline("mfma-fp32", flop, k["k_gemm32"], "k_gemm32",
                                  "2*1024^3 = 2.147 GFLOP per launch", "k_gemm32_cfg1")}
 
         # acfun_gemm_bf16 1024^3 (not a BASELINE config)

@@ -297,3 +297,34 @@ def test_resnet50_b64_batch_permutation(gpu, rng, int8, tmp_path):
         assert_bitexact(b, a, "int8 ResNet-50 body, batch 64 permuted")
     else:
         assert rel_err(b, a) < 1e-6, rel_err(b, a)
+
+
+def test_int8_model_uses_the_s8_chain(gpu, rng, tmp_path):
+    """An int8 model passes a tensor whose only reader is another int8 conv as
+    s8 with its device scale: its producer requantizes it (k_requant_s8) and the
+    reader runs no quantizer, while tensors an Add or a projection also reads
+    stay fp32.  The results are the oracle's bit for bit (the chain changes no
+    value: test_resnet50_headless_batch8[int8] at full size)."""
+    inC, H, W, recs = acfun0.resnet50(rng, in_hw=32, width=8, blocks=(2, 1), classes=10, head=False)
+    path = _write(tmp_path, "r.acfun", inC, H, W, recs, 2)
+    m = _load(gpu, path, 1)
+    x = rng.uniform(0, 1, (2, H, W, inC)).astype(np.float32)
+    n_out = 4 * 4 * 64                                   # 32 -> 16 (conv1) -> 8 (pool) -> 8 -> 4; 16 * 4 channels
+    y = np.full((2, n_out), np.nan, np.float32)          # (the call writes N x its output size)
+    try:
+        gpu.acfun_prof_enable(1)
+        try:
+            assert gpu.acfun_model_infer_batch(m, 2, P(x), P(y)) == n_out, capi.last_error()
+        finally:
+            gpu.acfun_prof_enable(0)
+        kernels, layers = capi.prof_report()
+    finally:
+        gpu.acfun_model_destroy(m)
+    convs = [L["i"] for L in layers if L["type"] == 1 and L["fused_into"] == -2]
+    per = {i: {k for (t, k) in kernels if t == i} for i in convs}
+    producers = [i for i in convs if "k_requant_s8" in per[i]]
+    readers = [i for i in convs if not per[i] & {"k_quant16", "k_absmax_prep"}]
+    assert len(producers) >= 4, per                      # conv a -> b and b -> c in each of 3 blocks
+    assert len(readers) >= len(producers), per
+    want = omodel.run(open(path, "rb").read(), x, int8=True)
+    assert_bitexact(y, want, "int8 chain")
