@@ -15,6 +15,10 @@
 // wave interleaved MFMA, V fmas, MFMA, ... or in two waves of one SIMD.
 // HBM: a grid-stride float4 read (sum) and copy over buffers of 4 GiB, far
 // beyond the 256 MB last-level cache, timed after one untimed pass.
+// Launch floor: 500 back-to-back launches of a kernel that does nothing (its
+// one store is never taken), at several grid / block / dynamic-LDS shapes,
+// between two events on the null stream; and the same launches replayed
+// from a HIP graph of 20.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -33,6 +37,10 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef int i16v __attribute__((ext_vector_type(16)));
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+
+__global__ void k_nothing(float* p) {
+  if (p && threadIdx.x == 1u << 30) p[0] = 1.f;
+}
 
 template <int KIND>
 __global__ __launch_bounds__(256) void k_peak(float* out, int iters, unsigned long long* clk) {
@@ -270,6 +278,48 @@ int main() {
   }
   CHECK(hipFree(a));
   CHECK(hipFree(b));
+
+  {
+    CHECK(hipFuncSetAttribute((const void*)k_nothing, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+    const int shapes[][3] = {{1, 64, 0}, {224, 256, 0}, {224, 512, 60000}, {1024, 256, 0}, {2048, 256, 0}};
+    for (const auto& sh : shapes) {
+      auto launch = [&](hipStream_t st) {
+        hipLaunchKernelGGL(k_nothing, dim3(sh[0]), dim3(sh[1]), sh[2], st, nullptr);
+      };
+      for (int i = 0; i < 20; ++i) launch(0);
+      CHECK(hipGetLastError());
+      CHECK(hipDeviceSynchronize());
+      CHECK(hipEventRecord(e0, 0));
+      for (int i = 0; i < 500; ++i) launch(0);
+      CHECK(hipEventRecord(e1, 0));
+      CHECK(hipEventSynchronize(e1));
+      float ms;
+      CHECK(hipEventElapsedTime(&ms, e0, e1));
+      std::printf("empty kernel, grid %5d x %4d threads, %5d B LDS: %.2f us per launch back to back\n",
+                  sh[0], sh[1], sh[2], ms * 1e3 / 500);
+    }
+    hipStream_t st;
+    CHECK(hipStreamCreate(&st));
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int i = 0; i < 20; ++i) hipLaunchKernelGGL(k_nothing, dim3(224), dim3(512), 60000, st, nullptr);
+    CHECK(hipStreamEndCapture(st, &g));
+    CHECK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    for (int i = 0; i < 5; ++i) CHECK(hipGraphLaunch(ge, st));
+    CHECK(hipStreamSynchronize(st));
+    CHECK(hipEventRecord(e0, st));
+    for (int i = 0; i < 25; ++i) CHECK(hipGraphLaunch(ge, st));
+    CHECK(hipEventRecord(e1, st));
+    CHECK(hipEventSynchronize(e1));
+    float ms;
+    CHECK(hipEventElapsedTime(&ms, e0, e1));
+    std::printf("empty kernel, grid   224 x  512 threads, 60000 B LDS: %.2f us per launch in a graph of 20\n",
+                ms * 1e3 / 500);
+    CHECK(hipGraphExecDestroy(ge));
+    CHECK(hipGraphDestroy(g));
+    CHECK(hipStreamDestroy(st));
+  }
   CHECK(hipFree(out));
   CHECK(hipFree(clk));
   return 0;

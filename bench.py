@@ -832,9 +832,9 @@ def main():
         configs["cfg4b_grouped_pool"] = {
             "ms": round(t, 5), "ms_cold": round(tc, 5), "ms_graph_replay": round(tg, 5),
             "ms_two_launches": round(t2, 5),
-            "roofline": roofline("hbm", c["bytes"], k["k_gconv_pool"], "k_gconv3_pool_img<1>",
+            "roofline": roofline("hbm", c["bytes"], k["k_gconv_pool"], "k_gconv3_pool_row<1>",
                                  f"{c['bytes'] / 1e6:.2f} MB per launch (input once, pooled output "
-                                 "once); launch-bound at this size"),
+                                 "once); latency-bound at this size", "k_gconv_pool_cfg4b"),
             "kernel_ms": k}
 
         # 5: ResNet-50-style, batch 64, fp32 and int8
