@@ -6,9 +6,12 @@
 //
 // Workgroup = 64 x 64 tile of C, 4 waves in a 2 x 2 grid, each wave one
 // 32 x 32 accumulator (16 registers per lane): a single dependent MFMA chain,
-// which gfx950 issues back to back.  K is consumed in chunks of 64:
+// which gfx950 issues back to back.  K is consumed in chunks of KC = 64:
 //   A stage [64 rows][16 quads], quad q of row r at slot q ^ (r & 15);
-//   B stage [64 k][16 quads],    quad q of row k at slot q ^ ((k & 32) >> 2).
+//   B stage [64 k][16 quads],    quad q of row k at slot q ^ ((k & 32) >> 2);
+// or KC = 32:
+//   A stage [64 rows][8 quads],  quad q of row r at slot q ^ ((r >> 1) & 7);
+//   B stage [32 k][16 quads],    quad q of row k at slot q ^ ((k & 16) >> 1).
 // Both are filled by buffer_load_dwordx4 ... lds (no data VGPRs; rows and
 // columns past the matrix read zeros through the buffer range check or an
 // out-of-range offset), three stages deep with chunk c+2 issued while chunk
@@ -20,6 +23,10 @@
 // residual tensor (a model's Add fused into the conv before it: the same two
 // roundings as a separate Add), applies ReLU (max_ps order) and stores 128
 // contiguous bytes per half-wave row.
+//
+// KS > 1: KS groups of four waves in one workgroup split K by chunk
+// (group kg takes chunks kg, kg + KS, ...), each with its own stages; the
+// groups' accumulators are summed through LDS at the end, group 1's first.
 #include "rt.hpp"
 
 #include <cstdlib>
@@ -32,7 +39,6 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4g __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void32;
 
-constexpr int G32_KC = 64;
 
 // Implicit-GEMM convolution geometry (CONV mode): A is the NHWC input
 // [n][H][W][Cin], row m of the GEMM the output pixel (n, oh, ow), k = tap*Cin + ic.
@@ -41,10 +47,10 @@ struct G32Conv {
     unsigned bytes;    // N*H*W*Cin*4, below 2^31
 };
 
-constexpr int g32_stage(int BM, int BN) { return BM * G32_KC + G32_KC * BN; }   // floats
+constexpr int g32_stage(int BM, int BN, int KC) { return BM * KC + KC * BN; }   // floats
 constexpr int g32_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-template <int BM, int BN, int NST, bool CONV, int KS>
+template <int BM, int BN, int NST, bool CONV, int KS, int KC>
 __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 float* __restrict__ C,
@@ -54,18 +60,22 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
                                                 int act, G32Conv cv) {
     constexpr unsigned kOOB = 0x80000000u;
     constexpr int FM = BM / 64, FN = BN / 64;          // 32 x 32 blocks per wave
-    constexpr int STAGE = g32_stage(BM, BN);
-    constexpr int SB = BM * G32_KC;                     // B's offset in a stage (floats)
-    constexpr int AIT = BM / 16, BIT = BN / 16;         // DMA instructions per wave per chunk
+    constexpr int STAGE = g32_stage(BM, BN, KC);
+    constexpr int SB = BM * KC;                         // B's offset in a stage (floats)
+    constexpr int QA = KC / 4;                          // quads per A row
+    constexpr int RPI = 64 / QA;                        // A rows per DMA instruction
+    constexpr int AIT = BM * QA / 256, BIT = KC * BN / 1024;   // DMA instructions per wave per chunk
     constexpr int ITEMS = AIT + BIT;
     constexpr int BQ = BN / 4;                          // quads per B row
+    constexpr int KSTEP = KC / 2;                       // MFMA k-steps per chunk
+    static_assert(KC == 64 || KC == 32, "chunk of 32 or 64");
+    static_assert(AIT >= 1 && BIT >= 1, "whole DMA instructions");
     extern __shared__ __attribute__((aligned(16))) float sm[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // KS = 2: two groups of four waves split K by chunk parity (group kg takes
-    // chunks kg, kg + 2, ...) with their own stages; their accumulators are
-    // summed through LDS at the end.
-    const int kg = KS == 2 ? wave >> 2 : 0, wl = wave & 3;
+    // KS > 1: group kg = wave / 4 takes chunks kg, kg + KS, ... with its own
+    // stages; the accumulators are summed through LDS at the end.
+    const int kg = KS > 1 ? wave >> 2 : 0, wl = wave & 3;
     const int wm = wl >> 1, wn = wl & 1;
     // Tile order: the 1-D grid is cut into 8 contiguous runs, one per XCD
     // (workgroup id mod 8), and within a run tiles go in groups of 4 tile rows,
@@ -80,12 +90,13 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     const int r_in = L - grp * GRP * gn;
     const int tm = gbase + r_in % rows, tn = r_in / rows;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int nch0 = (K + G32_KC - 1) / G32_KC;
+    const int nch0 = (K + KC - 1) / KC;
     const int nch = (nch0 + KS - 1) / KS;                 // chunks per group (local)
 
     // ---- DMA descriptors.  A: wave w issues instructions w + 4t (t < AIT),
-    // each 4 rows x 16 quads; lane l -> row 4(w + 4t) + l/16, quad slot l%16.
-    // B: instructions w + 4t (t < BIT), each 64 slots of k rows of BQ quads.
+    // each RPI rows x QA quads; lane l -> row RPI(w + 4t) + l/QA, quad slot
+    // l%QA.  B: instructions w + 4t (t < BIT), each 64 slots of k rows of BQ
+    // quads.
     const __amdgpu_buffer_rsrc_t ares = CONV
         ? __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)cv.bytes, 0x00020000)
         : __builtin_amdgcn_make_buffer_rsrc(
@@ -94,10 +105,12 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
               0x00020000);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)B, (short)0, (int)((long long)K * ldb * 4), 0x00020000);
-    const int arow = 4 * wl + (lane >> 4);                 // + 16t
-    const int aq = (lane & 15) ^ (arow & 15);              // same for every t
+    const int arow = RPI * wl + lane / QA;                 // + 4 RPI t
+    // the quad this lane's slot holds (the swizzle is the same for every t:
+    // 4 RPI t is a multiple of 16)
+    const int aq = KC == 64 ? (lane & 15) ^ (arow & 15) : (lane & 7) ^ ((arow >> 1) & 7);
     const unsigned av = (unsigned)(arow * lda + 4 * aq) * 4u;
-    const unsigned astep = 16u * lda * 4u;                 // 16 rows per t
+    const unsigned astep = 4u * RPI * lda * 4u;            // 4 RPI rows per t
     // CONV: per row t, the byte offset of channel quad aq of tap (0, 0) and the
     // in-image taps as bits kh*8 + kw (KH, KW <= 8)
     int cbase[AIT];
@@ -105,7 +118,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     if (CONV) {
 #pragma unroll
         for (int t = 0; t < AIT; ++t) {
-            const int m = m0 + arow + 16 * t;
+            const int m = m0 + arow + 4 * RPI * t;
             cbase[t] = 0;
             cmask[t] = 0;
             if (m < M) {
@@ -132,22 +145,22 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     for (int t = 0; t < BIT; ++t) {
         const int slot = 64 * (wl + 4 * t) + lane;
         const int krow = slot / BQ;
-        const int q = (slot % BQ) ^ ((krow & 32) >> 2);    // quad q of k row r at slot q ^ 8[r >= 32]
+        const int q = (slot % BQ) ^ ((krow & (KC / 2)) ? 8 : 0);   // quad q of k row r: slot q ^ 8[r >= KC/2]
         bok[t] = n0 + 4 * q < N;
         bv[t] = (unsigned)(krow * ldb + n0 + 4 * q) * 4u;
     }
-    const bool kragged = (K & (G32_KC - 1)) != 0;
+    const bool kragged = (K & (KC - 1)) != 0;
 
     // Every variable part of an address is in the per-lane offset (which the
     // buffer range check covers); the scalar offset stays 0.
     auto issue = [&](int t, int c, float* st) {            // item t of (local) chunk c into stage st
-        const int k0 = (KS * c + kg) * G32_KC;
+        const int k0 = (KS * c + kg) * KC;
         if (t < AIT) {
             unsigned v;
             if (KS > 1 && k0 >= K) {
                 v = kOOB;                                   // a group's padding chunk: zeros
             } else if (CONV) {
-                // a 64-channel chunk lies in one tap (Cin % 64 == 0): wave-uniform
+                // a chunk lies in one tap (Cin % 64 == 0): wave-uniform
                 const int tap = k0 / cv.Cin, ic0 = k0 - tap * cv.Cin;
                 const int kh = tap / cv.KW, kw = tap - kh * cv.KW;
                 const bool ok = (cmask[t] >> (kh * 8 + kw)) & 1ull;
@@ -167,19 +180,23 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     };
 
     // ---- per-lane read offsets within a stage (floats).  MFMA k assignment:
-    // in k-step s of a chunk, lane half h carries k = 32h + s for both operands.
+    // in k-step s of a chunk, lane half h carries k = (KC/2) h + s for both
+    // operands.
     const int r = lane & 31, h = lane >> 5;
-    int aoff[FM][8], boff[FN];
+    constexpr int AQ = KC / 8;                          // A quads a lane reads per chunk
+    int aoff[FM][AQ], boff[FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         const int rowA = (BM / 2) * wm + 32 * i + r;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) aoff[i][j] = (rowA * 16 + ((8 * h + j) ^ (rowA & 15))) * 4;
+        for (int j = 0; j < AQ; ++j)
+            aoff[i][j] = KC == 64 ? (rowA * 16 + ((8 * h + j) ^ (rowA & 15))) * 4
+                                  : (rowA * 8 + ((4 * h + j) ^ ((rowA >> 1) & 7))) * 4;
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int col = (BN / 2) * wn + 32 * j + r;
-        boff[j] = SB + ((32 * h) * BQ + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
+        boff[j] = SB + ((KSTEP * h) * BQ + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
     }
 
     f16v acc[FM][FN];
@@ -210,14 +227,17 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
         }
     }
 
-    // NST = 3: chunk c+2 is issued while chunk c is multiplied; NST = 2: c+1.
+    // Chunk c goes to stage c % NST, and chunk c + NST - 1 is issued while
+    // chunk c is multiplied.
     constexpr int AHEAD = NST - 1;
+    static_assert(NST >= 2 && NST <= 4, "two to four stages");
     float* const smg = sm + kg * NST * STAGE;           // this group's stages
 #pragma unroll
-    for (int t = 0; t < ITEMS; ++t) issue(t, 0, smg);
-    if (AHEAD == 2 && nch > 1) {
+    for (int c0 = 0; c0 < AHEAD; ++c0) {
+        if (c0 < nch) {
 #pragma unroll
-        for (int t = 0; t < ITEMS; ++t) issue(t, 1, smg + STAGE);
+            for (int t = 0; t < ITEMS; ++t) issue(t, c0, smg + c0 * STAGE);
+        }
     }
 
     // Software pipeline per chunk c (operands in registers):
@@ -233,11 +253,14 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     // The barrier before chunk c+1's reads also orders every wave's reads of
     // chunk c-1's stage before the DMA of chunk c+AHEAD overwrites it.
     constexpr int DEFER = 4;
-    f4g a[FM][8];
-    float bb[FN][32];
+    f4g a[FM][AQ];
+    float bb[FN][KSTEP];
     auto wait_chunk = [&](int c) {            // chunk c's DMA has landed (everyone's)
-        // outstanding in issue order: ..., chunk c, [chunk c+1] (ITEMS each)
-        if (AHEAD == 2 && c + 1 < nch) __builtin_amdgcn_s_waitcnt(g32_vmcnt(ITEMS));
+        // outstanding in issue order: ..., chunk c, then chunks c+1 ..
+        // min(c + AHEAD - 1, nch - 1) (ITEMS loads each) that may stay in flight
+        const int later = nch - 1 - c < AHEAD - 1 ? nch - 1 - c : AHEAD - 1;
+        if (AHEAD >= 3 && later >= 2) __builtin_amdgcn_s_waitcnt(g32_vmcnt(2 * ITEMS));
+        else if (AHEAD >= 2 && later >= 1) __builtin_amdgcn_s_waitcnt(g32_vmcnt(ITEMS));
         else __builtin_amdgcn_s_waitcnt(g32_vmcnt(0));
         // LDS-only workgroup barrier: this wave's LDS reads are complete; the
         // loads of later chunks stay in flight.
@@ -247,23 +270,23 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a[i][j] = *(const f4g*)&S[aoff[i][j]];
+            for (int j = 0; j < AQ; ++j) a[i][j] = *(const f4g*)&S[aoff[i][j]];
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int s = 0; s < 32; ++s) bb[j][s] = S[boff[j] + s * BN];
+            for (int s = 0; s < KSTEP; ++s) bb[j][s] = S[boff[j] + s * BN];
     };
     if (nch > 0) {
         wait_chunk(0);
         read_chunk(smg);
     }
-    int st = 0;
+    int st = 0;                                         // c % NST
     for (int c = 0; c < nch; ++c) {
-        const int sta = AHEAD == 2 ? (st == 0 ? 2 : st - 1) : (st ^ 1);     // (c + AHEAD) % NST
+        const int sta = st == 0 ? AHEAD : st - 1;       // (c + AHEAD) % NST
         float* NA = smg + sta * STAGE;
         const bool more = c + AHEAD < nch;
 #pragma unroll
-        for (int s = 0; s < 32 - DEFER; ++s) {
+        for (int s = 0; s < KSTEP - DEFER; ++s) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -278,12 +301,12 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
         f4g al[FM];
         float bl[FN][DEFER];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) al[i] = a[i][7];
+        for (int i = 0; i < FM; ++i) al[i] = a[i][AQ - 1];
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int u = 0; u < DEFER; ++u) bl[j][u] = bb[j][32 - DEFER + u];
-        st = AHEAD == 2 ? (st == 2 ? 0 : st + 1) : (st ^ 1);
+            for (int u = 0; u < DEFER; ++u) bl[j][u] = bb[j][KSTEP - DEFER + u];
+        st = st == NST - 1 ? 0 : st + 1;
         if (c + 1 < nch) {
             wait_chunk(c + 1);
             read_chunk(smg + st * STAGE);
@@ -297,25 +320,28 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(al[i][u], bl[j][u], acc[i][j], 0, 0, 0);
     }
 
-    if (KS == 2) {                 // group 1's sums through LDS into group 0's
+    if (KS > 1) {                  // groups 1..KS-1's sums through LDS into group 0's
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stages no longer read
+        constexpr int PART = 4 * FM * FN * 16 * 64;     // floats of one group's partial tile
         float* const red = sm + wl * (FM * FN * 16 * 64) + lane;
-        if (kg == 1) {
+        if (kg > 0) {
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) red[((i * FN + j) * 16 + e) * 64] = acc[i][j][e];
+                    for (int e = 0; e < 16; ++e) red[(kg - 1) * PART + ((i * FN + j) * 16 + e) * 64] = acc[i][j][e];
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kg == 1) return;
+        if (kg > 0) return;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int g = 0; g < KS - 1; ++g)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((i * FN + j) * 16 + e) * 64];
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[i][j][e] += red[g * PART + ((i * FN + j) * 16 + e) * 64];
     }
 
     // ---- epilogue: lane l, register e of block (i, j) <->
@@ -352,7 +378,7 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
 }  // namespace
 
 namespace {
-struct G32Tile { int bm, bn, nst, ks = 1; };
+struct G32Tile { int bm, bn, nst, ks = 1, kc = 64; };
 
 // Tile choice.  Measured on MI355X (config 1 and the ResNet-50 batch-64
 // layers): 64 x 64 tiles, two or three workgroups per CU, beat the 128-row
@@ -361,7 +387,7 @@ struct G32Tile { int bm, bn, nst, ks = 1; };
 // (sweeps).  Three stages when the 64 x 64 grid is a single wave of workgroups.
 G32Tile pick_g32(int M, int N, int K) {
     const long long cus = num_cus();
-    const int nch = (K + G32_KC - 1) / G32_KC;
+    const int nch = (K + 63) / 64;
     auto tiles = [&](int bm, int bn) {
         return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
@@ -382,42 +408,52 @@ G32Tile pick_g32(int M, int N, int K) {
     return G32Tile{64, 64, deep ? 3 : 2};
 }
 
-template <int BM, int BN, int NST, bool CONV, int KS = 1>
+template <int BM, int BN, int NST, bool CONV, int KS = 1, int KC = 64>
 bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C,
                 int ldc, const float* bias, int act, hipStream_t s, const float* res, int ldr,
                 const G32Conv& cv) {
-    const int nch = ((K + G32_KC - 1) / G32_KC + KS - 1) / KS;
-    // LDS holds only the stages that can be in use (per group)
+    const int nch = ((K + KC - 1) / KC + KS - 1) / KS;
+    // LDS holds only the stages that can be in use (per group); with K groups
+    // the partial tiles of groups 1..KS-1 are summed through the same memory
     const int stages = KS > 1 ? NST : (nch < NST ? (nch < 1 ? 1 : nch) : NST);
-    const size_t lds = (size_t)KS * stages * g32_stage(BM, BN) * 4;
+    constexpr size_t kPart = (size_t)(KS - 1) * BM * BN * 4;
+    const size_t lds0 = (size_t)KS * stages * g32_stage(BM, BN, KC) * 4;
+    const size_t lds = lds0 > kPart ? lds0 : kPart;
+    constexpr size_t kMax = (size_t)KS * NST * g32_stage(BM, BN, KC) * 4;
+    static_assert(kMax >= kPart && kMax <= 160 * 1024, "LDS budget");
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV, KS>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  KS * NST * g32_stage(BM, BN) * 4);
+        (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV, KS, KC>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMax);
     }
     dim3 grid((unsigned)(((N + BN - 1) / BN) * ((M + BM - 1) / BM)));
-    ACFUN_LAUNCH("k_gemm32", (k_gemm32<BM, BN, NST, CONV, KS>), grid, dim3(256 * KS), lds, s, A, B, C,
-                 bias, res, M, N, K, lda, ldb, ldc, ldr, act, cv);
+    ACFUN_LAUNCH("k_gemm32", (k_gemm32<BM, BN, NST, CONV, KS, KC>), grid, dim3(256 * KS), lds, s, A, B,
+                 C, bias, res, M, N, K, lda, ldb, ldc, ldr, act, cv);
     return check_launch("k_gemm32");
 }
 
 // Tile-search candidates (kind "g32"): 64 x 64 with 2 or 3 stages, 64 x 64
-// with two K groups, 128 x 64 with 2 or 3 stages, 128 x 128.
-constexpr G32Tile kG32Cand[] = {{64, 64, 2, 1}, {64, 64, 3, 1}, {64, 64, 2, 2},
-                                {128, 64, 2, 1}, {128, 64, 3, 1}, {128, 128, 2, 1}};
-constexpr int kG32NC = 6;
+// with two K groups, 128 x 64 with 2 or 3 stages, 128 x 128; then 32-wide
+// chunks: 64 x 64 with four K groups (1,024 threads, four waves per SIMD),
+// and with two K groups three or four stages deep.
+constexpr G32Tile kG32Cand[] = {{64, 64, 2, 1},     {64, 64, 3, 1},     {64, 64, 2, 2},
+                                {128, 64, 2, 1},    {128, 64, 3, 1},    {128, 128, 2, 1},
+                                {64, 64, 2, 4, 32}, {64, 64, 3, 2, 32}, {64, 64, 4, 2, 32}};
+constexpr int kG32NC = 9;
 
 int g32_index(const G32Tile& t) {
     for (int i = 0; i < kG32NC; ++i)
         if (kG32Cand[i].bm == t.bm && kG32Cand[i].bn == t.bn && kG32Cand[i].nst == t.nst &&
-            kG32Cand[i].ks == t.ks)
+            kG32Cand[i].ks == t.ks && kG32Cand[i].kc == t.kc)
             return i;
     return 0;
 }
-// Two K groups need chunks for both (the heuristic takes them from 8 chunks).
-bool g32_admits(int c, int K) { return kG32Cand[c].ks == 1 || (K + G32_KC - 1) / G32_KC >= 4; }
+// K groups need chunks for every group: at least two each.
+bool g32_admits(int c, int K) {
+    const G32Tile& t = kG32Cand[c];
+    return t.ks == 1 || (K + t.kc - 1) / t.kc >= 2 * t.ks;
+}
 
 template <bool CONV>
 bool launch_cand(int c, int M, int N, int K, const float* A, int lda, const float* B, int ldb,
@@ -429,6 +465,9 @@ bool launch_cand(int c, int M, int N, int K, const float* A, int lda, const floa
         case 3: return launch_g32<128, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         case 4: return launch_g32<128, 64, 3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         case 5: return launch_g32<128, 128, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 6: return launch_g32<64, 64, 2, CONV, 4, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 7: return launch_g32<64, 64, 3, CONV, 2, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 8: return launch_g32<64, 64, 4, CONV, 2, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         default: return launch_g32<64, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
     }
 }
