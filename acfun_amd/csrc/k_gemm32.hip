@@ -375,10 +375,268 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
     }
 }
 
+// ---------------------------------------------------------------- k_gemm32p
+// Persistent form for short K and many tiles, where one tile per workgroup
+// leaves a tile's load latency and epilogue exposed: each workgroup runs a
+// list of 64 x 64 tiles back to back, and one DMA stream of (tile, chunk)
+// items runs NST - 1 chunks ahead of the MFMAs across tile boundaries, so
+// the next tile's operands load during the current tile's last chunks and
+// its epilogue.  K in chunks of 32 (the KC = 32 stage layouts above), NST
+// stages of 16 KB, three workgroups per CU.  Tiles: XCD x = blockIdx % 8 owns
+// a contiguous run of k_gemm32's tile order, which its workgroups take round
+// robin.  Every iteration issues the same number of DMA loads (items past
+// the workgroup's last chunk are issued out of range and write zeros to a
+// stage no chunk reads again), so every wait of the loop is the same.
+// Epilogue: the waves write the tile's sums into the stage of its last chunk
+// (every wave has read it), then thread t forms quad t % 16 of rows t/16 +
+// 16i: + bias, + the fused residual, the activation, one 16-byte store (rows
+// and quads past M and N element by element).  Per output the arithmetic is
+// k_gemm32's: the chunk sums in k order, then fl(fl(sum + bias) + res).
+template <int NST, bool CONV>
+__global__ __launch_bounds__(256) void k_gemm32p(const float* __restrict__ A,
+                                                 const float* __restrict__ B,
+                                                 float* __restrict__ C,
+                                                 const float* __restrict__ bias,
+                                                 const float* __restrict__ res, int M, int N, int K,
+                                                 int lda, int ldb, int ldc, int ldr, int act, int vec,
+                                                 unsigned a_bytes, G32Conv cv) {
+    constexpr int BM = 64, BN = 64, KC = 32;
+    constexpr int STAGE = g32_stage(BM, BN, KC);        // 4096 floats
+    constexpr int SB = BM * KC;
+    constexpr int QA = KC / 4, RPI = 64 / QA;           // 8 quads per A row, 8 rows per instruction
+    constexpr int AIT = BM * QA / 256, BIT = KC * BN / 1024;
+    constexpr int ITEMS = AIT + BIT;
+    constexpr int BQ = BN / 4, KSTEP = KC / 2, AQ = KC / 8;
+    constexpr int AHEAD = NST - 1;
+    static_assert(NST >= 2 && AIT == 2 && BIT == 2, "k_gemm32p layout");
+    constexpr unsigned kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM, total = gm * gn;
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    int t0, tstr, cnt;
+    if ((G & 7) == 0) {
+        const int x = b & 7, i = b >> 3, gx = G >> 3;
+        const int sx = (int)(((long long)x * total) >> 3);
+        const int ex = (int)(((long long)(x + 1) * total) >> 3);
+        t0 = sx + i;
+        tstr = gx;
+        cnt = ex > t0 ? (ex - t0 + gx - 1) / gx : 0;
+    } else {
+        t0 = b;
+        tstr = G;
+        cnt = b < total ? (total - b + G - 1) / G : 0;
+    }
+    const int nch = (K + KC - 1) / KC;
+    const int nit = cnt * nch;
+    if (nit == 0) return;                               // uniform per workgroup
+    constexpr int GRP = 4;
+    auto tile_of = [&](int k, int& m0, int& n0) {      // k-th tile of this workgroup
+        const int L = t0 + k * tstr;
+        const int grp = L / (GRP * gn), gbase = grp * GRP;
+        const int rows = gm - gbase < GRP ? gm - gbase : GRP;
+        const int r_in = L - grp * GRP * gn;
+        m0 = (gbase + r_in % rows) * BM;
+        n0 = (r_in / rows) * BN;
+    };
+
+    const __amdgpu_buffer_rsrc_t ares =
+        __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)B, (short)0, (int)((long long)K * ldb * 4), 0x00020000);
+    // DMA slots of this lane (the KC = 32 layouts): A row arow + 32t, quad aq;
+    // B k row krow[t], quad bq[t]
+    const int arow = RPI * wave + lane / QA;
+    const int aq = (lane & 7) ^ ((arow >> 1) & 7);
+    int bkr[BIT], bq4[BIT];
+#pragma unroll
+    for (int t = 0; t < BIT; ++t) {
+        const int slot = 64 * (wave + 4 * t) + lane;
+        bkr[t] = slot / BQ;
+        bq4[t] = 4 * ((slot % BQ) ^ ((bkr[t] & (KC / 2)) ? 8 : 0));
+    }
+    const bool kragged = (K & (KC - 1)) != 0;
+    // issue cursor: tile ik of this workgroup, chunk ic; its rows' descriptors
+    int ik = 0, ic = 0, in0 = 0;
+    unsigned arowoff[AIT];                              // plain: byte offset of the row (kOOB past M)
+    int cbase[AIT];                                     // CONV: tap-(0,0) offset, in-image taps
+    unsigned long long cmask[AIT];
+    auto setup = [&](int k) {
+        int m0, n0;
+        tile_of(k, m0, n0);
+        in0 = n0;
+#pragma unroll
+        for (int t = 0; t < AIT; ++t) {
+            const int m = m0 + arow + 32 * t;
+            if (!CONV) {
+                arowoff[t] = m < M ? (unsigned)(m * lda + 4 * aq) * 4u : kOOB;
+            } else {
+                cbase[t] = 0;
+                cmask[t] = 0;
+                if (m < M) {
+                    const int hw = cv.OH * cv.OW;
+                    const int n = m / hw, rem = m - n * hw;
+                    const int oh = rem / cv.OW, ow = rem - oh * cv.OW;
+                    const int ih0 = oh * cv.stride - cv.pad, iw0 = ow * cv.stride - cv.pad;
+                    cbase[t] = ((n * cv.H + ih0) * cv.W + iw0) * cv.Cin * 4 + 16 * aq;
+                    unsigned rm = 0, cm = 0;
+                    for (int d = 0; d < 8; ++d) {
+                        rm |= ((unsigned)(ih0 + d) < (unsigned)cv.H) ? (1u << d) : 0u;
+                        cm |= ((unsigned)(iw0 + d) < (unsigned)cv.W) ? (1u << d) : 0u;
+                    }
+                    unsigned long long mk = 0;
+                    for (int d = 0; d < 8; ++d)
+                        if ((rm >> d) & 1u) mk |= (unsigned long long)cm << (8 * d);
+                    cmask[t] = mk;
+                }
+            }
+        }
+    };
+    // item t of the issue cursor's chunk into stage st (out of range when !live)
+    auto issue = [&](int t, float* st, bool live) {
+        const int k0 = ic * KC;
+        if (t < AIT) {
+            unsigned v = kOOB;
+            if (live) {
+                if (CONV) {
+                    const int tap = k0 / cv.Cin, ic0 = k0 - tap * cv.Cin;
+                    const int kh = tap / cv.KW, kw = tap - kh * cv.KW;
+                    if ((cmask[t] >> (kh * 8 + kw)) & 1ull)
+                        v = (unsigned)(cbase[t] + ((kh * cv.W + kw) * cv.Cin + ic0) * 4);
+                } else if (arowoff[t] != kOOB && !(kragged && k0 + 4 * aq >= K)) {
+                    v = arowoff[t] + (unsigned)k0 * 4u;
+                }
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void32*)(st + (wave + 4 * t) * 256), 16, v, 0,
+                                                     0, 0);
+        } else {
+            const int tt = t - AIT;
+            const unsigned v = live && in0 + bq4[tt] < N && k0 + bkr[tt] < K
+                                   ? (unsigned)((k0 + bkr[tt]) * ldb + in0 + bq4[tt]) * 4u
+                                   : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void32*)(st + SB + (wave + 4 * tt) * 256), 16, v,
+                                                     0, 0, 0);
+        }
+    };
+    auto advance = [&]() {
+        if (++ic == nch) {
+            ic = 0;
+            if (++ik < cnt) setup(ik);
+        }
+    };
+
+    // per-lane read offsets within a stage (floats): in k-step s lane half h
+    // carries k = 16h + s
+    const int r = lane & 31, h = lane >> 5;
+    int aoff[AQ];
+    const int rowA = 32 * wm + r;
+#pragma unroll
+    for (int j = 0; j < AQ; ++j) aoff[j] = (rowA * 8 + ((4 * h + j) ^ ((rowA >> 1) & 7))) * 4;
+    const int col = 32 * wn + r;
+    const int boff = SB + ((KSTEP * h) * BQ + ((col >> 2) ^ (h << 3))) * 4 + (col & 3);
+
+    f16v acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+    setup(0);
+#pragma unroll
+    for (int a = 0; a < AHEAD; ++a) {
+        const bool live = a < nit;
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t) issue(t, sm + a * STAGE, live);
+        if (live) advance();
+    }
+
+    int st = 0, ck = 0, cc = 0;
+    for (int g = 0; g < nit; ++g) {
+        // Chunk g has landed once at most the (AHEAD - 1) * ITEMS loads issued
+        // after it are outstanding: loads complete in issue order, and the
+        // epilogue's inline-asm stores queued among them only lengthen the wait.
+        __builtin_amdgcn_s_waitcnt(g32_vmcnt((AHEAD - 1) * ITEMS));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float* S = sm + st * STAGE;
+        float* NA = sm + (st == 0 ? NST - 1 : st - 1) * STAGE;   // (g + AHEAD) % NST
+        const bool more = g + AHEAD < nit;
+        f4g a[AQ];
+        float bb[KSTEP];
+#pragma unroll
+        for (int j = 0; j < AQ; ++j) a[j] = *(const f4g*)&S[aoff[j]];
+#pragma unroll
+        for (int k = 0; k < KSTEP; ++k) bb[k] = S[boff + k * BN];
+#pragma unroll
+        for (int k = 0; k < KSTEP; ++k) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[k >> 2][k & 3], bb[k], acc, 0, 0, 0);
+            if (k == 1) {
+#pragma unroll
+                for (int t = 0; t < ITEMS; ++t) issue(t, NA, more);
+            }
+        }
+        if (more) advance();
+        st = st == NST - 1 ? 0 : st + 1;
+        if (++cc < nch) continue;
+        cc = 0;
+        // ---- epilogue of tile ck through the stage of its last chunk
+        int m0, n0;
+        tile_of(ck, m0, n0);
+        ++ck;
+        float* const stg = sm + (st == 0 ? NST - 1 : st - 1) * STAGE;
+        auto sidx = [](int rr, int cq) { return rr * 64 + ((((cq >> 2) ^ (((rr >> 2) & 1) << 3))) << 2) + (cq & 3); };
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int rr = 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+            stg[sidx(rr, col)] = acc[e];
+            acc[e] = 0.f;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int q = tid & 15, n = n0 + 4 * q;
+        f4g bq = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+            if (vec && n + 4 <= N) {
+                bq = *(const f4g*)(bias + n);
+            } else {
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) bq[kq] = n + kq < N ? bias[n + kq] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = (tid >> 4) + 16 * i, m = m0 + rr;
+            if (m >= M) continue;
+            f4g v = *(const f4g*)&stg[sidx(rr, 4 * q)];
+            float* dst = C + (long long)m * ldc + n;
+            if (vec && n + 4 <= N) {
+                if (bias) v = v + bq;
+                if (res) v = v + *(const f4g*)(res + (long long)m * ldr + n);
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) v[kq] = act_apply(v[kq], act);
+                // s_nop: a VALU write to the data registers of a store of more
+                // than 8 bytes needs a wait state after it
+                asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
+            } else {
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                    if (n + kq >= N) continue;
+                    float w = v[kq];
+                    if (bias) w = w + bq[kq];
+                    if (res) w = w + res[(long long)m * ldr + n + kq];
+                    w = act_apply(w, act);
+                    asm volatile("global_store_dword %0, %1, off" ::"v"(dst + kq), "v"(w) : "memory");
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(g32_vmcnt(0));          // the out-of-range loads and the stores
+}
+
 }  // namespace
 
 namespace {
-struct G32Tile { int bm, bn, nst, ks = 1, kc = 64; };
+struct G32Tile { int bm, bn, nst, ks = 1, kc = 64, pers = 0; };
 
 // Tile choice.  Measured on MI355X (config 1 and the ResNet-50 batch-64
 // layers): 64 x 64 tiles, two or three workgroups per CU, beat the 128-row
@@ -404,6 +662,15 @@ G32Tile pick_g32(int M, int N, int K) {
     static int ks_off = -1;
     if (ks_off < 0) ks_off = getenv("ACFUN_G32_NOKS") ? 1 : 0;
     if (!ks_off && nch >= 8 && tiles(64, 64) <= cus) return G32Tile{64, 64, 2, 2};
+    // Two or more 64 x 64 tiles per CU: the persistent kernel, two stages,
+    // four workgroups per CU (config 5, fp32: 5.71 -> 5.09 ms per batch of 64;
+    // three stages at three per CU: 5.33 ms).  ACFUN_G32P=0 turns it off.
+    static int pers = -1;
+    if (pers < 0) {
+        const char* e = getenv("ACFUN_G32P");
+        pers = e && atoi(e) == 0 ? 0 : 1;
+    }
+    if (pers && tiles(64, 64) >= 2 * cus) return G32Tile{64, 64, 2, 1, 32, 1};
     const bool deep = nch > 2 && tiles(64, 64) < 2 * cus;
     return G32Tile{64, 64, deep ? 3 : 2};
 }
@@ -433,25 +700,54 @@ bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, in
     return check_launch("k_gemm32");
 }
 
+// Persistent launch (k_gemm32p): as many workgroups as fit on a CU (four
+// with two stages, three with three), at most one per tile, a multiple of 8
+// so that each XCD owns a run of tiles.
+template <int NST, bool CONV>
+bool launch_g32p(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                 const float* bias, int act, hipStream_t s, const float* res, int ldr, const G32Conv& cv) {
+    constexpr size_t lds = (size_t)NST * g32_stage(64, 64, 32) * 4;
+    static_assert(lds <= 160 * 1024 / 2, "two workgroups per CU at least");
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_gemm32p<NST, CONV>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+    }
+    const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
+    const long long slots = (NST == 2 ? 4ll : 3ll) * num_cus(), need = (tiles + 7) / 8 * 8;
+    const unsigned grid = (unsigned)(slots < need ? slots : need);
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    const int vec = al(C) && ldc % 4 == 0 && (!bias || al(bias)) && (!res || (al(res) && ldr % 4 == 0));
+    const unsigned a_bytes = CONV ? cv.bytes : (unsigned)((long long)M * lda * 4);
+    ACFUN_LAUNCH("k_gemm32", (k_gemm32p<NST, CONV>), dim3(grid), dim3(256), lds, s, A, B, C, bias, res, M, N,
+                 K, lda, ldb, ldc, ldr, act, vec, a_bytes, cv);
+    return check_launch("k_gemm32p");
+}
+
 // Tile-search candidates (kind "g32"): 64 x 64 with 2 or 3 stages, 64 x 64
 // with two K groups, 128 x 64 with 2 or 3 stages, 128 x 128; then 32-wide
 // chunks: 64 x 64 with four K groups (1,024 threads, four waves per SIMD),
-// and with two K groups three or four stages deep.
-constexpr G32Tile kG32Cand[] = {{64, 64, 2, 1},     {64, 64, 3, 1},     {64, 64, 2, 2},
-                                {128, 64, 2, 1},    {128, 64, 3, 1},    {128, 128, 2, 1},
-                                {64, 64, 2, 4, 32}, {64, 64, 3, 2, 32}, {64, 64, 4, 2, 32}};
-constexpr int kG32NC = 9;
+// and with two K groups three or four stages deep; then the persistent
+// kernel with 2 or 3 stages.
+constexpr G32Tile kG32Cand[] = {{64, 64, 2, 1},        {64, 64, 3, 1},        {64, 64, 2, 2},
+                                {128, 64, 2, 1},       {128, 64, 3, 1},       {128, 128, 2, 1},
+                                {64, 64, 2, 4, 32},    {64, 64, 3, 2, 32},    {64, 64, 4, 2, 32},
+                                {64, 64, 2, 1, 32, 1}, {64, 64, 3, 1, 32, 1}};
+constexpr int kG32NC = 11;
 
 int g32_index(const G32Tile& t) {
     for (int i = 0; i < kG32NC; ++i)
         if (kG32Cand[i].bm == t.bm && kG32Cand[i].bn == t.bn && kG32Cand[i].nst == t.nst &&
-            kG32Cand[i].ks == t.ks && kG32Cand[i].kc == t.kc)
+            kG32Cand[i].ks == t.ks && kG32Cand[i].kc == t.kc && kG32Cand[i].pers == t.pers)
             return i;
     return 0;
 }
 // K groups need chunks for every group: at least two each.
-bool g32_admits(int c, int K) {
+// The persistent kernel addresses A through one 32-bit buffer resource.
+bool g32_admits(int c, int K, long long a_bytes) {
     const G32Tile& t = kG32Cand[c];
+    if (t.pers) return a_bytes < 0x7fffffffll;
     return t.ks == 1 || (K + t.kc - 1) / t.kc >= 2 * t.ks;
 }
 
@@ -468,6 +764,8 @@ bool launch_cand(int c, int M, int N, int K, const float* A, int lda, const floa
         case 6: return launch_g32<64, 64, 2, CONV, 4, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         case 7: return launch_g32<64, 64, 3, CONV, 2, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         case 8: return launch_g32<64, 64, 4, CONV, 2, 32>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 9: return launch_g32p<2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
+        case 10: return launch_g32p<3, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
         default: return launch_g32<64, 64, 2, CONV>(M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
     }
 }
@@ -490,7 +788,7 @@ TuneMaker g32_maker(int M, int N, int K, const G32Conv& cv) {
             return TuneRunner();
         return [=](int cand, hipStream_t st) {
             if (cand < 0) cand = g32_index(pick_g32(M, N, K));     // the built-in choice
-            if (!g32_admits(cand, K)) return false;
+            if (!g32_admits(cand, K, CONV ? (long long)cv.bytes : (long long)M * K * 4)) return false;
             return launch_cand<CONV>(cand, M, N, K, a->as<float>(), CONV ? cv.Cin : K, b->as<float>(), N,
                                      c->as<float>(), N, nullptr, 0, st, nullptr, 0, cv);
         };
@@ -514,7 +812,9 @@ bool launch_gemm32(int M, int N, int K, const float* A, int lda, const float* B,
             c = tune_lookup("g32", key, kG32NC, &rec);
         }
     }
-    if (c < 0 || !g32_admits(c, K)) c = g32_index(pick_g32(M, N, K));
+    const long long a_bytes = CONV ? (long long)cv.bytes : (long long)M * lda * 4;
+    if (c < 0 || !g32_admits(c, K, a_bytes)) c = g32_index(pick_g32(M, N, K));
+    if (!g32_admits(c, K, a_bytes)) c = 0;
     return launch_cand<CONV>(c, M, N, K, A, lda, B, ldb, C, ldc, bias, act, s, res, ldr, cv);
 }
 }  // namespace

@@ -41,6 +41,33 @@ def test_gemm_f32(gpu, rng, M, N, K, epi):
     assert rel_err(got, want) < GEMM_TOL, rel_err(got, want)
 
 
+@pytest.mark.parametrize("M,N,K", [(2065, 1028, 200), (4096, 512, 64), (8192, 256, 4), (2049, 1040, 1032)])
+@pytest.mark.parametrize("epi", [0, 1])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_gemm_persistent(gpu, rng, M, N, K, epi, offset):
+    """Shapes of at least two 64 x 64 tiles per CU take the persistent kernel
+    (k_gemm32p): ragged M, N and K against 32-wide chunks, bias and ReLU, and C
+    offset by one float so that its rows are not 16-byte aligned (element
+    stores) -- through the device entry point, against the f64 product."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    tA, tB, tb = (torch.from_numpy(a).to(dev) for a in (A, B, bias))
+    buf = torch.full((M * N + 4,), float("nan"), device=dev)
+    torch.cuda.synchronize()
+    rc = gpu.acfun_dev_gemm_epi(M, N, K, tA.data_ptr(), tB.data_ptr(), buf.data_ptr() + 4 * offset,
+                                tb.data_ptr() if epi else None, epi, None)
+    torch.cuda.synchronize()
+    assert rc == 0
+    got = buf.cpu().numpy()[offset:offset + M * N].reshape(M, N)
+    want = oracle.gemm_f64(A, B)
+    if epi:
+        want = np.maximum(want + bias, 0)
+    assert rel_err(got, want) < GEMM_TOL, rel_err(got, want)
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 96, 300), (64, 64, 64), (1, 1, 1), (130, 70, 7),
                                    (1024, 1024, 1024), (33, 40, 0), (7, 300, 64), (290, 5, 33)])
 def test_gemm_bf16(gpu, rng, M, N, K):

@@ -43,10 +43,10 @@ def test_tile_search_caches_and_keeps_parity(gpu, tmp_path):
 def _forced_cache():
     lines = []
     for c, (M, N, K) in enumerate(R.G32_GEMM):
-        lines.append(f"gfx950 g32 9 0,{M},{N},{K} {c}")
+        lines.append(f"gfx950 g32 11 0,{M},{N},{K} {c}")
     for c, (N, H, W, Cin, KH, KW, Cout, s, p) in enumerate(R.G32_CONV):
         OH, OW = oracle.out_hw(H, W, KH, KW, s, p)
-        lines.append(f"gfx950 g32 9 1,{N * OH * OW},{Cout},{KH * KW * Cin},{H},{W},{Cin},{KW},{s},{p},{OH},{OW} {c}")
+        lines.append(f"gfx950 g32 11 1,{N * OH * OW},{Cout},{KH * KW * Cin},{H},{W},{Cin},{KW},{s},{p},{OH},{OW} {c}")
     for c, (N, H, W, Cin, KH, KW, Cout, s, p) in enumerate(R.I8):
         OH, OW = oracle.out_hw(H, W, KH, KW, s, p)
         Cinp = (Cin + 15) // 16 * 16

@@ -27,8 +27,8 @@ GEMM_TOL, WINO_TOL = 1e-4, 1e-3
 
 # (kind, shape) -> the cases the forced mode assigns to candidate c: shapes are
 # distinct per candidate so one cache file carries all assignments
-G32_GEMM = [(96 + 32 * c, 160, 256 + 64 * c) for c in range(9)]          # M, N, K
-G32_CONV = [(2, 15 + c, 13, 64, 3, 3, 40, 2, 1) for c in range(9)]         # N,H,W,Cin,KH,KW,Cout,s,p
+G32_GEMM = [(96 + 32 * c, 160, 256 + 64 * c) for c in range(11)]         # M, N, K
+G32_CONV = [(2, 15 + c, 13, 64, 3, 3, 40, 2, 1) for c in range(11)]        # N,H,W,Cin,KH,KW,Cout,s,p
 I8 = [(2, 10 + c, 12, 64, 3, 3, 48, 2, 1) for c in range(5)]              # strided: the GEMM route
 W23 = [(0, 2, 40, 36 + 2 * c, 32, 40) for c in range(4)] + [(4, 3, 7, 7, 64, 32)] + \
       [(c, 3, 18, 20, 24, 32) for c in (2, 3)]                             # cand, N, H, W, Cin, Cout
