@@ -8,9 +8,11 @@
 //   2. an idle block: no work that used it can still be running;
 //   3. when blocks of the size sit cached on other streams and those streams
 //      hold at least kReclaimBytes of cache: the device is synchronized once,
-//      which finishes every use of every cached block whatever stream (live
-//      or since destroyed) queued it, every cached block of the device becomes
-//      idle, and the allocation takes one of them;
+//      which finishes every use of the blocks freed before the sync began
+//      whatever stream (live or since destroyed) queued it; those blocks
+//      become idle, and the allocation takes one of them.  A block that
+//      another host thread frees while the sync runs keeps its stream: the
+//      work it was freed after may have been queued after the sync began;
 //   4. a new block from the backend; if that fails, every cached block of the
 //      device is released (after a device sync) and the allocation retried.
 // A caller that keeps to one stream never pays for 3.  A caller that creates
@@ -64,16 +66,29 @@ class PoolCore {
             }
         }
         if (reclaim) {                                         // 3. reclaim other streams' blocks
+            unsigned long long seq0;
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                seq0 = seq_;                                   // frees up to here precede the sync
+            }
             b_.sync_device();
             std::lock_guard<std::mutex> lk(mu_);
             ++reclaims_;
-            for (auto& kv : free_)
-                if (kv.first.first == dev)
-                    for (auto& bl : kv.second) bl.idle = true;
-            for (auto it = stream_bytes_.begin(); it != stream_bytes_.end();)
-                it = it->first.first == dev ? stream_bytes_.erase(it) : std::next(it);
+            for (auto& kv : free_) {
+                if (kv.first.first != dev) continue;
+                for (auto& bl : kv.second) {
+                    if (bl.idle || bl.seq > seq0) continue;
+                    bl.idle = true;
+                    auto sb = stream_bytes_.find({dev, bl.s});
+                    if (sb != stream_bytes_.end() && (sb->second -= kv.first.second) == 0) stream_bytes_.erase(sb);
+                }
+            }
             auto it = free_.find({dev, rb});
-            if (it != free_.end() && !it->second.empty()) return take(dev, rb, it->second, 0);
+            if (it != free_.end()) {
+                auto& v = it->second;
+                for (size_t i = 0; i < v.size(); ++i)
+                    if (v[i].idle || v[i].s == s) return take(dev, rb, v, i);
+            }
         }
         void* p = b_.alloc(rb);                                // 4. new
         if (!p) {
@@ -109,7 +124,7 @@ class PoolCore {
         auto it = size_.find(p);
         if (it == size_.end()) return;
         const size_t rb = it->second;
-        free_[{dev, rb}].push_back(Block{p, s, false});
+        free_[{dev, rb}].push_back(Block{p, s, false, ++seq_});
         cached_[dev] += rb;
         stream_bytes_[{dev, s}] += rb;
     }
@@ -134,6 +149,7 @@ class PoolCore {
         void* p;
         Stream s;
         bool idle;
+        unsigned long long seq;                        // order of the free
     };
 
     // cached bytes of dev that belong to streams other than s (not idle)
@@ -162,6 +178,7 @@ class PoolCore {
     std::map<int, size_t> cached_;                             // cached bytes per device
     std::map<void*, size_t> size_;
     size_t reclaims_ = 0;
+    unsigned long long seq_ = 0;                       // frees so far
 };
 
 }  // namespace acfun

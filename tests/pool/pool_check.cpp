@@ -3,7 +3,9 @@
 // and exits 0 when every check holds.
 #include <cstdio>
 #include <cstdlib>
+#include <functional>
 #include <map>
+#include <vector>
 
 #include "../../acfun_amd/csrc/pool.hpp"
 
@@ -30,7 +32,11 @@ struct Mock {
         live.erase(p);
         std::free(p);
     }
-    void sync_device() { ++syncs; }
+    std::function<void()> on_sync;          // runs during a sync (another host thread)
+    void sync_device() {
+        ++syncs;
+        if (on_sync) on_sync();
+    }
 };
 
 using Pool = acfun::PoolCore<Mock, int>;
@@ -66,6 +72,25 @@ int main() {
         expect(m.allocs <= (int)(2 * bound), "stream-per-call growth bounded by the reclaim threshold");
         expect(m.syncs > 0 && m.syncs <= 2000 / (int)(bound - 2) + 1, "few reclaims");
         expect(pool.reclaims() == (size_t)m.syncs, "each sync is a reclaim");
+    }
+    {   // a block another thread frees while the reclaim's sync runs keeps its stream:
+        // the work it was freed after may have been queued after the sync began
+        Mock m;
+        Pool pool(m);
+        const size_t S = 8 << 20;
+        std::vector<void*> v;
+        for (int i = 0; i < 9; ++i) v.push_back(pool.alloc(0, S, 100 + i));   // 72 MiB on other streams
+        void* late = pool.alloc(0, S, 50);
+        for (int i = 0; i < 9; ++i) pool.free(0, v[i], 100 + i);
+        m.on_sync = [&]() { pool.free(0, late, 50); };
+        std::vector<void*> got{pool.alloc(0, S, 7)};                          // reclaims
+        m.on_sync = nullptr;
+        expect(m.syncs == 1, "one reclaim");
+        for (int i = 0; i < 9; ++i) got.push_back(pool.alloc(0, S, 7));       // the reclaimed blocks, one more
+        bool clean = m.syncs == 1;
+        for (void* g : got) clean = clean && g != late;
+        expect(clean, "a block freed during the sync is not handed to another stream");
+        expect(pool.alloc(0, S, 50) == late, "its own stream reuses it");
     }
     {   // a block of another live stream is never handed out without a sync
         Mock m;
