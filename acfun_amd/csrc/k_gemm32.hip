@@ -671,7 +671,11 @@ G32Tile pick_g32(int M, int N, int K) {
         pers = e && atoi(e) == 0 ? 0 : 1;
     }
     if (pers && tiles(64, 64) >= 2 * cus) return G32Tile{64, 64, 2, 1, 32, 1};
-    const bool deep = nch > 2 && tiles(64, 64) < 2 * cus;
+    // Three stages (one workgroup per CU) only when the tiles fit in one wave;
+    // between one and two tiles per CU two stages at two workgroups per CU
+    // (config 5's 392-tile layers: GEMM 3136 x 512 x 2048 94.9 -> 81.0 us,
+    // conv 3x3/2 14x14x512 203 -> 174 us).
+    const bool deep = nch > 2 && tiles(64, 64) <= cus;
     return G32Tile{64, 64, deep ? 3 : 2};
 }
 
