@@ -34,50 +34,81 @@ __device__ __forceinline__ unsigned bf16_bits(float f) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// One lane: 8 consecutive k of one row of A -> one 16-byte store.
+// One lane: 8 consecutive k of one row of A -> one 16-byte store (two 16-byte
+// loads when the row segment is whole and aligned).
 __device__ __forceinline__ void pack_a_bf16(long long t, const float* __restrict__ A, int M, int K,
-                                            int lda, unsigned short* __restrict__ Ab, int Kp) {
+                                            int lda, unsigned short* __restrict__ Ab, int Kp, bool va) {
     const int kq = Kp >> 3;
     if (t >= (long long)M * kq) return;
     const int m = (int)(t / kq), k0 = (int)(t - (long long)m * kq) * 8;
     const float* src = A + (long long)m * lda + k0;
+    float v[8];
+    if (va && k0 + 8 <= K) {
+        const float4 x0 = *(const float4*)src, x1 = *(const float4*)(src + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = k0 + e < K ? src[e] : 0.f;
+    }
     unsigned w[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const int k = k0 + 2 * p;
-        const unsigned lo = k < K ? bf16_bits(src[2 * p]) : 0u;
-        const unsigned hi = k + 1 < K ? bf16_bits(src[2 * p + 1]) : 0u;
+        const unsigned lo = k0 + 2 * p < K ? bf16_bits(v[2 * p]) : 0u;
+        const unsigned hi = k0 + 2 * p + 1 < K ? bf16_bits(v[2 * p + 1]) : 0u;
         w[p] = lo | (hi << 16);
     }
     *(i4v*)(Ab + (long long)m * Kp + k0) = i4v{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
 
-// One lane: column n, 8 consecutive k of B -> one 16-byte store into Bt[n][k0..].
-// Lanes run n fastest, so each of the 8 loads is a coalesced row segment.
-__device__ __forceinline__ void pack_bt_bf16(long long t, const float* __restrict__ B, int K, int N,
-                                             int ldb, unsigned short* __restrict__ Bt, int Kp) {
-    if (t >= (long long)N * (Kp >> 3)) return;
-    const int kb = (int)(t / N), n = (int)(t - (long long)kb * N);
-    const int k0 = kb * 8;
-    unsigned w[4];
+// One block: a 64 k x 64 n tile of B -> Bt[n][k] through LDS.  Thread t loads
+// quad t % 16 of rows t / 16 + 16 i (256 contiguous bytes per row), rounds
+// each value (the same bf16_bits) and writes it transposed into LDS; then 8
+// threads store the 128 bytes of one Bt row segment (16 bytes each).  k past K
+// is zero (Kp padding); n past N is not stored.
+__device__ __forceinline__ void pack_bt_bf16(int tile, const float* __restrict__ B, int K, int N, int ldb,
+                                             unsigned short* __restrict__ Bt, int Kp, bool vb) {
+    __shared__ unsigned short tr[64][64 + 8];          // [n][k], rows padded by 16 bytes
+    const int t = (int)threadIdx.x;
+    const int ntn = (N + 63) >> 6;
+    const int kb = tile / ntn, nb = tile - kb * ntn;
+    const int k0 = kb * 64, n0 = nb * 64;
+    const int q = t & 15, n = n0 + 4 * q;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int k = k0 + 2 * p;
-        const unsigned lo = k < K ? bf16_bits(B[(long long)k * ldb + n]) : 0u;
-        const unsigned hi = k + 1 < K ? bf16_bits(B[(long long)(k + 1) * ldb + n]) : 0u;
-        w[p] = lo | (hi << 16);
+    for (int i = 0; i < 4; ++i) {
+        const int kr = (t >> 4) + 16 * i, k = k0 + kr;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (k < K) {
+            const float* src = B + (long long)k * ldb + n;
+            if (vb && n + 4 <= N) {
+                const float4 x = *(const float4*)src;
+                v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = n + e < N ? src[e] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tr[4 * q + e][kr] = k < K ? (unsigned short)bf16_bits(v[e]) : (unsigned short)0;
     }
-    *(i4v*)(Bt + (long long)n * Kp + k0) = i4v{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int nr = (t >> 3) + 32 * i, kc = 8 * (t & 7);
+        if (n0 + nr < N && k0 + kc < Kp)
+            *(i4v*)(Bt + (long long)(n0 + nr) * Kp + k0 + kc) = *(const i4v*)&tr[nr][kc];
+    }
 }
 
-// Both operands in one launch: blocks [0, nba) pack A, the rest B.
+// Both operands in one launch: blocks [0, nba) pack A (8 k per lane), the
+// rest B (a 64 x 64 tile per block).
 __global__ __launch_bounds__(256) void k_pack_bf16(const float* __restrict__ A, const float* __restrict__ B,
                                                    int M, int N, int K, int lda, int ldb, int Kp, int nba,
                                                    unsigned short* __restrict__ Ab,
-                                                   unsigned short* __restrict__ Bt) {
+                                                   unsigned short* __restrict__ Bt, int va, int vb) {
     const int b = (int)blockIdx.x;
-    if (b < nba) pack_a_bf16((long long)b * 256 + threadIdx.x, A, M, K, lda, Ab, Kp);
-    else pack_bt_bf16((long long)(b - nba) * 256 + threadIdx.x, B, K, N, ldb, Bt, Kp);
+    if (b < nba) pack_a_bf16((long long)b * 256 + threadIdx.x, A, M, K, lda, Ab, Kp, va != 0);
+    else pack_bt_bf16(b - nba, B, K, N, ldb, Bt, Kp, vb != 0);
 }
 
 constexpr int BF_BM = 64, BF_BN = 64, BF_NST = 4, BF_KB = 256;   // K chunk: 256 bytes, 128 bf16
@@ -199,14 +230,16 @@ bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, f
     }
     Scratch ab((size_t)M * Kp * 2, s), bt((size_t)N * Kp * 2, s);
     if (!ab.p || !bt.p) return false;
-    const long long na = (long long)M * (Kp / 8), nb = (long long)N * (Kp / 8);
-    const long long nba = (na + 255) / 256, nbb = (nb + 255) / 256;
+    const long long na = (long long)M * (Kp / 8);
+    const long long nba = (na + 255) / 256, nbb = (long long)(Kp / 64) * ((N + 63) / 64);
     if (nba + nbb >= (1ll << 31)) {
         set_error("acfun_gemm_bf16: operands too large");
         return false;
     }
+    auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    const int va = al(A) && K % 4 == 0, vb = al(B) && ldb % 4 == 0 && N % 4 == 0;
     ACFUN_LAUNCH("k_pack_bf16", k_pack_bf16, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, A, B, M, N, K, K, ldb, Kp,
-                       (int)nba, ab.as<unsigned short>(), bt.as<unsigned short>());
+                       (int)nba, ab.as<unsigned short>(), bt.as<unsigned short>(), va, vb);
     if (!check_launch("k_pack_bf16")) return false;
     static bool attr = false;
     constexpr int lds = BF_NST * BF_STG;
