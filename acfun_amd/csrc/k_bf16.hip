@@ -241,12 +241,13 @@ bool bf16_region(int M, int N, int ldb, int K, const float* A, const float* B, f
     ACFUN_LAUNCH("k_pack_bf16", k_pack_bf16, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, A, B, M, N, K, K, ldb, Kp,
                        (int)nba, ab.as<unsigned short>(), bt.as<unsigned short>(), va, vb);
     if (!check_launch("k_pack_bf16")) return false;
-    static bool attr = false;
     constexpr int lds = BF_NST * BF_STG;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_bf16mm, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    }
+        return true;
+    }();
+    (void)attr;
     const long long tiles = (long long)((M + BF_BM - 1) / BF_BM) * ((N + BF_BN - 1) / BF_BN);
     ACFUN_LAUNCH("k_bf16mm", k_bf16mm, dim3((unsigned)tiles), dim3(256), lds, s, ab.as<unsigned short>(),
                  bt.as<unsigned short>(), C, M, N, Kp, ldb, (unsigned)((long long)M * Kp * 2),

@@ -446,11 +446,10 @@ bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int 
     // kernel spreads K over the CUs that k_gemm32's tiles leave idle (batch-64
     // FC 2048 -> 1000: 40.8 -> 16.7 us; 4096 -> 4096: 76 -> 44 us).
     // ACFUN_FC_SPLITK=0 turns it off.
-    static int fcs = -1;
-    if (fcs < 0) {
+    static const bool fcs = [] {
         const char* e = getenv("ACFUN_FC_SPLITK");
-        fcs = e && atoi(e) == 0 ? 0 : 1;
-    }
+        return !(e && atoi(e) == 0);
+    }();
     const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
     const bool fc_split = fcs && K >= 1024 && t64 * 4 <= num_cus();
     if (K > 0 && !fc_split && gemm32_ok(M, N, K, A, lda, B, ldb))

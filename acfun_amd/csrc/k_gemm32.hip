@@ -650,26 +650,23 @@ G32Tile pick_g32(int M, int N, int K) {
         return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
     // ACFUN_G32_KMIN: the K from which the larger tiles are used (sweeps)
-    static int kmin = -1;
-    if (kmin < 0) {
+    static const int kmin = [] {
         const char* e = getenv("ACFUN_G32_KMIN");
-        kmin = e ? atoi(e) : 0x7fffffff;
-    }
+        return e ? atoi(e) : 0x7fffffff;
+    }();
     if (K >= kmin && N > 64 && tiles(128, 128) >= cus) return G32Tile{128, 128, 2};
     if (K >= kmin && tiles(128, 64) >= cus) return G32Tile{128, 64, nch > 2 ? 3 : 2};
     // At most one 64 x 64 tile per CU and a long K: two four-wave groups per
     // workgroup split K (two waves per SIMD instead of one).
-    static int ks_off = -1;
-    if (ks_off < 0) ks_off = getenv("ACFUN_G32_NOKS") ? 1 : 0;
+    static const bool ks_off = getenv("ACFUN_G32_NOKS") != nullptr;
     if (!ks_off && nch >= 8 && tiles(64, 64) <= cus) return G32Tile{64, 64, 2, 2};
     // Two or more 64 x 64 tiles per CU: the persistent kernel, two stages,
     // four workgroups per CU (config 5, fp32: 5.71 -> 5.09 ms per batch of 64;
     // three stages at three per CU: 5.33 ms).  ACFUN_G32P=0 turns it off.
-    static int pers = -1;
-    if (pers < 0) {
+    static const bool pers = [] {
         const char* e = getenv("ACFUN_G32P");
-        pers = e && atoi(e) == 0 ? 0 : 1;
-    }
+        return !(e && atoi(e) == 0);
+    }();
     if (pers && tiles(64, 64) >= 2 * cus) return G32Tile{64, 64, 2, 1, 32, 1};
     // Three stages (one workgroup per CU) only when the tiles fit in one wave;
     // between one and two tiles per CU two stages at two workgroups per CU
@@ -692,12 +689,13 @@ bool launch_g32(int M, int N, int K, const float* A, int lda, const float* B, in
     const size_t lds = lds0 > kPart ? lds0 : kPart;
     constexpr size_t kMax = (size_t)KS * NST * g32_stage(BM, BN, KC) * 4;
     static_assert(kMax >= kPart && kMax <= 160 * 1024, "LDS budget");
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_gemm32<BM, BN, NST, CONV, KS, KC>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMax);
-    }
+        return true;
+    }();
+    (void)attr;
     dim3 grid((unsigned)(((N + BN - 1) / BN) * ((M + BM - 1) / BM)));
     ACFUN_LAUNCH("k_gemm32", (k_gemm32<BM, BN, NST, CONV, KS, KC>), grid, dim3(256 * KS), lds, s, A, B,
                  C, bias, res, M, N, K, lda, ldb, ldc, ldr, act, cv);
@@ -712,12 +710,13 @@ bool launch_g32p(int M, int N, int K, const float* A, int lda, const float* B, i
                  const float* bias, int act, hipStream_t s, const float* res, int ldr, const G32Conv& cv) {
     constexpr size_t lds = (size_t)NST * g32_stage(64, 64, 32) * 4;
     static_assert(lds <= 160 * 1024 / 2, "two workgroups per CU at least");
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_gemm32p<NST, CONV>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
-    }
+        return true;
+    }();
+    (void)attr;
     const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
     const long long slots = (NST == 2 ? 4ll : 3ll) * num_cus(), need = (tiles + 7) / 8 * 8;
     const unsigned grid = (unsigned)(slots < need ? slots : need);

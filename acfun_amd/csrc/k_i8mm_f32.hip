@@ -13,12 +13,13 @@ template <int BM, int BN, int NST, int AM, int EPI>
 bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
     constexpr size_t lds = i8mm_lds(BM, BN, NST);
     static_assert(lds <= 160 * 1024, "k_i8mm LDS");
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_i8mm<BM, BN, NST, AM, EPI, OUT_F32>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    }
+        return true;
+    }();
+    (void)attr;
     i8mm_prepare(p, BM, BN);
     dim3 grid((unsigned)i8mm_grid(p, t));
     p.grid = (int)grid.x;

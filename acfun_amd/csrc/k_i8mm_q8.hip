@@ -11,12 +11,13 @@ using namespace i8k;
 template <int NST, int AM, int EPI, int OUT>
 bool launch_t(I8M& p, const I8Tile& t, hipStream_t s) {
     constexpr size_t lds = i8mm_lds(64, 64, NST);
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_i8mm<64, 64, NST, AM, EPI, OUT>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    }
+        return true;
+    }();
+    (void)attr;
     i8mm_prepare(p, 64, 64);
     dim3 grid((unsigned)i8mm_grid(p, t));
     p.grid = (int)grid.x;

@@ -646,23 +646,26 @@ bool launch_i8(const I8P& p, bool conv, bool va, hipStream_t s) {
 // ACFUN_I8_GRID=<workgroups per CU> the persistent grid (0: one tile per
 // workgroup); both exist for tile sweeps.
 I8Tile pick_i8mm_tile(int M, int N, int K) {
-    static int forced = -1;
-    static I8Tile ft{64, 64, 3, 0};
-    static int grid_cap = 3;
-    if (forced < 0) {
-        forced = 0;
+    // the overrides, read once per process (thread-safe initialization)
+    struct Env { bool forced = false; I8Tile ft{64, 64, 3, 0}; int grid_cap = 3; };
+    static const Env env = [] {
+        Env v;
         if (const char* e = getenv("ACFUN_I8_TILE")) {
             int a, b, c;
             if (sscanf(e, "%dx%dx%d", &a, &b, &c) == 3 && (a == 64 || a == 128) &&
                 (b == 64 || b == 128) && c >= 2 && c <= 4) {
-                ft = I8Tile{a, b, c, 0};
-                forced = 1;
+                v.ft = I8Tile{a, b, c, 0};
+                v.forced = true;
             }
         }
-        if (const char* e = getenv("ACFUN_I8_GRID")) grid_cap = atoi(e);
-    }
+        if (const char* e = getenv("ACFUN_I8_GRID")) v.grid_cap = atoi(e);
+        return v;
+    }();
+    const bool forced = env.forced;
+    const I8Tile ft = env.ft;
+    const int grid_cap = env.grid_cap;
     I8Tile t;
-    if (forced == 1) {
+    if (forced) {
         t = ft;
     } else {
         // Measured on configs 3a/3b and the ResNet-50 int8 model: 64 x 64 tiles

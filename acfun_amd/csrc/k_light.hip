@@ -1224,14 +1224,15 @@ bool gconv_pool_f32(const float* in, int N, int H, int W, int Cin, const float* 
     const size_t row_lds = ((size_t)(2 * stride + 3) * W * Cin + (size_t)Cout * 9 * Cin_p +
                             (size_t)3 * OW * Cout + Cout) * sizeof(float);
     if (row_lds <= 64 * 1024 && (long long)N * PH < (1ll << 31) && W * Cin % 4 == 0) {
-        static bool attr = false;
-        if (!attr) {
-            attr = true;
+        // set once per process, thread-safely, before any launch below
+        static const bool attr = [&] {
             (void)hipFuncSetAttribute((const void*)k_gconv3_pool_row<1>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
             (void)hipFuncSetAttribute((const void*)k_gconv3_pool_row<2>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-        }
+            return true;
+        }();
+        (void)attr;
         const dim3 grid((unsigned)(N * PH));
         if (Cin_p == 4)
             ACFUN_LAUNCH("k_gconv_pool", k_gconv3_pool_row<1>, grid, dim3(512), row_lds, s, in, H, W, Cin,

@@ -1050,12 +1050,13 @@ template <int TC>
 bool launch_wino23u(const float* in, const float* U, const float* bias, float* out, int N, int H,
                     int W, int Cin, int Cinp, int Cout, int tH, int tW, int act, hipStream_t s) {
     using CF = W23Cfg<TC>;
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_wino23u<TC>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, CF::LDS);
-    }
+        return true;
+    }();
+    (void)attr;
     const int rblocks = (tH + CF::R - 1) / CF::R;
     const int gx = (tW + TC - 1) / TC, gy = N * rblocks, gz = (Cout + 31) / 32;
     ACFUN_LAUNCH("k_wino23", k_wino23u<TC>, dim3((unsigned)(gx * gy * gz)), dim3(256), CF::LDS, s, in,
@@ -1425,16 +1426,17 @@ bool launch_wino23p(const float* in, const float* U, const float* bias, float* o
     const size_t lds = wino23p_lds<TC, NB>(Cout);
     const long long in_bytes = (long long)N * H * W * Cin * 4;
     if (Cinp / 8 < 4 || in_bytes >= (1ll << 31) || lds * 3 > 160 * 1024) return true;
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 0>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
         (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 1>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
         (void)hipFuncSetAttribute((const void*)k_wino23p<TC, NB, 2>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 / 3);
-    }
+        return true;
+    }();
+    (void)attr;
     const int rblocks = (tH + CF::R - 1) / CF::R;
     const long long gx = (tW + TC - 1) / TC, gy = (long long)N * rblocks, gz = (Cout + 31) / 32;
     const long long nblk = gx * gy;                    // R x TC tile blocks
@@ -1617,12 +1619,13 @@ bool run_wino23(const float* in, int N, int H, int W, int Cin, const float* w, c
         ConvShape gs{N, H, W, Cin, 3, 3, 1, 1, H, W};
         return conv_igemm_f32(gs, in, w, bias, Cout, out, act, s);
     }
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_wino23, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   160 * 1024);
-    }
+        return true;
+    }();
+    (void)attr;
     int rblocks = (tH + R - 1) / R;
     dim3 grid((unsigned)((tW + TC - 1) / TC), (unsigned)(N * rblocks), (unsigned)((Cout + 31) / 32));
     ACFUN_LAUNCH("k_wino23", k_wino23, grid, dim3(512), lds, s, in, Up, bias, out, N, H, W,

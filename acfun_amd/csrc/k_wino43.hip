@@ -486,13 +486,14 @@ bool run_wino43(const float* in, int N, int H, int W, int Cin, const float* w, c
     if (!Us.p) return false;
     if (!wino43_filter(w, Cin, Cout, Us.as<float>(), s)) return false;
     const size_t lds = wino43p_lds(Cout);
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
+    // set once per process, thread-safely, before any launch below
+    static const bool attr = [&] {
         (void)hipFuncSetAttribute((const void*)k_wino43p<0>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         (void)hipFuncSetAttribute((const void*)k_wino43p<1>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         (void)hipFuncSetAttribute((const void*)k_wino43p<2>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    }
+        return true;
+    }();
+    (void)attr;
     const long long slots = num_cus() / 8, need = (nunits + 7) / 8;
     const unsigned grid = (unsigned)(8 * (slots < need ? slots : need));
     const float* Up = Us.as<float>();
