@@ -1362,7 +1362,7 @@ __global__ __launch_bounds__(256, 3) void k_wino23p(
                 f4 S[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) S[i] = *(const f4*)&epi[(i * 32 + etile) * CF::SST + ecq];
-                // the round-1 writes must not overtake these reads
+                // the second pass's writes (cc == 1) must not overtake these reads
                 if (cc == 0) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
                 if (ec < Cout && cc < ecl) {
 #pragma unroll

@@ -356,9 +356,9 @@ __global__ __launch_bounds__(768, 1) void k_wino43p(
             float* const orow = out + (long long)(erl > 0 && ecl > 0 ? epx : 0) * Cout + ec;
 #pragma unroll
             for (int rd = 0; rd < 2; ++rd) {
-                // planes [row i][3] of 32 tiles x 32 channels: round 0 (output
+                // planes [row i][3] of 32 tiles x 32 channels: pass 0 (output
                 // columns 0, 2) A = M0+M1+M2, B = M1+M2 (half 0), B' = M3+M4
-                // (half 1); round 1 (columns 1, 3) C = M1-M2 (half 0),
+                // (half 1); pass 1 (columns 1, 3) C = M1-M2 (half 0),
                 // C' = M3-M4, D' = M5 (half 1).  Then column 0: S = A + B',
                 // 2: S = B + 4 B', 1: S = C + 2 C', 3: S = C + 8 C' + D'.
                 {
