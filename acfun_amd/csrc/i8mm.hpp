@@ -776,4 +776,31 @@ bool launch_i8mm_q8(I8M& p, const I8Tile& t, int am, int out, hipStream_t s);
 // The grid launch_i8mm_* uses for p and t (workgroups).
 int i8mm_grid(const I8M& p, const I8Tile& t);
 
+// Arguments of k_i8q1 (k_i8q1.hip): a float-input 1x1 / stride-1 / pad-0 int8
+// convolution (the GEMM route, RNE quantization) with the activation
+// quantization done while the A operand is staged, instead of a quantize pass
+// into an s8 tensor before k_i8mm.
+struct I8Q1 {
+    const float* x;       // fp32 NHWC activations [M][Cin]
+    const int8_t* Bt;     // prepared weights [N][ldb] (s8, zero past Cinp), N * ldb < 2^31
+    const int* Sw;        // their column sums
+    const float* ws;      // per-channel weight scales
+    const float* bias;    // nullable
+    const float* part;    // absmax partials of x (nparts of them, at most kAmaxParts)
+    int nparts;
+    float* scal;          // nullable: {inv_s, sa, zero flag, max}, written by workgroup 0
+    const float* res;     // nullable residual [M][ldr], added before the activation
+    float* Cf;            // output [M][ldc]
+    float* amax;          // nullable: per-workgroup max|stored value| at [workgroup]
+    int M, N, Cin, Cinp, ldb, ldc, ldr, act;
+    int grid;             // set by the launcher (workgroups = partials written to amax)
+};
+// Cinp (Cin rounded up to 16) up to this many channels: the block of 64
+// quantized rows stays in LDS.
+constexpr int kI8Q1MaxCinp = 512;
+bool launch_i8q1(I8Q1& a, hipStream_t s);
+// Whether a 1x1 conv with Cout output channels takes k_i8q1 (Cout <= 64
+// unless ACFUN_I8Q1 forces it on or off; read once).
+bool i8q1_route(int Cout);
+
 }  // namespace acfun

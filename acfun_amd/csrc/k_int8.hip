@@ -934,6 +934,35 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         const int mode = wino ? 2 : 0;
         // A shared tensor already quantized with this rule: no absmax, no quantizer.
         const bool reuse = shared && shared->ready && shared->mode == mode;
+        if (!reuse && !q8out && !wino && g.KH == 1 && g.KW == 1 && g.stride == 1 && g.pad == 0 &&
+            Cinp <= kI8Q1MaxCinp && i8q1_route(Cout)) {
+            // 1x1 / stride 1 / pad 0 into at most 64 channels: the absmax
+            // partials (unless the producer supplied them) with the weight
+            // preparation, then k_i8q1, which quantizes the rows as it stages
+            // them (a shared tensor is left to its other readers)
+            float* part = nullptr;
+            int nb = 0;
+            if (!amax_in) {
+                nb = (int)((inN / 4 + 1023) / 1024);
+                nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
+                part = (float*)ar.get((size_t)kParts * sizeof(float));
+                if (!part) return false;
+            }
+            if (nb + (prepared ? 0 : Cout) > 0) {
+                ACFUN_LAUNCH("k_absmax_prep", k_absmax_prep, dim3(nb + (prepared ? 0 : Cout)), dim3(256), 0, s,
+                             in, inN, part, nb, wq, 1, g.Cin, Cinp, Cout, nbt, ldb, nsw);
+                if (!check_launch("k_absmax_prep")) return false;
+            }
+            I8Q1 a{};
+            a.x = in; a.Bt = bt; a.Sw = sw; a.ws = ws; a.bias = bias;
+            a.part = amax_in ? amax_in : part;
+            a.nparts = amax_in ? kAmaxParts : nb;
+            a.scal = nullptr;
+            a.res = res; a.Cf = out; a.amax = amax_out;
+            a.M = (int)pix; a.N = Cout; a.Cin = g.Cin; a.Cinp = Cinp; a.ldb = ldb;
+            a.ldc = Cout; a.ldr = Cout; a.act = act;
+            return launch_i8q1(a, s);
+        }
         float* scal = reuse || shared ? nullptr : (float*)ar.get((size_t)(8 + kParts) * sizeof(float));
         int8_t* q = reuse || shared ? nullptr : (int8_t*)ar.get((size_t)pix * Cinp);
         float* part = nullptr;
