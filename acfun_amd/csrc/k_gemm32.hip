@@ -603,6 +603,13 @@ __global__ __launch_bounds__(256) void k_gemm32p(const float* __restrict__ A,
                 for (int kq = 0; kq < 4; ++kq) bq[kq] = n + kq < N ? bias[n + kq] : 0.f;
             }
         }
+        const bool full = m0 + BM <= M && n0 + BN <= N;
+        f4g rv[4];
+        if (res && vec && full) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                rv[i] = *(const f4g*)(res + (long long)(m0 + (tid >> 4) + 16 * i) * ldr + n);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rr = (tid >> 4) + 16 * i, m = m0 + rr;
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(256) void k_gemm32p(const float* __restrict__ A,
             float* dst = C + (long long)m * ldc + n;
             if (vec && n + 4 <= N) {
                 if (bias) v = v + bq;
-                if (res) v = v + *(const f4g*)(res + (long long)m * ldr + n);
+                if (res) v = v + (full ? rv[i] : *(const f4g*)(res + (long long)m * ldr + n));
 #pragma unroll
                 for (int kq = 0; kq < 4; ++kq) v[kq] = act_apply(v[kq], act);
                 // s_nop: a VALU write to the data registers of a store of more
