@@ -484,6 +484,7 @@ bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const f
     if (g.KH == 1 && g.KW == 1 && g.stride == 1 && g.pad == 0)
         return gemm_f32(M, Cout, K, in, g.Cin, w, Cout, out, Cout, bias, act, s);
     if (conv32_ok(g, Cout, in, w)) return conv32_f32(g, in, w, bias, Cout, out, act, s);
+    if (conv_smallc_ok(g, Cout, in)) return conv_smallc_f32(g, in, w, bias, Cout, out, act, s);
     GemmP p{};
     p.A = in; p.B = w; p.C = out; p.bias = bias;
     p.M = M; p.N = Cout; p.K = K; p.lda = K; p.ldb = Cout; p.ldc = Cout; p.act = act;

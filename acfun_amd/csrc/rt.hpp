@@ -197,6 +197,12 @@ bool gemm_f32(int M, int N, int K, const float* A, int lda, const float* B, int 
               int ldc, const float* bias, int act, hipStream_t s);
 bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const float* bias,
                     int Cout, float* out, int act, hipStream_t s);
+// Convolutions with few input channels (k_stem.hip): the instantiated (KH, KW,
+// Cin) shapes whose input window fits the kernel's LDS, with W * Cin a multiple
+// of 4 and a 16-byte aligned input.
+bool conv_smallc_ok(const ConvShape& g, int Cout, const float* in);
+bool conv_smallc_f32(const ConvShape& g, const float* in, const float* w, const float* bias, int Cout, float* out,
+                     int act, hipStream_t s);
 // Batched GEMM (batch = gridDim.z) with fixed strides, no epilogue.
 bool gemm_f32_batched(int batch, int M, int N, int K, const float* A, long long sA, int lda,
                       const float* B, long long sB, int ldb, float* C, long long sC, int ldc,
