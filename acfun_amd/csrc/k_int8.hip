@@ -934,6 +934,26 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         const int mode = wino ? 2 : 0;
         // A shared tensor already quantized with this rule: no absmax, no quantizer.
         const bool reuse = shared && shared->ready && shared->mode == mode;
+        if (!reuse && !q8out && !wino && conv_smallc_ok(g, Cout, in)) {
+            // a stem (7x7 or 3x3 on 3 channels): the absmax partials (unless the
+            // producer supplied them), the input quantized once as dense s8, then
+            // k_i8stem with the [K][Cout] weights as they are
+            float* part = nullptr;
+            int nb = 0;
+            if (!amax_in) {
+                nb = (int)((inN / 4 + 1023) / 1024);
+                nb = nb < 1 ? 1 : (nb > kParts ? kParts : nb);
+                part = (float*)ar.get((size_t)kParts * sizeof(float));
+                if (!part) return false;
+                ACFUN_LAUNCH("k_absmax_prep", k_absmax_prep, dim3(nb), dim3(256), 0, s, in, inN, part, nb, wq,
+                             g.KH * g.KW, g.Cin, Cinp, Cout, nbt, ldb, nsw);
+                if (!check_launch("k_absmax_prep")) return false;
+            }
+            int8_t* q8 = (int8_t*)ar.get((size_t)inN);
+            if (!q8) return false;
+            return conv_i8stem(g, in, wq, ws, bias, Cout, out, act, amax_in ? amax_in : part,
+                               amax_in ? kAmaxParts : nb, amax_out, nullptr, q8, s);
+        }
         if (!reuse && !q8out && !wino && g.KH == 1 && g.KW == 1 && g.stride == 1 && g.pad == 0 &&
             Cinp <= kI8Q1MaxCinp && i8q1_route(Cout)) {
             // 1x1 / stride 1 / pad 0 into at most 64 channels: the absmax

@@ -203,6 +203,14 @@ bool conv_igemm_f32(const ConvShape& g, const float* in, const float* w, const f
 bool conv_smallc_ok(const ConvShape& g, int Cout, const float* in);
 bool conv_smallc_f32(const ConvShape& g, const float* in, const float* w, const float* bias, int Cout, float* out,
                      int act, hipStream_t s);
+// The int8 form (acfun_conv2d_int8's GEMM route, RNE quantization) for the same
+// shapes: wq [K][Cout] s8 as the API takes it, the activation scale from nparts
+// absmax partials, q8 (16-byte aligned, N*H*W*Cin bytes) a temporary for the
+// quantized input; amax (nullable) receives one output-maximum partial per
+// workgroup, *grid of them (at most kI8AmaxParts).
+bool conv_i8stem(const ConvShape& g, const float* in, const int8_t* wq, const float* ws, const float* bias,
+                 int Cout, float* out, int act, const float* part, int nparts, float* amax, int* grid,
+                 int8_t* q8, hipStream_t s);
 // Batched GEMM (batch = gridDim.z) with fixed strides, no epilogue.
 bool gemm_f32_batched(int batch, int M, int N, int K, const float* A, long long sA, int lda,
                       const float* B, long long sB, int ldb, float* C, long long sC, int ldc,

@@ -2,7 +2,9 @@
 of a network's stem (the reference's im2col + GEMM route, src/layers.cpp:178-194,
 for 7x7 and 3x3 kernels on 3 channels), through the C ABI against the f64 direct
 convolution (oracle.conv2d_f64) within the fp32 GEMM tolerance 1e-4 (relative
-to the output's largest magnitude).  Each case also checks, through the
+to the output's largest magnitude); and of its int8 form k_i8stem
+(acfun_conv2d_int8, src/conv_int8.cpp:63-148), bit-exact against
+oracle.conv2d_int8.  Each case also checks, through the
 library's kernel timing, that k_conv_smallc ran -- or, for rows of W*Cin not a
 multiple of 4 floats and inputs not 16-byte aligned (which its 16-byte window
 DMA needs), that the general implicit GEMM did."""
@@ -12,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.helpers import P, rel_err
+from tests.helpers import P, assert_bitexact, int8_conv_inputs, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -114,3 +116,49 @@ def test_stem_unaligned_input_takes_general_kernel(gpu, rng):
         assert rc == 0
         assert (n.value > 0) == (off == 0)
         assert rel_err(y.cpu().numpy(), want) < GEMM_TOL
+
+
+def _conv_i8(gpu, x, wq, ws, b, KH, Cout, s, p, act):
+    N, H, W, Cin = x.shape
+    OH, OW = oracle.out_hw(H, W, KH, KH, s, p)
+    got = np.full((N, OH, OW, Cout), np.nan, np.float32)
+    gpu.acfun_prof_enable(1)
+    try:
+        gpu.acfun_conv2d_int8(P(x), N, H, W, Cin, P(wq), P(ws), P(b), KH, KH, Cout, s, p, np.float32(0.5),
+                              P(got), act)
+        n = C.c_int(0)
+        gpu.acfun_prof_kernel_ms(b"k_i8stem", C.byref(n))
+    finally:
+        gpu.acfun_prof_enable(0)
+    return got, n.value
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_stem_int8_exact(gpu, rng, case, act):
+    N, H, W, K, Cout, s, p = case
+    x, wq, ws, b = int8_conv_inputs(rng, N, H, W, 3, K, K, Cout, bias=(act == 1))
+    got, ran = _conv_i8(gpu, x, wq, ws, b, K, Cout, s, p, act)
+    assert (ran > 0) == (W % 4 == 0)
+    assert_bitexact(got, oracle.conv2d_int8(x, wq, ws, b, K, K, Cout, s, p, act), f"int8 stem {case}")
+
+
+def test_stem_int8_special_inputs(gpu, rng):
+    """Normal-distributed activations with NaNs (the x86 conversion's rule: s8
+    -128) and the maximum magnitude negated; then an all-zero input, which
+    gives 0 without the bias (src/conv_int8.cpp:78)."""
+    N, H, W, K, Cout, s, p = 2, 40, 44, 7, 64, 2, 3
+    x = rng.standard_normal((N, H, W, 3)).astype(np.float32)
+    flat = x.reshape(-1)
+    flat[rng.choice(flat.size, 9, replace=False)] = np.nan
+    flat[5] = -flat[np.nanargmax(np.abs(flat))]
+    wq = rng.integers(-128, 128, size=(K * K * 3, Cout)).astype(np.int8)
+    ws = rng.uniform(0.005, 0.05, Cout).astype(np.float32)
+    b = (rng.standard_normal(Cout) * 0.1).astype(np.float32)
+    got, ran = _conv_i8(gpu, x, wq, ws, b, K, Cout, s, p, 1)
+    assert ran > 0
+    assert_bitexact(got, oracle.conv2d_int8(x, wq, ws, b, K, K, Cout, s, p, 1), "int8 stem floats")
+    z = np.zeros((1, 16, 16, 3), np.float32)
+    got, ran = _conv_i8(gpu, z, wq, ws, np.full(Cout, 3.0, np.float32), K, Cout, s, p, 1)
+    assert ran > 0
+    assert np.all(got == 0.0) and not np.any(np.signbit(got))
