@@ -19,6 +19,12 @@ sample of the same workload, 3 warmups then the median (src/benchmark.cpp:98-111
 Configs 3 and 4 also report "ms_cold": the step cycling over copies of its
 operands whose total exceeds the 256 MB MALL.
 
+Every timed run (the W warmup steps, then exactly K timed steps) follows a
+clock ramp: the step repeated, untimed, for --ramp-ms of wall time (100 ms),
+because an idle MI355X takes 10-50 ms of sustained load to raise its shader
+clock.  The headline's step time without the ramp is reported beside it as
+ms_per_step_without_ramp.
+
 --profile CFG runs only CFG's step (5 times) and then three plain 256 MiB
 device copies, for rocprofv3 --pmc passes whose counters the copies scale.
 """
@@ -37,6 +43,7 @@ PEAK_FP32 = 157.3e12     # dense fp32 MFMA, FLOP/s
 PEAK_INT8 = 5.0e15       # dense int8 MFMA, OP/s
 PEAK_BF16 = 2.5e15       # dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12        # B/s
+CFG_REPS = 5            # timed runs per config step (median)
 CPU_BUDGET_S = 5.0       # timed CPU work per configuration (after the warmups)
 
 
@@ -45,6 +52,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ramp-ms", type=float, default=100.0,
+                    help="untimed steps for this long (wall time) before each timed run's warmup "
+                         "steps, so that the GPU's clock has left its idle state (0: none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
     ap.add_argument("--profile", metavar="CFG", default=None,
@@ -65,24 +75,48 @@ def parse():
 
 
 class Timer:
-    """HIP events on the stream the library launches on."""
+    """HIP events on the stream the library launches on.  Each run first
+    repeats its step, untimed, for ramp_ms of wall time: an idle MI355X
+    needs about 10-50 ms of sustained work before its shader clock leaves
+    the idle state (config 2a's kernel: 46.7 us per launch in the first
+    milliseconds, 39.6 us after 50 ms, 46.7 us again after 1 s idle), so
+    without the ramp a few-millisecond measurement times the clock's rise,
+    not the kernel."""
 
-    def __init__(self, torch, stream):
-        self.torch, self.stream = torch, stream
+    def __init__(self, torch, stream, ramp_ms=100.0):
+        self.torch, self.stream, self.ramp_ms = torch, stream, ramp_ms
 
-    def run(self, fn, steps, warmup):
+    def ramp(self, fn):
+        if self.ramp_ms <= 0:
+            return
+        t0, n = time.perf_counter(), 0
+        while n < 100000:
+            fn()
+            n += 1
+            if n % 16 == 0 and (time.perf_counter() - t0) * 1e3 >= self.ramp_ms:
+                break
+        self.torch.cuda.synchronize()
+
+    def run(self, fn, steps, warmup, reps=1):
+        """ms per step over `steps` timed steps; with reps > 1 the median of
+        reps such runs back to back (the configs' short steps, where one host
+        stall moves a single run's mean)."""
         torch = self.torch
+        self.ramp(fn)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(self.stream)
-        for _ in range(steps):
-            fn()
-        e1.record(self.stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps   # ms per step
+        ts = []
+        for _ in range(reps):
+            e0.record(self.stream)
+            for _ in range(steps):
+                fn()
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) / steps)   # ms per step
+        return sorted(ts)[len(ts) // 2]
 
     def kernel_ms(self, lib, fn, steps, kernels):
         """Mean duration (ms) of library kernels over `steps` more steps: the
@@ -624,7 +658,7 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     torch.cuda.set_stream(stream)
     sp = stream.cuda_stream
-    T = Timer(torch, stream)
+    T = Timer(torch, stream, args.ramp_ms)
     rng = np.random.default_rng(12345 + 1)
 
     def check(rc):
@@ -642,7 +676,7 @@ def main():
         m, path, xin, out = load_cfg5(lib, torch, dev, rng, cfg, int8)
         run = lambda: check_infer(lib, m, xin, out, sp)
         run()                                          # makes the Winograd filter transforms
-        torch.cuda.synchronize()
+        T.ramp(run)
         rows, untagged = model_layer_profile(lib, run)
         torch.cuda.synchronize()
         lib.acfun_model_destroy(m)
@@ -663,6 +697,7 @@ def main():
     if args.profile:
         if args.profile not in cfg or "step" not in cfg[args.profile]:
             raise SystemExit(f"bench.py: no configuration {args.profile!r}")
+        T.ramp(cfg[args.profile]["step"])
         for _ in range(5):
             cfg[args.profile]["step"]()
         src = torch.empty(64 << 20, device=dev)        # 256 MiB
@@ -673,6 +708,11 @@ def main():
         return
 
     # ---------------------------------------------------------------- headline
+    # first the same steps with no clock ramp (reported beside the headline),
+    # then with it
+    ramp_ms, T.ramp_ms = T.ramp_ms, 0.0
+    ms_no_ramp = T.run(cfg["cfg2a"]["step"], args.steps, args.warmup)
+    T.ramp_ms = ramp_ms
     ms = T.run(cfg["cfg2a"]["step"], args.steps, args.warmup)
     k = T.kernel_ms(lib, cfg["cfg2a"]["step"], args.steps, ["k_wino23", "k_wino_filter_t"])
     direct_flop = 7.398752256e9
@@ -685,6 +725,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "clock_ramp_ms": args.ramp_ms,
+        "ms_per_step_without_ramp": round(ms_no_ramp, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -725,7 +767,7 @@ def main():
                                                  "time; never the headline value"}
 
         # 1: GEMM 1024^3
-        t = T.run(cfg["cfg1"]["step"], steps, args.warmup)
+        t = T.run(cfg["cfg1"]["step"], steps, args.warmup, CFG_REPS)
         k = T.kernel_ms(lib, cfg["cfg1"]["step"], steps, ["k_gemm32"])
         flop = 2.0 * 1024 ** 3
         configs["cfg1_gemm_1024"] = {
@@ -734,7 +776,7 @@ def main():
                                  "2*1024^3 = 2.147 GFLOP per launch", "k_gemm32_cfg1")}
 
         # acfun_gemm_bf16 1024^3 (not a BASELINE config)
-        t = T.run(cfg["bf16"]["step"], steps, args.warmup)
+        t = T.run(cfg["bf16"]["step"], steps, args.warmup, CFG_REPS)
         k = T.kernel_ms(lib, cfg["bf16"]["step"], steps, ["k_bf16mm"])
         configs["gemm_bf16_1024"] = {"ms": round(t, 5), "TFLOPS": round(flop / (t * 1e-3) / 1e12, 3),
                                      "frac_bf16_peak_kernel": round(flop / (k["k_bf16mm"] * 1e-3) / PEAK_BF16, 4)
@@ -742,7 +784,7 @@ def main():
                                      "kernel_ms": k, "note": "step = one bf16 packing launch (A and B) + k_bf16mm"}
 
         # 2(b): F(4,3) route; the fraction counts the F(4,3) work the route needs
-        t = T.run(cfg["cfg2b"]["step"], steps, args.warmup)
+        t = T.run(cfg["cfg2b"]["step"], steps, args.warmup, CFG_REPS)
         k = T.kernel_ms(lib, cfg["cfg2b"]["step"], steps, ["k_wino43", "k_wino23", "k_wino_fused",
                                                              "k_wino_filter_t"])
         f43 = 1.849688064e9
@@ -759,18 +801,18 @@ def main():
         # 3(a) / 3(b)
         for name, key in (("cfg3a", "cfg3a_int8_1x1"), ("cfg3b", "cfg3b_int8_3x3")):
             c = cfg[name]
-            t = T.run(c["step"], steps, args.warmup)
+            t = T.run(c["step"], steps, args.warmup, CFG_REPS)
             k = T.kernel_ms(lib, c["step"], steps, ["k_i8mm"])
             fn, xt, yt = c["rot"]
             xs, ys = rotation_sets(xt, yt)
-            tc = T.run(rotating(fn, xs, ys), steps, args.warmup)
+            tc = T.run(rotating(fn, xs, ys), steps, args.warmup, CFG_REPS)
             del xs, ys
-            tq = T.run(cfg[name + "_q"]["step"], steps, args.warmup)
+            tq = T.run(cfg[name + "_q"]["step"], steps, args.warmup, CFG_REPS)
             kq = T.kernel_ms(lib, cfg[name + "_q"]["step"], steps,
                              ["k_i8mm_amax", "k_i8mm_q8", "k_i8mm", "k_requant_s8"])
             fn, xt, yt = cfg[name + "_q"]["rot"]
             xs, ys = rotation_sets(xt, yt)
-            tqc = T.run(rotating(fn, xs, ys), steps, args.warmup)
+            tqc = T.run(rotating(fn, xs, ys), steps, args.warmup, CFG_REPS)
             del xs, ys
             ops = c["ops"]
             configs[key] = {
@@ -799,11 +841,11 @@ def main():
 
         # 4(a): fused depthwise + BN + ReLU + MaxPool
         c = cfg["cfg4a"]
-        t = T.run(c["step"], steps, args.warmup)
+        t = T.run(c["step"], steps, args.warmup, CFG_REPS)
         k = T.kernel_ms(lib, c["step"], steps, ["k_dwconv_pool"])
         fn, xt, zt = c["rot"]
         xs, zs = rotation_sets(xt, zt)
-        tc = T.run(rotating(fn, xs, zs), steps, args.warmup)
+        tc = T.run(rotating(fn, xs, zs), steps, args.warmup, CFG_REPS)
         del xs, zs
         configs["cfg4a_dw_bn_relu_pool"] = {
             "ms": round(t, 5), "ms_cold": round(tc, 5),
@@ -815,20 +857,20 @@ def main():
         # 4(b): grouped conv + ReLU + MaxPool fused; the two-launch path beside
         # it; and the fused step replayed from a HIP graph (launch cost removed)
         c = cfg["cfg4b"]
-        t = T.run(c["step"], steps, args.warmup)
+        t = T.run(c["step"], steps, args.warmup, CFG_REPS)
         k = T.kernel_ms(lib, c["step"], steps, ["k_gconv_pool"])
         fn, xt, zt = c["rot"]
         xs, zs = rotation_sets(xt, zt)
-        tc = T.run(rotating(fn, xs, zs), steps, args.warmup)
+        tc = T.run(rotating(fn, xs, zs), steps, args.warmup, CFG_REPS)
         del xs, zs
-        t2 = T.run(c["two"], steps, args.warmup)
+        t2 = T.run(c["two"], steps, args.warmup, CFG_REPS)
         per_graph = 10
         graph = torch.cuda.CUDAGraph()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
             for _ in range(per_graph):
                 c["step"]()
-        tg = T.run(graph.replay, max(2, steps // 2), 2) / per_graph
+        tg = T.run(graph.replay, max(2, steps // 2), 2, CFG_REPS) / per_graph
         configs["cfg4b_grouped_pool"] = {
             "ms": round(t, 5), "ms_cold": round(tc, 5), "ms_graph_replay": round(tg, 5),
             "ms_two_launches": round(t2, 5),
@@ -844,7 +886,7 @@ def main():
                 configs[f"cfg5_resnet50_b64_{tag}"] = {"error": capi.last_error()}
                 continue
             s6 = lambda m=m, xin=xin, out=out: check_infer(lib, m, xin, out, sp)
-            t = T.run(s6, max(3, steps // 4), 2)
+            t = T.run(s6, max(3, steps // 4), 2, 3)
             rows, _ = model_layer_profile(lib, s6)
             gfl = acfun0.resnet50_flops()
             configs[f"cfg5_resnet50_b64_{tag}"] = {
