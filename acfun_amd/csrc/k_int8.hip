@@ -934,7 +934,7 @@ bool conv2d_int8_run(const float* in, const ConvShape& g, const int8_t* wq, cons
         const int mode = wino ? 2 : 0;
         // A shared tensor already quantized with this rule: no absmax, no quantizer.
         const bool reuse = shared && shared->ready && shared->mode == mode;
-        if (!reuse && !q8out && !wino && conv_smallc_ok(g, Cout, in)) {
+        if (!reuse && !q8out && !wino && (Cout + 63) / 64 <= kI8AmaxParts && conv_smallc_ok(g, Cout, in)) {
             // a stem (7x7 or 3x3 on 3 channels): the absmax partials (unless the
             // producer supplied them), the input quantized once as dense s8, then
             // k_i8stem with the [K][Cout] weights as they are

@@ -597,7 +597,10 @@ bool conv_smallc_f32(const ConvShape& g, const float* in, const float* w, const 
 bool conv_i8stem(const ConvShape& g, const float* in, const int8_t* wq, const float* ws, const float* bias,
                  int Cout, float* out, int act, const float* part, int nparts, float* amax, int* grid,
                  int8_t* q8, hipStream_t s) {
-    if (!conv_smallc_ok(g, Cout, in) || nparts < 0 || nparts > kI8AmaxParts || (((uintptr_t)q8) & 15u) != 0) {
+    // (one output-maximum partial per workgroup: at most kI8AmaxParts, and at
+    // least one workgroup per 64-channel tile)
+    if (!conv_smallc_ok(g, Cout, in) || nparts < 0 || nparts > kI8AmaxParts || (Cout + 63) / 64 > kI8AmaxParts ||
+        (((uintptr_t)q8) & 15u) != 0) {
         set_error("conv_i8stem: unsupported shape");
         return false;
     }
