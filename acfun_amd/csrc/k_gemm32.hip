@@ -27,6 +27,8 @@
 // KS > 1: KS groups of four waves in one workgroup split K by chunk
 // (group kg takes chunks kg, kg + KS, ...), each with its own stages; the
 // groups' accumulators are summed through LDS at the end, group 1's first.
+// With two groups each group finalizes and stores half of the tile, so all
+// eight waves share the merge and the stores.
 #include "rt.hpp"
 
 #include <cstdlib>
@@ -320,7 +322,38 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(al[i][u], bl[j][u], acc[i][j], 0, 0, 0);
     }
 
-    if (KS > 1) {                  // groups 1..KS-1's sums through LDS into group 0's
+    // Each output is group 0's sum plus the other groups' partials, in group
+    // order.  Two groups: each finalizes half of every block's registers
+    // (group 0 e < 8, group 1 e >= 8), adding the other group's partial read
+    // back from LDS (g0 + g1 is the same float sum in either order), and
+    // stores that half.  More groups: their partials through LDS into group 0.
+    int e_lo = 0;                                       // this wave's first register to store
+    if (KS == 2) {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stages no longer read
+        float* const red = sm + wl * (FM * FN * 16 * 64) + lane;   // slot e of block b: (16 b + e) * 64
+        auto hand = [&](auto kgc) {
+            constexpr int G = decltype(kgc)::value;
+            constexpr int GIVE = G == 0 ? 8 : 0, KEEP = 8 - GIVE;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        red[((i * FN + j) * 16 + GIVE + e) * 64] = acc[i][j][GIVE + e];
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        acc[i][j][KEEP + e] += red[((i * FN + j) * 16 + KEEP + e) * 64];
+        };
+        if (kg == 0) hand(std::integral_constant<int, 0>{});
+        else hand(std::integral_constant<int, 1>{});
+        e_lo = kg == 0 ? 0 : 8;
+    } else if (KS > 2) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // stages no longer read
         constexpr int PART = 4 * FM * FN * 16 * 64;     // floats of one group's partial tile
         float* const red = sm + wl * (FM * FN * 16 * 64) + lane;
@@ -346,33 +379,40 @@ __global__ __launch_bounds__(256 * KS) void k_gemm32(const float* __restrict__ A
 
     // ---- epilogue: lane l, register e of block (i, j) <->
     //      row m0 + BM/2*wm + 32i + 8*(e/4) + 4*(l/32) + e%4, column n0 + BN/2*wn + 32j + l%32
+    //      (registers E0 .. E1-1 of this wave)
+    auto store = [&](auto e0c, auto e1c) {
+        constexpr int E0 = decltype(e0c)::value, E1 = decltype(e1c)::value;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int n = n0 + (BN / 2) * wn + 32 * j + r;
-        if (n >= N) continue;
+        for (int j = 0; j < FN; ++j) {
+            const int n = n0 + (BN / 2) * wn + 32 * j + r;
+            if (n >= N) continue;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            float rv[16];
-            if (res && !PRE) {                            // all 16 loads in flight at once
+            for (int i = 0; i < FM; ++i) {
+                float rv[16];
+                if (res && !PRE) {                        // all the loads in flight at once
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-                    rv[e] = m < M ? res[(long long)m * ldr + n] : 0.f;
+                    for (int e = E0; e < E1; ++e) {
+                        const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                        rv[e] = m < M ? res[(long long)m * ldr + n] : 0.f;
+                    }
                 }
-            }
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (m < M) {
-                    float v = acc[i][j][e];
-                    if (bias) v = v + bn[j];
-                    if (res) v = v + (PRE ? rv0[e] : rv[e]);   // fused residual Add
-                    v = act_apply(v, act);
-                    C[(long long)m * ldc + n] = v;
+                for (int e = E0; e < E1; ++e) {
+                    const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (m < M) {
+                        float v = acc[i][j][e];
+                        if (bias) v = v + bn[j];
+                        if (res) v = v + (PRE ? rv0[e] : rv[e]);   // fused residual Add
+                        v = act_apply(v, act);
+                        C[(long long)m * ldc + n] = v;
+                    }
                 }
             }
         }
-    }
+    };
+    if (KS != 2) store(std::integral_constant<int, 0>{}, std::integral_constant<int, 16>{});
+    else if (e_lo == 0) store(std::integral_constant<int, 0>{}, std::integral_constant<int, 8>{});
+    else store(std::integral_constant<int, 8>{}, std::integral_constant<int, 16>{});
 }
 
 // ---------------------------------------------------------------- k_gemm32p
