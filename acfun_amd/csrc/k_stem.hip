@@ -260,12 +260,12 @@ __global__ __launch_bounds__(256, 3) void k_conv_smallc(const float* __restrict_
             for (int e = 0; e < 16; ++e) vs[e] = act_apply(acc[e] + bcol, c.act);
             float* const ol = out + (obase + wm * 32 + 4 * h) * c.Cout + col;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) ol[(long long)(8 * (e >> 2) + (e & 3)) * c.Cout] = vs[e];
+            for (int e = 0; e < 16; ++e) __builtin_nontemporal_store(vs[e], &ol[(long long)(8 * (e >> 2) + (e & 3)) * c.Cout]);
         } else if (col < c.Cout) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int p = wm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (p < npx) out[(obase + p) * c.Cout + col] = act_apply(acc[e] + bcol, c.act);
+                if (p < npx) __builtin_nontemporal_store(act_apply(acc[e] + bcol, c.act), &out[(obase + p) * c.Cout + col]);
             }
         }
         prev_full = full;
@@ -491,12 +491,12 @@ __global__ __launch_bounds__(256, 3) void k_i8stem(const int8_t* __restrict__ q8
             for (int e = 0; e < 16; ++e) vs[e] = value(e);
             float* const ol = out + (obase + wm * 32 + 4 * h) * c.Cout + col;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) ol[(long long)(8 * (e >> 2) + (e & 3)) * c.Cout] = vs[e];
+            for (int e = 0; e < 16; ++e) __builtin_nontemporal_store(vs[e], &ol[(long long)(8 * (e >> 2) + (e & 3)) * c.Cout]);
         } else if (col < c.Cout) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int p = wm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (p < npx) out[(obase + p) * c.Cout + col] = value(e);
+                if (p < npx) __builtin_nontemporal_store(value(e), &out[(obase + p) * c.Cout + col]);
             }
         }
         full2 = full1;
