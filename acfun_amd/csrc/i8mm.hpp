@@ -607,7 +607,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                             }
                             // s_nop: a VALU write to the data registers of a store of
                             // more than 8 bytes needs a wait state after it
-                            asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(dst), "v"(v)
+                            asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v)
                                          : "memory");
                         } else if (!FAST && m < p.M) {
 #pragma unroll
@@ -620,7 +620,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                                     const float av = fabsf(w);
                                     amx = av > amx ? av : amx;
                                 }
-                                asm volatile("global_store_dword %0, %1, off nt" ::"v"(dst + k), "v"(w)
+                                asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst + k), "v"(w)
                                              : "memory");
                             }
                         }
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                     }
                     const i4 pk = {(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
                     int8_t* dq = p.Cq + (long long)m * p.ldq + n;
-                    asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(dq), "v"(pk)
+                    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dq), "v"(pk)
                                  : "memory");
                 }
             }
@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) void k_i8mm(I8M p) {
                             v = act_select(v, relu1, relu2);
                             if (FULL || (m < p.M && n < p.N)) {
                                 float* dst = cl + (32 * i + 8 * (e >> 2) + (e & 3)) * (long long)p.ldc + 32 * j;
-                                asm volatile("global_store_dword %0, %1, off nt" ::"v"(dst), "v"(v) : "memory");
+                                asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst), "v"(v) : "memory");
                                 const float av = fabsf(v);
                                 amx = av > amx ? av : amx;             // NaN never wins
                             }

@@ -665,7 +665,7 @@ __global__ __launch_bounds__(256) void k_gemm32p(const float* __restrict__ A,
                 for (int kq = 0; kq < 4; ++kq) v[kq] = act_apply(v[kq], act);
                 // s_nop: a VALU write to the data registers of a store of more
                 // than 8 bytes needs a wait state after it
-                asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
+                asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v) : "memory");
             } else {
 #pragma unroll
                 for (int kq = 0; kq < 4; ++kq) {
@@ -674,7 +674,7 @@ __global__ __launch_bounds__(256) void k_gemm32p(const float* __restrict__ A,
                     if (bias) w = w + bq[kq];
                     if (res) w = w + res[(long long)m * ldr + n + kq];
                     w = act_apply(w, act);
-                    asm volatile("global_store_dword %0, %1, off nt" ::"v"(dst + kq), "v"(w) : "memory");
+                    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst + kq), "v"(w) : "memory");
                 }
             }
         }

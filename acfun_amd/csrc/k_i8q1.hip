@@ -378,7 +378,7 @@ __global__ __launch_bounds__(256, OCC) void k_i8q1(I8Q1 p, Q1L l) {
                         }
                         // s_nop: a VALU write to the data registers of a store of
                         // more than 8 bytes needs a wait state after it
-                        asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(dst), "v"(v)
+                        asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v)
                                      : "memory");
                     } else if (!FAST && m < p.M) {
 #pragma unroll
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256, OCC) void k_i8q1(I8Q1 p, Q1L l) {
                                 const float av = fabsf(w);
                                 amx = av > amx ? av : amx;
                             }
-                            asm volatile("global_store_dword %0, %1, off nt" ::"v"(dst + k), "v"(w) : "memory");
+                            asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst + k), "v"(w) : "memory");
                         }
                     }
                 }

@@ -420,13 +420,13 @@ __global__ __launch_bounds__(768, 1) void k_wino43p(
                                 // store of more than 8 bytes needs a wait state
                                 // after it, which the compiler cannot insert after
                                 // inline asm
-                                asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 1" ::"v"(dst), "v"(v)
+                                asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(dst), "v"(v)
                                              : "memory");
                             } else {
 #pragma unroll
                                 for (int e = 0; e < 4; ++e)
                                     if (ec + e < Cout)
-                                        asm volatile("global_store_dword %0, %1, off nt" ::"v"(dst + e), "v"(v[e])
+                                        asm volatile("global_store_dword %0, %1, off sc1" ::"v"(dst + e), "v"(v[e])
                                                      : "memory");
                             }
                         }
