@@ -299,6 +299,43 @@ def test_resnet50_b64_batch_permutation(gpu, rng, int8, tmp_path):
         assert rel_err(b, a) < 1e-6, rel_err(b, a)
 
 
+@pytest.mark.parametrize("int8", [True, False])
+@pytest.mark.parametrize("head", [False, True])
+def test_resnet50_b64_tiles_equal_batch8(gpu, rng, int8, head, tmp_path):
+    """Config 5 at the bench's batch of 64, tied to the oracle-checked batch of
+    8: the 64 images are 8 copies of 8 images, so every batch-wide int8
+    activation scale (a maximum over the batch) equals the batch-8 run's, and
+    each block of 8 outputs must reproduce the batch-8 outputs -- bit for bit
+    for the int8 body, within 1e-5 where fp32 kernels may choose other tiles at
+    the larger batch.  test_resnet50_headless_batch8 and
+    test_resnet50_int8_head_batch3 check the small batches against the oracle."""
+    import torch
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5), head=head)
+    path = _write(tmp_path, "r50t.acfun", inC, H, W, recs, 2)
+    x8 = torch.rand((8, H, W, inC), device="cuda", generator=torch.Generator(device="cuda").manual_seed(13))
+    x64 = x8.repeat(8, 1, 1, 1).contiguous()
+    F = 1000 if head else 7 * 7 * 2048
+    y8 = torch.full((8, F), float("nan"), device="cuda")
+    y64 = torch.full((64, F), float("nan"), device="cuda")
+    m = _load(gpu, path, 1 if int8 else 0)
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        print("ResNet-50 batch 8 and batch 64 (8 copies), int8", int8, "head", head, flush=True)
+        assert gpu.acfun_dev_model_infer_batch(m, 8, x8.data_ptr(), y8.data_ptr(), s) == F, capi.last_error()
+        assert gpu.acfun_dev_model_infer_batch(m, 64, x64.data_ptr(), y64.data_ptr(), s) == F, capi.last_error()
+        torch.cuda.synchronize()
+    finally:
+        gpu.acfun_model_destroy(m)
+    a = y8.cpu().numpy()
+    assert not np.isnan(a).any() and np.count_nonzero(a) > a.size // 4
+    b = y64.cpu().numpy().reshape(8, 8, F)
+    for k in range(8):
+        if int8 and not head:
+            assert_bitexact(b[k], a, f"int8 ResNet-50 body, batch 64, copy {k}")
+        else:
+            assert rel_err(b[k], a) < 1e-5, (k, rel_err(b[k], a))
+
+
 def test_int8_model_uses_the_s8_chain(gpu, rng, tmp_path):
     """An int8 model passes a tensor whose only reader is another int8 conv as
     s8 with its device scale: its producer requantizes it (k_requant_s8) and the
