@@ -565,10 +565,11 @@ __global__ __launch_bounds__(256) void k_dwconv3_pool_rs(
     const int blk = (int)(blockIdx.x & 7u) * per + (int)(blockIdx.x >> 3);
     const int idx = blk * 256 + (int)threadIdx.x;
     if (idx >= items) return;
-    const int q = idx % C4;
-    int t = idx / C4;
-    const int pw = t % PW;
-    t /= PW;
+    // a strip's lanes are padded to whole waves, so every wave walks one way
+    const int lps = (PW * C4 + 63) & ~63, li = idx % lps;
+    if (li >= PW * C4) return;
+    const int q = li % C4, pw = li / C4;
+    const int t = idx / lps;
     const int st = t % nstrip;
     const int n = t / nstrip;
     const int ph0 = st * DWR_RP, ph1 = ph0 + DWR_RP < PH ? ph0 + DWR_RP : PH;
@@ -639,6 +640,57 @@ __global__ __launch_bounds__(256) void k_dwconv3_pool_rs(
     const f4 lo = {-1e30f, -1e30f, -1e30f, -1e30f};
     // depthwise rows yA .. yB feed pool rows ph0 .. ph1 - 1
     const int yA = 2 * ph0 - PP, yB = 2 * (ph1 - 1) - PP + 2;
+    if (st & 1) {
+        // Odd strips walk up, so each halo shared with a neighbour is read by
+        // both strips at the same time (both at their start, or both at their
+        // end) and the second read hits L2.  Row y folds its input rows in kh
+        // order (r0, r1, then r2 = the row below, kept from the previous step);
+        // its activated values go to a per-lane ring of the last three rows in
+        // LDS, and pool row ph is formed, in kh order, once its top row 2 ph - PP
+        // arrives.  Same arithmetic in the same order as the downward walk.
+        __shared__ f4 ring[9][256];
+        const int lt = (int)threadIdx.x;
+        f4 r2[7];
+        bool ok2 = ldrow(2 * yB - pad + 2, r2);
+        int ph = ph1 - 1;
+        for (int y = yB; y >= yA; --y) {
+            f4 r1[7], r0[7];
+            const bool ok1 = ldrow(2 * y - pad + 1, r1);
+            const bool ok0 = ldrow(2 * y - pad, r0);
+            f4 d[3] = {b4, b4, b4};
+            fold(d, r0, ok0, 0);
+            fold(d, r1, ok1, 1);
+            fold(d, r2, ok2, 2);
+            const int slot = (y - yA) % 3;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                d[j].x = act_apply(d[j].x, act); d[j].y = act_apply(d[j].y, act);
+                d[j].z = act_apply(d[j].z, act); d[j].w = act_apply(d[j].w, act);
+                ring[slot * 3 + j][lt] = d[j];
+            }
+            if (y == 2 * ph - PP) {
+                f4 m = lo;
+#pragma unroll
+                for (int kh = 0; kh < 3; ++kh) {
+                    const int yy = y + kh, sl = (yy - yA) % 3;
+                    const f4 dd[3] = {ring[sl * 3][lt], ring[sl * 3 + 1][lt], ring[sl * 3 + 2][lt]};
+                    pmax(m, dd, (unsigned)yy < (unsigned)OH);
+                }
+                if (ph < PH) {
+                    if (post_relu) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) m[e] = pv[e] ? vmax(m[e], 0.f) : (m[e] < 0.f ? 0.f : m[e]);
+                    }
+                    out[(((size_t)n * PH + ph) * PW + pw) * C4 + q] = float4{m.x, m.y, m.z, m.w};
+                }
+                --ph;
+            }
+#pragma unroll
+            for (int l = 0; l < 7; ++l) r2[l] = r0[l];
+            ok2 = ok0;
+        }
+        return;
+    }
     f4 part[3], rowa[7], rowb[7];
     {
         f4 acc0[3] = {b4, b4, b4};
@@ -1174,7 +1226,7 @@ bool dwconv_pool_f32(const float* in, int N, int H, int W, int C, const float* w
     const long long in_bytes = (long long)N * H * W * C * 4;
     if (stride == 2 && in_bytes < (1ll << 31)) {
         const int nstrip = (PH + DWR_RP - 1) / DWR_RP;
-        const long long lanes = (long long)N * nstrip * PW * C4;
+        const long long lanes = (long long)N * nstrip * ((PW * C4 + 63) / 64 * 64);
         const long long wgs = (lanes + 255) / 256;
         if (lanes < (1ll << 30)) {
             ACFUN_LAUNCH("k_dwconv_pool", k_dwconv3_pool_rs, dim3((unsigned)(8 * ((wgs + 7) / 8))), dim3(256),
