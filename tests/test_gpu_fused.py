@@ -48,6 +48,8 @@ CASES = [
     (3, 6, 6, 8, 2, 0, 1, 1, 0),         # tiny: most pool windows clipped
     (1, 57, 45, 48, 2, 1, 1, 1, 0),      # odd sizes
     (2, 12, 12, 6, 2, 1, 1, 1, 0),       # C % 4 != 0: the two-kernel path
+    (2, 37, 26, 24, 2, 1, 1, 0, 1),      # stride 2, pool pad 0: 3 strips, the middle one walks up
+    (1, 40, 18, 12, 2, 0, 0, 0, 0),      # conv pad 0, 9 lanes per strip padded to a wave
 ]
 
 
