@@ -141,6 +141,7 @@ struct AcfunModel {
     int inC = 0, inH = 0, inW = 0;
     int version = 0;
     int int8 = 0;
+    int per_image = 0;   // int8 models: batched calls run image by image (load flag 2)
     std::vector<Layer> layers;
     int outSize = 0;
 };
@@ -258,6 +259,7 @@ AcfunModel* load_impl(const char* path, int flags) {
     AcfunModel* m = new AcfunModel();
     m->inC = inC; m->inH = inH; m->inW = inW; m->version = version;
     m->int8 = (flags & 1) ? 1 : 0;
+    m->per_image = (flags & 2) ? 1 : 0;
     std::vector<char> consumed(num, 0);
     std::vector<int> raw2fused(num, -1);
     bool fail = false;
@@ -711,10 +713,27 @@ void acfun_model_input_dims(AcfunModel* m, int* Cin, int* Hin, int* Win) {
     if (Win) *Win = m->inW;
 }
 
+}  // extern "C"
+
+// A batch through the executor.  An int8 model loaded with flag 2 runs its
+// images one at a time, so every int8 activation scale is the image's own, as
+// the reference's acfun_model_infer computes it (one image per call,
+// src/model.cpp:274-349); otherwise the batch runs at once.
+static int run_batch(AcfunModel* m, int N, const float* in, float* out, hipStream_t s) {
+    if (!(m->int8 && m->per_image) || N == 1) return run_model(m, N, in, out, s);
+    const size_t in1 = (size_t)m->inC * m->inH * m->inW;
+    int per = run_model(m, 1, in, out, s);
+    for (int i = 1; i < N && per > 0; ++i)
+        if (run_model(m, 1, in + i * in1, out + (size_t)i * per, s) != per) return 0;
+    return per;
+}
+
+extern "C" {
+
 int acfun_dev_model_infer_batch(AcfunModel* m, int N, const float* input, float* output,
                                 void* stream) {
     if (!m || N <= 0 || !ensure_device()) return 0;
-    return run_model(m, N, input, output, resolve(stream));
+    return run_batch(m, N, input, output, resolve(stream));
 }
 
 int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* output) {
@@ -749,7 +768,7 @@ int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* out
     }
     Scratch dres((size_t)N * maxper * sizeof(float), s);
     if (!dres.p) return 0;
-    int per = run_model(m, N, din, dres.as<float>(), s);
+    int per = run_batch(m, N, din, dres.as<float>(), s);
     if (per > 0) {
         void* dst = output;
         if (is_device_ptr(output)) {

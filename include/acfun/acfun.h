@@ -250,7 +250,10 @@ int acfun_dev_softmax(const float* input, int rows, int cols, float* output, voi
  * runs it through the acfun_conv2d_int8 rules; other layers stay fp32.  The
  * activation scale of each int8 conv is dynamic and per tensor, i.e. max|x|
  * over the whole batch, exactly as acfun_conv2d_int8 computes it for an N-image
- * input (src/conv_int8.cpp:75-81 of the reference). */
+ * input (src/conv_int8.cpp:75-81 of the reference).  flags & 2 (with flags & 1)
+ * makes the batched calls run an int8 model image by image instead, so each
+ * image gets its own scales and acfun_model_infer's result, as the reference's
+ * one-image executor gives it (src/model.cpp:274-349), at lower throughput. */
 AcfunModel* acfun_model_load_ex(const char* path, int flags);
 
 /* Batched inference: input [N, inH, inW, inC], output [N, outSize].  Returns
@@ -259,7 +262,8 @@ AcfunModel* acfun_model_load_ex(const char* path, int flags);
  * arithmetic per output element does not depend on the batch).  For int8
  * models (acfun_model_load_ex flags & 1) it is not: every int8 conv quantizes
  * its input with one scale for the whole batch, so an image's result depends
- * on the other images of its batch; with N = 1 it is acfun_model_infer's. */
+ * on the other images of its batch; with N = 1, or for a model loaded with
+ * flags & 2, it is acfun_model_infer's for each image. */
 int acfun_model_infer_batch(AcfunModel* m, int N, const float* input, float* output);
 /* The same on device pointers, queued on `stream` (not synchronized).  A model
  * holds per-layer device state (Winograd filter transforms made at first use),

@@ -336,6 +336,43 @@ def test_resnet50_b64_tiles_equal_batch8(gpu, rng, int8, head, tmp_path):
             assert rel_err(b[k], a) < 1e-5, (k, rel_err(b[k], a))
 
 
+def test_int8_model_per_image_flag(gpu, rng, tmp_path):
+    """acfun_model_load_ex flag 2: an int8 model's batched call gives every
+    image its own activation scales -- bit for bit the batch-1 call on that
+    image, which test_resnet50_224_matches_oracle[int8] checks against the
+    oracle -- while flag 1 alone shares them over the batch."""
+    import torch
+    inC, H, W, recs = acfun0.resnet50(np.random.default_rng(5), head=False)
+    path = _write(tmp_path, "r50p.acfun", inC, H, W, recs, 2)
+    n, F = 3, 7 * 7 * 2048
+    x = torch.rand((n, H, W, inC), device="cuda", generator=torch.Generator(device="cuda").manual_seed(17))
+    x[1] *= 4.0                              # one image's wider range moves a shared scale
+    s = torch.cuda.current_stream().cuda_stream
+    yb = torch.full((n, F), float("nan"), device="cuda")
+    y1 = torch.full((n, F), float("nan"), device="cuda")
+    yd = torch.full((n, F), float("nan"), device="cuda")
+    print("ResNet-50 body, int8 per-image flag, batch", n, flush=True)
+    m = _load(gpu, path, 3)
+    try:
+        assert gpu.acfun_dev_model_infer_batch(m, n, x.data_ptr(), yb.data_ptr(), s) == F, capi.last_error()
+        for i in range(n):
+            xi = x[i:i + 1].contiguous()
+            assert gpu.acfun_dev_model_infer_batch(m, 1, xi.data_ptr(), y1[i].data_ptr(), s) == F, capi.last_error()
+        torch.cuda.synchronize()
+    finally:
+        gpu.acfun_model_destroy(m)
+    m = _load(gpu, path, 1)
+    try:
+        assert gpu.acfun_dev_model_infer_batch(m, n, x.data_ptr(), yd.data_ptr(), s) == F, capi.last_error()
+        torch.cuda.synchronize()
+    finally:
+        gpu.acfun_model_destroy(m)
+    a = y1.cpu().numpy()
+    assert not np.isnan(a).any() and np.count_nonzero(a) > a.size // 4
+    assert_bitexact(yb.cpu().numpy(), a, "int8 per-image batch against batch-1 calls")
+    assert not np.array_equal(yd.cpu().numpy(), a)      # the shared scale changes the batch
+
+
 def test_int8_model_uses_the_s8_chain(gpu, rng, tmp_path):
     """An int8 model passes a tensor whose only reader is another int8 conv as
     s8 with its device scale: its producer requantizes it (k_requant_s8) and the
